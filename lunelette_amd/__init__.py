@@ -1,0 +1,223 @@
+"""Python bindings (ctypes) for the gfx950 Lunelette forward path.
+
+The product is the C-ABI shared library lunelette_amd/liblunelette_hip.so
+(include/lunelette_runtime.h, include/lunelette_kernels.h,
+include/lunelette_generation.h). This module only loads it and declares
+prototypes; it never substitutes another implementation. If the library has
+not been built, `lib()` raises.
+"""
+import ctypes
+import os
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIBRARY = os.path.join(_HERE, "liblunelette_hip.so")
+
+VOCAB = 131072
+HIDDEN = 3072
+QUERY = 4096
+KV = 1024
+INNER = 9216
+LAYERS = 26
+QKV_ROWS = QUERY + 2 * KV
+
+PREFILL_MPS = 0
+PREFILL_CUSTOM = 1
+RESIDENT_FP32 = 0
+COMPACT_FP8_ARITHMETIC = 1
+COMPACT_FP8_LOOKUP = 2
+
+PATH_FUSED, PATH_LOOKUP, PATH_UNFUSED, PATH_RESIDENT, PATH_MFMA = range(5)
+
+_lib = None
+
+c_size = ctypes.c_size_t
+c_void = ctypes.c_void_p
+c_float_p = ctypes.POINTER(ctypes.c_float)
+c_int64_p = ctypes.POINTER(ctypes.c_int64)
+
+
+class Options(ctypes.Structure):
+    _fields_ = [("prefill", ctypes.c_int), ("strategy", ctypes.c_int)]
+
+
+class Limits(ctypes.Structure):
+    _fields_ = [("context", c_size), ("block", c_size)]
+
+
+class Memory(ctypes.Structure):
+    _fields_ = [("strategy", ctypes.c_int), ("weight_bytes", ctypes.c_uint64),
+                ("conversion_stage_bytes", ctypes.c_uint64), ("scratch_bytes", ctypes.c_uint64),
+                ("kv_bytes", ctypes.c_uint64), ("total_bytes", ctypes.c_uint64)]
+
+
+class SyntheticConfig(ctypes.Structure):
+    _fields_ = [("seed", ctypes.c_uint64), ("layers", ctypes.c_uint32)]
+
+
+class LayerWeights(ctypes.Structure):
+    _fields_ = [("qkv", c_void), ("o", c_void), ("gate", c_void), ("up", c_void), ("down", c_void),
+                ("f32_qkv", c_void), ("f32_o", c_void), ("f32_gate", c_void), ("f32_up", c_void),
+                ("f32_down", c_void), ("scale", ctypes.c_float * 7),
+                ("input_norm", c_void), ("post_norm", c_void)]
+
+
+class GenerationConfig(ctypes.Structure):
+    _fields_ = [("max_new_tokens", c_size), ("eos_token", ctypes.c_int64)]
+
+
+class GenerationResult(ctypes.Structure):
+    _fields_ = [("tokens", ctypes.c_int64 * 256), ("count", c_size), ("stop", ctypes.c_int)]
+
+
+LOGITS_FN = ctypes.CFUNCTYPE(ctypes.c_int, c_void, c_int64_p, c_size, c_float_p,
+                             ctypes.c_char_p, c_size)
+
+
+def _proto(lib, name, restype, *argtypes):
+    fn = getattr(lib, name)
+    fn.restype = restype
+    fn.argtypes = list(argtypes)
+
+
+def lib():
+    """Load the built library (raises if it is missing)."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIBRARY):
+        raise RuntimeError("liblunelette_hip.so is not built; run __graft_entry__.build()")
+    l = ctypes.CDLL(LIBRARY)
+    i, v, f = ctypes.c_int, None, ctypes.c_float
+    _proto(l, "lh_last_error", ctypes.c_char_p)
+    _proto(l, "lh_device_count", i)
+    _proto(l, "lh_device_alloc", c_void, c_size)
+    _proto(l, "lh_device_free", v, c_void)
+    _proto(l, "lh_host_alloc_pinned", c_void, c_size)
+    _proto(l, "lh_host_free_pinned", v, c_void)
+    _proto(l, "lh_memcpy_htod", i, c_void, c_void, c_size)
+    _proto(l, "lh_memcpy_dtoh", i, c_void, c_void, c_size)
+    _proto(l, "lh_memcpy_dtod", i, c_void, c_void, c_size)
+    _proto(l, "lh_memset_device", i, c_void, i, c_size)
+    _proto(l, "lh_device_synchronize", i)
+    _proto(l, "lh_stream_create", c_void)
+    _proto(l, "lh_stream_synchronize", i, c_void)
+    _proto(l, "lh_stream_destroy", v, c_void)
+    _proto(l, "lh_event_create", c_void)
+    _proto(l, "lh_event_record", i, c_void, c_void)
+    _proto(l, "lh_event_elapsed_ms", i, c_void, c_void, c_float_p)
+    _proto(l, "lh_event_destroy", v, c_void)
+    _proto(l, "lh_fp8_matvec", i, c_void, f, c_void, c_void, c_size, c_size, c_size, i, c_void)
+    _proto(l, "lh_f32_matvec", i, c_void, c_void, c_void, c_size, c_size, c_size, c_void)
+    _proto(l, "lh_bf16_matvec", i, c_void, c_void, c_void, c_size, c_size, c_size, c_void)
+    _proto(l, "lh_rmsnorm", i, c_void, c_void, c_void, c_size, c_size, c_void)
+    _proto(l, "lh_element", i, i, c_void, c_void, c_void, c_size, c_void)
+    _proto(l, "lh_rope", i, c_void, c_void, c_void, c_void, c_void, c_size, c_size, c_void)
+    _proto(l, "lh_fp8_decode", i, c_void, c_void, c_size, c_void)
+    _proto(l, "lh_expf", i, c_void, c_void, c_size, c_void)
+    _proto(l, "lh_workspace_create", c_void, c_size, c_size)
+    _proto(l, "lh_workspace_destroy", v, c_void)
+    _proto(l, "lh_workspace_set_tokens", i, c_void, c_int64_p, c_size, c_size, c_void)
+    _proto(l, "lh_layer_forward", i, ctypes.POINTER(LayerWeights), c_void, c_void, c_void,
+           c_void, i, c_void)
+    _proto(l, "lh_head_forward", i, c_void, c_void, c_void, c_void, c_void)
+    _proto(l, "lh_attention", i, c_void, c_void, c_void, c_void, c_void, c_void)
+    _proto(l, "lh_embed_forward", i, c_void, c_void, c_void, c_void)
+    _proto(l, "lh_yarn", i, ctypes.c_uint32, c_float_p, c_float_p)
+    _proto(l, "lh_query_factor", f, ctypes.c_uint32)
+    _proto(l, "lh_synth_fp8", v, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint64, c_void, c_size)
+    _proto(l, "lh_synth_normal_f32", v, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint64, f, f,
+           c_void, c_size)
+    _proto(l, "lh_synth_normal_bf16", v, ctypes.c_uint64, ctypes.c_uint32, ctypes.c_uint64, f, f,
+           c_void, c_size)
+    _proto(l, "lh_synth_scale", f, ctypes.c_uint64, ctypes.c_uint32)
+    _proto(l, "lh_synth_tokens", v, ctypes.c_uint64, ctypes.c_uint32, c_int64_p, c_size)
+    err = ctypes.c_char_p
+    _proto(l, "lunelette_metal_create", c_void, ctypes.c_char_p, err, c_size)
+    _proto(l, "lunelette_metal_create_with_options", c_void, ctypes.c_char_p,
+           ctypes.POINTER(Options), err, c_size)
+    _proto(l, "lunelette_metal_create_configured", c_void, ctypes.c_char_p,
+           ctypes.POINTER(Options), ctypes.POINTER(Limits), err, c_size)
+    _proto(l, "lunelette_metal_create_synthetic", c_void, ctypes.POINTER(SyntheticConfig),
+           ctypes.POINTER(Options), ctypes.POINTER(Limits), err, c_size)
+    _proto(l, "lunelette_metal_get_limits", i, c_void, ctypes.POINTER(Limits))
+    _proto(l, "lunelette_metal_get_memory", i, c_void, ctypes.POINTER(Memory))
+    _proto(l, "lunelette_metal_destroy", v, c_void)
+    _proto(l, "lunelette_metal_reset", i, c_void, err, c_size)
+    logits_out = ctypes.POINTER(c_float_p)
+    _proto(l, "lunelette_metal_prefill", i, c_void, c_int64_p, c_size, logits_out, err, c_size)
+    _proto(l, "lunelette_metal_decode", i, c_void, ctypes.c_int64, logits_out, err, c_size)
+    _proto(l, "lunelette_metal_append", i, c_void, c_int64_p, c_size, logits_out, err, c_size)
+    _proto(l, "lunelette_metal_checkpoint_create", i, c_void, ctypes.POINTER(c_void), err, c_size)
+    _proto(l, "lunelette_metal_checkpoint_restore", i, c_void, c_void, logits_out, err, c_size)
+    _proto(l, "lunelette_metal_checkpoint_destroy", v, c_void)
+    _proto(l, "lunelette_metal_last_device_ms", i, c_void, c_float_p)
+    _proto(l, "lunelette_metal_read_kv", i, c_void, c_size, i, c_size, c_size, c_float_p)
+    _proto(l, "lunelette_metal_test_inject", i, c_void, i)
+    _proto(l, "lunelette_metal_test_set_logit", i, c_void, c_size, f)
+    _proto(l, "lunelette_select_greedy", i, c_float_p, c_int64_p, err, c_size)
+    _proto(l, "lunelette_generate_with_logits", i, LOGITS_FN, c_void, c_int64_p, c_size,
+           ctypes.POINTER(GenerationConfig), ctypes.POINTER(GenerationResult), err, c_size)
+    _proto(l, "lunelette_generate_with_logits_capacity", i, LOGITS_FN, c_void, c_int64_p, c_size,
+           c_size, ctypes.POINTER(GenerationConfig), ctypes.POINTER(GenerationResult), err,
+           c_size)
+    _lib = l
+    return l
+
+
+def last_error():
+    return lib().lh_last_error().decode()
+
+
+def require_gpu():
+    """Raise unless a HIP device is visible (the product has no CPU path)."""
+    if lib().lh_device_count() < 1:
+        raise RuntimeError("no HIP device visible: the gfx950 library needs an MI355X")
+
+
+class DeviceBuffer:
+    """Owned device allocation with numpy upload/download."""
+
+    def __init__(self, nbytes):
+        self.nbytes = int(nbytes)
+        self.ptr = lib().lh_device_alloc(self.nbytes)
+        if not self.ptr:
+            raise MemoryError(last_error())
+
+    @classmethod
+    def from_array(cls, array):
+        array = np.ascontiguousarray(array)
+        buf = cls(array.nbytes)
+        buf.upload(array)
+        return buf
+
+    def upload(self, array):
+        array = np.ascontiguousarray(array)
+        assert array.nbytes <= self.nbytes
+        if lib().lh_memcpy_htod(self.ptr, array.ctypes.data, array.nbytes):
+            raise RuntimeError(last_error())
+
+    def download(self, dtype, count=None):
+        dtype = np.dtype(dtype)
+        count = self.nbytes // dtype.itemsize if count is None else count
+        out = np.empty(count, dtype=dtype)
+        if lib().lh_memcpy_dtoh(out.ctypes.data, self.ptr, out.nbytes):
+            raise RuntimeError(last_error())
+        return out
+
+    def free(self):
+        if self.ptr:
+            lib().lh_device_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def check(status, what="call"):
+    if status != 0:
+        raise RuntimeError("%s failed: %s" % (what, last_error()))

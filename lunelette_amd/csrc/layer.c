@@ -1,0 +1,265 @@
+/* One decoder layer on device buffers, shared by the runtime and the
+ * kernel-level ABI (operator order of src/metal_encode.m:124-187), plus the
+ * per-call step parameters (positions, host YaRN, query factors, ids). */
+#include "lunelette_kernels.h"
+#include "lh_internal.h"
+#include "lh_layer.h"
+
+#include <stdlib.h>
+#include <string.h>
+
+static int check(hipError_t status, const char *what)
+{
+    if (status != hipSuccess) {
+        lh_set_error("%s: %s", what, hipGetErrorString(status));
+        return -1;
+    }
+    return 0;
+}
+
+static int alloc_device(void **out, size_t bytes, uint64_t *total)
+{
+    *out = NULL;
+    if (check(hipMalloc(out, bytes ? bytes : 16), "workspace allocation")) {
+        return -1;
+    }
+    *total += bytes;
+    return 0;
+}
+
+lh_workspace *lh_workspace_create(size_t capacity, size_t block)
+{
+    if (!capacity || !block || block > LH_MAX_BLOCK || capacity % LH_ATTN_BLOCK ||
+        capacity > 262144 || block > capacity) {
+        lh_set_error("workspace: capacity must be a multiple of 64 up to 262144 and block 1..256");
+        return NULL;
+    }
+    lh_workspace *ws = calloc(1, sizeof *ws);
+    if (!ws) {
+        lh_set_error("workspace: host allocation failed");
+        return NULL;
+    }
+    ws->capacity = capacity;
+    ws->block = block;
+    const size_t nbc = capacity / LH_ATTN_BLOCK;
+    const size_t B = block;
+    if (check(hipHostMalloc((void **)&ws->h_params, sizeof(lh_step_params), hipHostMallocDefault),
+            "workspace pinned parameters") ||
+        alloc_device((void **)&ws->d_params, sizeof(lh_step_params), &ws->bytes) ||
+        alloc_device((void **)&ws->d_q, B * LH_QUERY * sizeof(float), &ws->bytes) ||
+        alloc_device((void **)&ws->d_attn, B * LH_QUERY * sizeof(float), &ws->bytes) ||
+        alloc_device((void **)&ws->d_gated, B * LH_INNER * sizeof(float), &ws->bytes) ||
+        alloc_device((void **)&ws->d_up, B * LH_INNER * sizeof(float), &ws->bytes) ||
+        alloc_device((void **)&ws->d_xn, B * LH_HIDDEN * sizeof(float), &ws->bytes) ||
+        alloc_device((void **)&ws->d_qraw, B * LH_QUERY * sizeof(float), &ws->bytes) ||
+        alloc_device((void **)&ws->d_kraw, B * LH_KV * sizeof(float), &ws->bytes) ||
+        alloc_device((void **)&ws->d_vraw, B * LH_KV * sizeof(float), &ws->bytes) ||
+        alloc_device((void **)&ws->d_S, B * LH_HEADS * capacity * sizeof(float), &ws->bytes) ||
+        alloc_device((void **)&ws->d_BM, B * LH_HEADS * nbc * sizeof(float), &ws->bytes) ||
+        alloc_device((void **)&ws->d_PT, B * LH_HEADS * nbc * sizeof(float), &ws->bytes) ||
+        alloc_device((void **)&ws->d_PA, B * LH_HEADS * nbc * LH_HEAD_DIM * sizeof(float),
+            &ws->bytes)) {
+        lh_workspace_destroy(ws);
+        return NULL;
+    }
+    memset(ws->h_params, 0, sizeof(lh_step_params));
+    return ws;
+}
+
+void lh_workspace_destroy(lh_workspace *ws)
+{
+    if (!ws) {
+        return;
+    }
+    void *device[] = {ws->d_params, ws->d_q, ws->d_attn, ws->d_gated, ws->d_up, ws->d_xn,
+        ws->d_qraw, ws->d_kraw, ws->d_vraw, ws->d_S, ws->d_BM, ws->d_PT, ws->d_PA};
+    for (size_t i = 0; i < sizeof device / sizeof device[0]; i++) {
+        if (device[i]) {
+            (void)hipFree(device[i]);
+        }
+    }
+    if (ws->h_params) {
+        (void)hipHostFree(ws->h_params);
+    }
+    free(ws);
+}
+
+int lh_workspace_set_tokens(lh_workspace *ws, const int64_t *ids, size_t length, size_t count,
+    void *stream)
+{
+    if (!ws || !ids || !count || count > ws->block || length > ws->capacity ||
+        count > ws->capacity - length) {
+        lh_set_error("set_tokens: require 1..block ids within capacity");
+        return -1;
+    }
+    hipStream_t s = (hipStream_t)stream;
+    /* The pinned record may still feed the previous upload. */
+    if (check(hipStreamSynchronize(s), "set_tokens synchronize")) {
+        return -1;
+    }
+    lh_step_params *p = ws->h_params;
+    p->length = (uint32_t)length;
+    p->count = (uint32_t)count;
+    for (size_t t = 0; t < count; t++) {
+        if (ids[t] < 0 || ids[t] >= LH_VOCAB) {
+            lh_set_error("set_tokens: invalid token id at %zu", t);
+            return -1;
+        }
+        const uint32_t position = (uint32_t)(length + t);
+        lh_token_params *tp = &p->tokens[t];
+        tp->id = (int32_t)ids[t];
+        tp->position = position;
+        tp->qfactor = lh_query_factor(position);
+        if (lh_yarn(position, tp->cosine, tp->sine)) {
+            lh_set_error("set_tokens: position out of range");
+            return -1;
+        }
+    }
+    const size_t bytes = offsetof(lh_step_params, tokens) + count * sizeof(lh_token_params);
+    if (check(hipMemcpyAsync(ws->d_params, p, bytes, hipMemcpyHostToDevice, s),
+            "set_tokens upload")) {
+        return -1;
+    }
+    ws->length = length;
+    ws->count = count;
+    return 0;
+}
+
+static int launched(int status, const char *what)
+{
+    if (status) {
+        hipError_t e = hipGetLastError();
+        lh_set_error("%s launch failed: %s", what, hipGetErrorString(e));
+        return -1;
+    }
+    return 0;
+}
+
+/* Separate-operator path (also the resident FP32 strategy): every operator is
+ * its own kernel, every row dot follows the same canonical schedule as the
+ * fused kernels, so results are bitwise identical. */
+static int layer_unfused(const lh_layer_weights *w, float *x, float *keys, float *values,
+    lh_workspace *ws, int resident, hipStream_t s)
+{
+    const uint32_t n = (uint32_t)ws->count, C = (uint32_t)ws->capacity;
+    const int kind = resident ? 2 : 0;
+    const void *wq = resident ? (const void *)w->f32_qkv : (const void *)w->qkv;
+    const size_t esize = resident ? 4 : 1;
+    const char *base = (const char *)wq;
+    const void *wk = base + (size_t)LH_QUERY * LH_HIDDEN * esize;
+    const void *wv = base + (size_t)(LH_QUERY + LH_KV) * LH_HIDDEN * esize;
+    const void *wo = resident ? (const void *)w->f32_o : (const void *)w->o;
+    const void *wg = resident ? (const void *)w->f32_gate : (const void *)w->gate;
+    const void *wu = resident ? (const void *)w->f32_up : (const void *)w->up;
+    const void *wd = resident ? (const void *)w->f32_down : (const void *)w->down;
+    const lh_step_params *params = ws->d_params;
+    if (launched(lh_launch_rmsnorm(w->input_norm, x, ws->d_xn, LH_HIDDEN, n, s), "input norm") ||
+        launched(lh_launch_matvec(kind, 0, wq, w->scale[0], ws->d_xn, ws->d_qraw, NULL,
+            LH_QUERY, LH_HIDDEN, n, s), "q") ||
+        launched(lh_launch_matvec(kind, 0, wk, w->scale[1], ws->d_xn, ws->d_kraw, NULL,
+            LH_KV, LH_HIDDEN, n, s), "k") ||
+        launched(lh_launch_matvec(kind, 0, wv, w->scale[2], ws->d_xn, ws->d_vraw, NULL,
+            LH_KV, LH_HIDDEN, n, s), "v") ||
+        launched(lh_launch_rope_append(ws->d_qraw, ws->d_kraw, ws->d_vraw, params, n, ws->d_q,
+            keys, values, C, s), "rope/append") ||
+        launched(lh_launch_attention(ws->d_q, keys, values, params, n,
+            (uint32_t)(ws->length + n), C, ws->d_S, ws->d_BM, ws->d_PT, ws->d_PA, ws->d_attn, s),
+            "attention") ||
+        launched(lh_launch_matvec(kind, 0, wo, w->scale[3], ws->d_attn, x, x, LH_HIDDEN,
+            LH_QUERY, n, s), "o") ||
+        launched(lh_launch_rmsnorm(w->post_norm, x, ws->d_xn, LH_HIDDEN, n, s), "post norm") ||
+        launched(lh_launch_matvec(kind, 0, wg, w->scale[4], ws->d_xn, ws->d_gated, NULL,
+            LH_INNER, LH_HIDDEN, n, s), "gate") ||
+        launched(lh_launch_matvec(kind, 0, wu, w->scale[5], ws->d_xn, ws->d_up, NULL,
+            LH_INNER, LH_HIDDEN, n, s), "up") ||
+        launched(lh_launch_silu_mul(ws->d_gated, ws->d_up, ws->d_gated, (size_t)n * LH_INNER, s),
+            "silu") ||
+        launched(lh_launch_matvec(kind, 0, wd, w->scale[6], ws->d_gated, x, x, LH_HIDDEN,
+            LH_INNER, n, s), "down")) {
+        return -1;
+    }
+    return 0;
+}
+
+static int layer_fused(const lh_layer_weights *w, float *x, float *keys, float *values,
+    lh_workspace *ws, int lookup, hipStream_t s)
+{
+    const uint32_t n = (uint32_t)ws->count, C = (uint32_t)ws->capacity;
+    const lh_step_params *params = ws->d_params;
+    if (launched(lh_launch_qkv_rope(lookup, w->qkv, w->scale[0], w->scale[1], w->scale[2],
+            w->input_norm, x, params, n, ws->d_q, keys, values, C, s), "qkv") ||
+        launched(lh_launch_attention(ws->d_q, keys, values, params, n,
+            (uint32_t)(ws->length + n), C, ws->d_S, ws->d_BM, ws->d_PT, ws->d_PA, ws->d_attn, s),
+            "attention") ||
+        launched(lh_launch_matvec(0, lookup, w->o, w->scale[3], ws->d_attn, x, x, LH_HIDDEN,
+            LH_QUERY, n, s), "o") ||
+        launched(lh_launch_gateup_silu(lookup, w->gate, w->up, w->scale[4], w->scale[5],
+            w->post_norm, x, n, ws->d_gated, s), "gate/up") ||
+        launched(lh_launch_matvec(0, lookup, w->down, w->scale[6], ws->d_gated, x, x, LH_HIDDEN,
+            LH_INNER, n, s), "down")) {
+        return -1;
+    }
+    return 0;
+}
+
+int lh_layer_forward(const lh_layer_weights *w, float *d_x, float *d_keys, float *d_values,
+    lh_workspace *ws, int path, void *stream)
+{
+    if (!w || !d_x || !d_keys || !d_values || !ws || !ws->count) {
+        lh_set_error("layer_forward: missing argument or tokens not set");
+        return -1;
+    }
+    hipStream_t s = (hipStream_t)stream;
+    switch (path) {
+    case LH_PATH_FUSED:
+        return layer_fused(w, d_x, d_keys, d_values, ws, 0, s);
+    case LH_PATH_LOOKUP:
+        return layer_fused(w, d_x, d_keys, d_values, ws, 1, s);
+    case LH_PATH_UNFUSED:
+        return layer_unfused(w, d_x, d_keys, d_values, ws, 0, s);
+    case LH_PATH_RESIDENT:
+        if (!w->f32_qkv || !w->f32_o || !w->f32_gate || !w->f32_up || !w->f32_down) {
+            lh_set_error("layer_forward: resident path needs FP32 weights");
+            return -1;
+        }
+        return layer_unfused(w, d_x, d_keys, d_values, ws, 1, s);
+    case LH_PATH_MFMA:
+        return lh_layer_forward_mfma(w, d_x, d_keys, d_values, ws, s);
+    default:
+        lh_set_error("layer_forward: unknown path %d", path);
+        return -1;
+    }
+}
+
+int lh_attention(const float *d_q, const float *d_keys, const float *d_values, lh_workspace *ws,
+    float *d_out, void *stream)
+{
+    if (!d_q || !d_keys || !d_values || !ws || !ws->count || !d_out) {
+        lh_set_error("attention: missing argument or tokens not set");
+        return -1;
+    }
+    return launched(lh_launch_attention(d_q, d_keys, d_values, ws->d_params, (uint32_t)ws->count,
+        (uint32_t)(ws->length + ws->count), (uint32_t)ws->capacity, ws->d_S, ws->d_BM, ws->d_PT,
+        ws->d_PA, d_out, (hipStream_t)stream), "attention");
+}
+
+int lh_head_forward(const uint16_t *d_embedding, const float *d_gamma, const float *d_xrow,
+    float *d_logits, void *stream)
+{
+    if (!d_embedding || !d_gamma || !d_xrow || !d_logits) {
+        lh_set_error("head_forward: missing argument");
+        return -1;
+    }
+    return launched(lh_launch_head(d_embedding, d_gamma, d_xrow, d_logits, (hipStream_t)stream),
+        "head");
+}
+
+int lh_embed_forward(const uint16_t *d_embedding, float *d_x, lh_workspace *ws, void *stream)
+{
+    if (!d_embedding || !d_x || !ws || !ws->count) {
+        lh_set_error("embed_forward: missing argument or tokens not set");
+        return -1;
+    }
+    return launched(lh_launch_embed(d_embedding, ws->d_params, (uint32_t)ws->count, d_x,
+        (hipStream_t)stream), "embed");
+}

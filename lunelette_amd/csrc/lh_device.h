@@ -1,0 +1,93 @@
+// Device helpers shared by the gfx950 kernels: weight element decode, the
+// fixed 64-lane reduction tree, and the Cody-Waite exp that the CPU oracle
+// restates bit for bit. Every reduction order used here is part of the
+// canonical schedule described in lh_schedule.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "lh_schedule.h"
+
+namespace lh {
+
+// E4M3FN -> FP32. gfx950's v_cvt_pk_f32_fp8 decodes the OCP E4M3FN encoding
+// (bias 7, subnormals f*2^-9, 0x7f/0xff NaN), matching src/safetensors.c:505-519
+// for every finite code; the all-256-code check runs in the GPU tests.
+__device__ __forceinline__ void fp8x4_to_f32(uint32_t packed, float out[4])
+{
+    auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(packed, false);
+    auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(packed, true);
+    out[0] = lo[0];
+    out[1] = lo[1];
+    out[2] = hi[0];
+    out[3] = hi[1];
+}
+
+// Table decode (the COMPACT_FP8_LOOKUP strategy): unscaled E4M3FN values,
+// built once per launch into LDS from the arithmetic decode, so both
+// strategies are bitwise identical by construction.
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16)
+{
+    return __uint_as_float(bits16 << 16);
+}
+
+// Pairwise halving tree over the 64 lanes of a wave: after the step with
+// distance s, lane i < s holds v_i + v_{i+s}. Lane 0 returns the total.
+__device__ __forceinline__ float wave_tree64(float v)
+{
+    v = v + __shfl_down(v, 32, 64);
+    v = v + __shfl_down(v, 16, 64);
+    v = v + __shfl_down(v, 8, 64);
+    v = v + __shfl_down(v, 4, 64);
+    v = v + __shfl_down(v, 2, 64);
+    v = v + __shfl_down(v, 1, 64);
+    return v;
+}
+
+__device__ __forceinline__ float wave_max64(float v)
+{
+    for (int s = 32; s >= 1; s >>= 1) {
+        v = fmaxf(v, __shfl_xor(v, s, 64));
+    }
+    return v;
+}
+
+// exp(x): Cody & Waite additive range reduction (Cody, Waite, "Software
+// Manual for the Elementary Functions", 1980) with ln2 split so k*ln2_hi is
+// exact, then the degree-7 Taylor polynomial of e^r by Horner's rule with
+// fused multiply-adds, then ldexp. Below the normal range flushes to +0,
+// above ln(FLT_MAX) gives +inf.
+__device__ __forceinline__ float expf_cw(float x)
+{
+    if (x != x) {
+        return x;
+    }
+    if (x > 88.72283935546875f) {
+        return __builtin_inff();
+    }
+    if (x < -87.33654022216796875f) {
+        return 0.0f;
+    }
+    float k = __builtin_rintf(x * 1.44269502162933349609375f);
+    float r = __builtin_fmaf(k, -0.693145751953125f, x);
+    r = __builtin_fmaf(k, -1.428606765330187045037746429443359375e-06f, r);
+    float p = 1.98412698412698412698e-04f;
+    p = __builtin_fmaf(p, r, 1.38888888888888888889e-03f);
+    p = __builtin_fmaf(p, r, 8.33333333333333333333e-03f);
+    p = __builtin_fmaf(p, r, 4.16666666666666666667e-02f);
+    p = __builtin_fmaf(p, r, 1.66666666666666666667e-01f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    return __builtin_ldexpf(p, (int)k);
+}
+
+// SiLU v/(1+exp(-v)) (src/metal_kernels.metal:55-56) with the division
+// correctly rounded (hipcc's default fp32 division).
+__device__ __forceinline__ float silu(float v)
+{
+    return v / (1.0f + expf_cw(-v));
+}
+
+}  // namespace lh

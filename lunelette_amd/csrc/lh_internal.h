@@ -1,0 +1,52 @@
+/* Internal launchers between the C runtime and the gfx950 kernels. Device
+ * pointers only; every launcher returns 0 or -1 (launch error). */
+#ifndef LH_INTERNAL_H
+#define LH_INTERNAL_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "lh_schedule.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* kind: 0 FP8 codes (scaled), 1 BF16, 2 FP32. residual may be NULL. */
+int lh_launch_matvec(int kind, int lookup, const void *W, float scale, const float *x, float *y,
+    const float *residual, uint32_t rows, uint32_t cols, uint32_t tokens, hipStream_t s);
+int lh_launch_qkv_rope(int lookup, const uint8_t *Wqkv, float sq, float sk, float sv,
+    const float *gamma, const float *x, const lh_step_params *params, uint32_t count,
+    float *q, float *kcache_layer, float *vcache_layer, uint32_t capacity, hipStream_t s);
+int lh_launch_gateup_silu(int lookup, const uint8_t *Wgate, const uint8_t *Wup, float sg,
+    float su, const float *gamma, const float *x, uint32_t count, float *gated, hipStream_t s);
+int lh_launch_head(const uint16_t *E, const float *gamma, const float *xrow, float *logits,
+    hipStream_t s);
+int lh_launch_rmsnorm(const float *gamma, const float *x, float *out, uint32_t width,
+    uint32_t tokens, hipStream_t s);
+int lh_launch_attention(const float *q, const float *kcache_layer, const float *vcache_layer,
+    const lh_step_params *params, uint32_t count, uint32_t max_positions, uint32_t capacity,
+    float *S, float *BM, float *PT, float *PA, float *out, hipStream_t s);
+int lh_launch_embed(const uint16_t *E, const lh_step_params *params, uint32_t count, float *x,
+    hipStream_t s);
+int lh_launch_element(int mode, const float *a, const float *b, float *out, size_t n,
+    hipStream_t s);
+int lh_launch_silu_mul(const float *gate, const float *up, float *out, size_t n, hipStream_t s);
+int lh_launch_rope(const float *x, const float *cosine, const float *sine, const float *qfactor,
+    float *out, uint32_t width, uint32_t tokens, hipStream_t s);
+/* q [count][4096], k/v [count][1024] raw projections. */
+int lh_launch_rope_append(const float *q_raw, const float *k_raw, const float *v_raw,
+    const lh_step_params *params, uint32_t count, float *q, float *kcache_layer,
+    float *vcache_layer, uint32_t capacity, hipStream_t s);
+int lh_launch_fp8_decode(const uint8_t *codes, float *out, size_t n, hipStream_t s);
+int lh_launch_expf(const float *x, float *out, size_t n, hipStream_t s);
+
+/* Thread-local diagnostic shared by the C ABI layers. */
+void lh_set_error(const char *format, ...);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif

@@ -1,0 +1,42 @@
+/* Workspace layout shared by layer.c, the MFMA path and the runtime. */
+#ifndef LH_LAYER_H
+#define LH_LAYER_H
+
+#include <hip/hip_runtime_api.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "lunelette_kernels.h"
+#include "lh_schedule.h"
+
+struct lh_workspace {
+    size_t capacity, block;
+    size_t length, count;          /* set by lh_workspace_set_tokens */
+    uint64_t bytes;                /* device bytes owned */
+    lh_step_params *h_params;      /* pinned */
+    lh_step_params *d_params;
+    float *d_q, *d_attn;           /* [B][4096] */
+    float *d_gated, *d_up;         /* [B][9216] */
+    float *d_xn;                   /* [B][3072] */
+    float *d_qraw, *d_kraw, *d_vraw;
+    float *d_S;                    /* [B][32][C] scores */
+    float *d_BM, *d_PT;            /* [B][32][C/64] */
+    float *d_PA;                   /* [B][32][C/64][128] */
+    /* MFMA path: BF16 hi/mid/lo splits of the GEMM inputs, [3][B][K]. */
+    uint16_t *d_split;
+    float *d_gemm;                 /* [B][18432] GEMM outputs */
+};
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+/* Multi-token layer with MFMA GEMM projections (mfma.hip). */
+int lh_layer_forward_mfma(const lh_layer_weights *w, float *d_x, float *d_keys,
+    float *d_values, lh_workspace *ws, hipStream_t s);
+/* Allocates the MFMA path's extra workspace buffers (idempotent). */
+int lh_mfma_prepare(lh_workspace *ws);
+#ifdef __cplusplus
+}
+#endif
+
+#endif

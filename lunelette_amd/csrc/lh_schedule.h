@@ -1,0 +1,72 @@
+/* Shapes, device layouts and the canonical reduction schedule shared by the
+ * host runtime (C) and the gfx950 kernels (HIP).
+ *
+ * Canonical schedule (the CPU oracle's ORC_MIRROR restates it):
+ *   row dot  : columns in chunks of 1024; lane l of a 64-lane wave owns columns
+ *              [16l, 16l+16) of each chunk and runs acc = fma(w, x, acc) from 0
+ *              over them in column order; the chunk's 64 lane values reduce by
+ *              the pairwise halving tree (32,16,8,4,2,1); chunk totals are
+ *              added in chunk order starting from chunk 0. FP8 elements are
+ *              w = fl(dec(code) * scale) (src/metal_kernels.metal:136-144).
+ *   RMSNorm  : ss by the row-dot schedule with w = x; r = 1/sqrt(ss/n + 1e-5);
+ *              out = gamma * (x * r).
+ *   attention: per (token, head) s_p = fl(chain_d fma(q_d, k_pd) * 1/sqrt(128));
+ *              M = max s_p; e_p = expf_cw(s_p - M); per 64-position block the
+ *              e_p reduce by the 64-lane tree and A_b[d] chains fma(e_p, v_pd)
+ *              over the block's valid positions; blocks chain into 256-position
+ *              tiles, tiles chain in order; out = A / T.
+ */
+#ifndef LH_SCHEDULE_H
+#define LH_SCHEDULE_H
+
+#include <stdint.h>
+
+#define LH_HIDDEN 3072
+#define LH_QUERY 4096
+#define LH_KV 1024
+#define LH_INNER 9216
+#define LH_LAYERS 26
+#define LH_VOCAB 131072
+#define LH_HEADS 32
+#define LH_KV_HEADS 8
+#define LH_HEAD_DIM 128
+#define LH_QKV_ROWS (LH_QUERY + 2 * LH_KV) /* fused q|k|v rows: 6144 */
+
+#define LH_CHUNK 1024      /* columns per canonical chunk */
+#define LH_LANE_COLS 16    /* columns per lane per chunk */
+#define LH_ATTN_BLOCK 64   /* positions per attention block */
+#define LH_ATTN_TILE 4     /* blocks per tile in the combine */
+#define LH_MAX_BLOCK 256   /* largest executed block (B) */
+
+#define LH_SCORE_SCALE 0.08838834764831845f
+
+/* Per-token step record; the host fills count of them after the header. */
+typedef struct {
+    int32_t id;
+    float qfactor;
+    uint32_t position;
+    uint32_t pad;
+    float cosine[128];
+    float sine[128];
+} lh_token_params;
+
+typedef struct {
+    uint32_t length; /* committed prefix before this call */
+    uint32_t count;  /* tokens in this call */
+    uint32_t pad[2];
+    lh_token_params tokens[LH_MAX_BLOCK];
+} lh_step_params;
+
+/* Device KV layout: [layer][kv_head][capacity][128] FP32, K rotated, V raw. */
+#ifdef __HIPCC__
+#define LH_HOST_DEVICE __host__ __device__
+#else
+#define LH_HOST_DEVICE
+#endif
+static inline LH_HOST_DEVICE uint64_t lh_kv_index(uint64_t capacity, uint32_t layer, uint32_t kv_head,
+    uint64_t position)
+{
+    return (((uint64_t)layer * LH_KV_HEADS + kv_head) * capacity + position) * LH_HEAD_DIM;
+}
+
+#endif

@@ -1,0 +1,339 @@
+/* Oracle kernels: matvec, RMSNorm, RoPE, SiLU*up, causal GQA attention, in the
+ * reference-literal (ORC_REF) and device-mirror (ORC_MIRROR) schedules.
+ * TEST INFRASTRUCTURE ONLY (see oracle.h). */
+#include "oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+static int orc_threads;
+
+void orc_set_threads(int threads)
+{
+    orc_threads = threads > 0 ? threads : 0;
+#ifdef _OPENMP
+    if (threads > 0) {
+        omp_set_num_threads(threads);
+    }
+#endif
+}
+
+int orc_get_threads(void)
+{
+#ifdef _OPENMP
+    return omp_get_max_threads();
+#else
+    return 1;
+#endif
+}
+
+/* Pairwise halving trees. tree32 stands in for Apple simd_sum (whose order is
+ * unpinned); tree64 is the device wave reduction (shuffle-down by 32,16,..,1). */
+static float tree32(float v[32])
+{
+    for (int s = 16; s >= 1; s >>= 1) {
+        for (int i = 0; i < s; i++) {
+            v[i] = v[i] + v[i + s];
+        }
+    }
+    return v[0];
+}
+
+static float tree64(float v[64])
+{
+    for (int s = 32; s >= 1; s >>= 1) {
+        for (int i = 0; i < s; i++) {
+            v[i] = v[i] + v[i + s];
+        }
+    }
+    return v[0];
+}
+
+static void weight_row(int kind, const void *weights, const float lut[256], size_t row,
+    size_t cols, float *out)
+{
+    if (kind == ORC_W_FP8) {
+        const uint8_t *w = (const uint8_t *)weights + row * cols;
+        for (size_t c = 0; c < cols; c++) {
+            out[c] = lut[w[c]];
+        }
+    } else if (kind == ORC_W_BF16) {
+        const uint16_t *w = (const uint16_t *)weights + row * cols;
+        for (size_t c = 0; c < cols; c++) {
+            out[c] = orc_bf16_widen(w[c]);
+        }
+    } else {
+        memcpy(out, (const float *)weights + row * cols, cols * sizeof(float));
+    }
+}
+
+/* Reference-literal row dot, src/metal_kernels.metal:7-27 and :153-177:
+ * lane l Kahan-sums fl(w*x) over c == l (mod 32) in increasing c, then the
+ * 32-lane tree. w is already fl(dec*s) for FP8 (weight(), :136-144). */
+static float dot_ref(const float *w, const float *x, size_t cols)
+{
+    float sum[32] = {0}, correction[32] = {0};
+    size_t full = cols / 32 * 32;
+    for (size_t base = 0; base < full; base += 32) {
+        for (int l = 0; l < 32; l++) {
+            float product = w[base + l] * x[base + l];
+            float value = product - correction[l];
+            float next = sum[l] + value;
+            correction[l] = (next - sum[l]) - value;
+            sum[l] = next;
+        }
+    }
+    for (size_t c = full; c < cols; c++) {
+        int l = (int)(c - full);
+        float product = w[c] * x[c];
+        float value = product - correction[l];
+        float next = sum[l] + value;
+        correction[l] = (next - sum[l]) - value;
+        sum[l] = next;
+    }
+    return tree32(sum);
+}
+
+/* Device-mirror row dot: 1024-column chunks; lane l owns columns
+ * [16l, 16l+16) of each chunk and runs acc = fma(w, x, acc) from 0 over its
+ * valid columns; the 64 lanes reduce by tree64; chunk results are summed in
+ * chunk order starting from chunk 0. */
+static float dot_mirror(const float *w, const float *x, size_t cols)
+{
+    float y = 0.0f;
+    for (size_t chunk = 0; chunk * 1024 < cols; chunk++) {
+        size_t base = chunk * 1024;
+        size_t valid = cols - base < 1024 ? cols - base : 1024;
+        float lanes[64];
+        if (valid == 1024) {
+            float acc[64] = {0};
+            for (int j = 0; j < 16; j++) {
+                for (int l = 0; l < 64; l++) {
+                    acc[l] = fmaf(w[base + 16 * l + j], x[base + 16 * l + j], acc[l]);
+                }
+            }
+            memcpy(lanes, acc, sizeof lanes);
+        } else {
+            for (int l = 0; l < 64; l++) {
+                float acc = 0.0f;
+                for (size_t j = 16 * (size_t)l; j < 16 * (size_t)l + 16 && j < valid; j++) {
+                    acc = fmaf(w[base + j], x[base + j], acc);
+                }
+                lanes[l] = acc;
+            }
+        }
+        float q = tree64(lanes);
+        y = chunk == 0 ? q : y + q;
+    }
+    return y;
+}
+
+void orc_matvec(int schedule, int kind, const void *weights, float scale,
+    const float *x, float *y, size_t rows, size_t cols, size_t tokens)
+{
+    float lut[256];
+    for (int b = 0; b < 256; b++) {
+        lut[b] = orc_fp8_decode((uint8_t)b) * scale;
+    }
+    #pragma omp parallel
+    {
+        float *w = malloc(cols * sizeof(float));
+        #pragma omp for schedule(static)
+        for (size_t r = 0; r < rows; r++) {
+            weight_row(kind, weights, lut, r, cols, w);
+            for (size_t t = 0; t < tokens; t++) {
+                y[t * rows + r] = schedule == ORC_REF ? dot_ref(w, x + t * cols, cols) :
+                    dot_mirror(w, x + t * cols, cols);
+            }
+        }
+        free(w);
+    }
+}
+
+/* RMSNorm, src/metal_kernels.metal:29-44: out = gamma*(x*r),
+ * r = 1/sqrt(ss/width + 1e-5). REF: per-lane v*v sums over c == l (mod 32) then
+ * tree32. MIRROR: the dot_mirror order with fma(x, x, acc). */
+void orc_rmsnorm(int schedule, const float *gamma, const float *x, float *out,
+    size_t width, size_t tokens)
+{
+    #pragma omp parallel for schedule(static)
+    for (size_t t = 0; t < tokens; t++) {
+        const float *row = x + t * width;
+        float ss;
+        if (schedule == ORC_REF) {
+            float lanes[32] = {0};
+            for (size_t c = 0; c < width; c++) {
+                lanes[c % 32] += row[c] * row[c];
+            }
+            ss = tree32(lanes);
+        } else {
+            ss = dot_mirror(row, row, width);
+        }
+        float r = 1.0f / sqrtf(ss / (float)width + 1e-5f);
+        for (size_t c = 0; c < width; c++) {
+            out[t * width + c] = gamma[c] * (row[c] * r);
+        }
+    }
+}
+
+/* Split-half rotation, src/metal_kernels.metal:59-78. */
+void orc_rope(const float *x, const float *cosine, const float *sine,
+    const float *qfactor, float *out, size_t width, size_t tokens)
+{
+    for (size_t t = 0; t < tokens; t++) {
+        for (size_t i = 0; i < width; i++) {
+            size_t index = t * width + i;
+            size_t column = i % 128;
+            float rotated = column < 64 ? -x[index + 64] : x[index - 64];
+            float value = x[index] * cosine[t * 128 + column] + rotated * sine[t * 128 + column];
+            if (qfactor) {
+                value *= qfactor[t];
+            }
+            out[index] = value;
+        }
+    }
+}
+
+void orc_silu_mul(int schedule, const float *gate, const float *up, float *out, size_t n)
+{
+    for (size_t i = 0; i < n; i++) {
+        float s = schedule == ORC_REF ? orc_silu_ref(gate[i]) : orc_silu_mirror(gate[i]);
+        out[i] = s * up[i];
+    }
+}
+
+#define ORC_SCORE_SCALE 0.08838834764831845f
+
+/* Reference-literal attention for one (token, head), src/metal_kernels.metal:
+ * 80-132: lane partials of q*k over d == l (mod 32), tree32, times 1/sqrt(128);
+ * max; e = exp(s - max) with lane partial sums over p == l (mod 32), tree32;
+ * P = e / total; out[d] = sum_p P*V in position order. */
+static void attend_ref(const float *q, const float *keys, const float *values,
+    size_t head_stride, size_t pos_stride, size_t kvh, size_t n, float *scores, float *out)
+{
+    const float *k0 = keys + kvh * head_stride;
+    const float *v0 = values + kvh * head_stride;
+    float maximum = -INFINITY;
+    for (size_t p = 0; p < n; p++) {
+        float lanes[32] = {0};
+        for (int d = 0; d < 128; d++) {
+            lanes[d % 32] += q[d] * k0[p * pos_stride + d];
+        }
+        float s = tree32(lanes) * ORC_SCORE_SCALE;
+        scores[p] = s;
+        maximum = fmaxf(maximum, s);
+    }
+    float lanes[32] = {0};
+    for (size_t p = 0; p < n; p++) {
+        float e = expf(scores[p] - maximum);
+        scores[p] = e;
+        lanes[p % 32] += e;
+    }
+    float total = tree32(lanes);
+    for (size_t p = 0; p < n; p++) {
+        scores[p] = scores[p] / total;
+    }
+    for (int d = 0; d < 128; d++) {
+        float sum = 0;
+        for (size_t p = 0; p < n; p++) {
+            sum += scores[p] * v0[p * pos_stride + d];
+        }
+        out[d] = sum;
+    }
+}
+
+/* Device-mirror attention for one (token, head):
+ *   s_p = fl(chain_d fma(q_d, k_pd) * 1/sqrt(128)); M = max_p s_p;
+ *   e_p = orc_expf(s_p - M);
+ *   per 64-position block b: T_b = tree64(e, zero-padded), A_b[d] = chain over
+ *   the block's valid p of fma(e_p, v_pd, acc);
+ *   per 256-position tile: chain of its non-empty blocks in order;
+ *   over tiles: chain in order; out[d] = A[d] / T. */
+static void attend_mirror(const float *q, const float *keys, const float *values,
+    size_t head_stride, size_t pos_stride, size_t kvh, size_t n, float *scores, float *out)
+{
+    const float *k0 = keys + kvh * head_stride;
+    const float *v0 = values + kvh * head_stride;
+    float maximum = -INFINITY;
+    for (size_t p = 0; p < n; p++) {
+        float acc = 0.0f;
+        for (int d = 0; d < 128; d++) {
+            acc = fmaf(q[d], k0[p * pos_stride + d], acc);
+        }
+        float s = acc * ORC_SCORE_SCALE;
+        scores[p] = s;
+        maximum = fmaxf(maximum, s);
+    }
+    for (size_t p = 0; p < n; p++) {
+        scores[p] = orc_expf(scores[p] - maximum);
+    }
+    float total = 0.0f, acc[128];
+    for (size_t tile = 0; tile * 256 < n; tile++) {
+        float tile_total = 0.0f, tile_acc[128];
+        for (size_t block = tile * 4; block < tile * 4 + 4 && block * 64 < n; block++) {
+            float lanes[64];
+            float block_acc[128];
+            for (int d = 0; d < 128; d++) {
+                block_acc[d] = 0.0f;
+            }
+            for (int l = 0; l < 64; l++) {
+                size_t p = block * 64 + (size_t)l;
+                lanes[l] = p < n ? scores[p] : 0.0f;
+                if (p < n) {
+                    for (int d = 0; d < 128; d++) {
+                        block_acc[d] = fmaf(scores[p], v0[p * pos_stride + d], block_acc[d]);
+                    }
+                }
+            }
+            float block_total = tree64(lanes);
+            if (block == tile * 4) {
+                tile_total = block_total;
+                memcpy(tile_acc, block_acc, sizeof tile_acc);
+            } else {
+                tile_total = tile_total + block_total;
+                for (int d = 0; d < 128; d++) {
+                    tile_acc[d] = tile_acc[d] + block_acc[d];
+                }
+            }
+        }
+        if (tile == 0) {
+            total = tile_total;
+            memcpy(acc, tile_acc, sizeof acc);
+        } else {
+            total = total + tile_total;
+            for (int d = 0; d < 128; d++) {
+                acc[d] = acc[d] + tile_acc[d];
+            }
+        }
+    }
+    for (int d = 0; d < 128; d++) {
+        out[d] = acc[d] / total;
+    }
+}
+
+void orc_attention(int schedule, const float *q, const float *keys, const float *values,
+    size_t head_stride, size_t pos_stride, size_t prefix, size_t count, float *out)
+{
+    #pragma omp parallel
+    {
+        float *scores = malloc((prefix + count) * sizeof(float));
+        #pragma omp for schedule(dynamic) collapse(2)
+        for (size_t t = 0; t < count; t++) {
+            for (size_t h = 0; h < ORC_HEADS; h++) {
+                size_t n = prefix + t + 1;
+                const float *qh = q + t * ORC_QUERY + h * ORC_HEAD_DIM;
+                float *oh = out + t * ORC_QUERY + h * ORC_HEAD_DIM;
+                if (schedule == ORC_REF) {
+                    attend_ref(qh, keys, values, head_stride, pos_stride, h / 4, n, scores, oh);
+                } else {
+                    attend_mirror(qh, keys, values, head_stride, pos_stride, h / 4, n, scores, oh);
+                }
+            }
+        }
+        free(scores);
+    }
+}

@@ -1,0 +1,60 @@
+"""Helpers for GPU tests: device copies of one synthetic layer and of the KV
+cache in the device layout [8][capacity][128]."""
+import numpy as np
+
+import lunelette_amd as lh
+from lunelette_amd import synthetic as syn
+
+import oracle_lib
+
+
+def decode_table():
+    o = oracle_lib.load()
+    return np.array([o.orc_fp8_decode(c) for c in range(256)], np.float32)
+
+
+class DeviceLayer:
+    """One layer's weights on device (compact FP8 and resident FP32)."""
+
+    def __init__(self, host, resident=False):
+        self.keep = []
+        qkv = np.concatenate([host["q"], host["k"], host["v"]], axis=0)
+        w = lh.LayerWeights()
+        names = ("qkv", "o", "gate", "up", "down")
+        mats = {"qkv": qkv, "o": host["o"], "gate": host["gate"], "up": host["up"],
+                "down": host["down"]}
+        for name in names:
+            buf = lh.DeviceBuffer.from_array(mats[name])
+            self.keep.append(buf)
+            setattr(w, name, buf.ptr)
+        if resident:
+            dec = decode_table()
+            scales = {"q": host["scale_q"], "k": host["scale_k"], "v": host["scale_v"]}
+            qkv32 = np.concatenate([dec[host[n]] * np.float32(scales[n]) for n in ("q", "k", "v")])
+            mats32 = {"qkv": qkv32}
+            for n in ("o", "gate", "up", "down"):
+                mats32[n] = dec[host[n]] * np.float32(host["scale_" + n])
+            for name in names:
+                buf = lh.DeviceBuffer.from_array(mats32[name].astype(np.float32))
+                self.keep.append(buf)
+                setattr(w, "f32_" + name, buf.ptr)
+        for j, n in enumerate(("q", "k", "v", "o", "gate", "up", "down")):
+            w.scale[j] = host["scale_" + n]
+        for n in ("input_norm", "post_norm"):
+            buf = lh.DeviceBuffer.from_array(syn.bf16_to_f32(host[n]))
+            self.keep.append(buf)
+            setattr(w, n, buf.ptr)
+        self.weights = w
+
+
+def kv_to_device_layout(kpm, capacity):
+    """[n][1024] position-major -> [8][capacity][128] head-major."""
+    n = kpm.shape[0]
+    out = np.zeros((8, capacity, 128), np.float32)
+    out[:, :n] = kpm.reshape(n, 8, 128).transpose(1, 0, 2)
+    return out
+
+
+def kv_from_device_layout(khm, position, count):
+    return np.ascontiguousarray(khm[:, position:position + count].transpose(1, 0, 2)).reshape(
+        count, 1024)

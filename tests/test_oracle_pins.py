@@ -1,0 +1,183 @@
+"""Pins the oracle's scalar pieces against the reference's golden vectors, the
+reference's own C compiled from its sources (oracle/_ref), and closed forms.
+
+- FP8 decode: tests/fp8_golden.h, all 256 codes (tests/test_safetensors.c:164-175);
+  bitwise against st_f8_e4m3_to_f32 (src/safetensors.c:505-519).
+- Scaled FP8: golden x {0.251953125, 1.0078125, 3.140625} exactly
+  (tests/test_safetensors.c:193-204).
+- YaRN: tests/rope_golden.h to 2e-6 (tests/test_metal.m:597-604); bitwise
+  against lunelette_metal_yarn (src/metal_yarn.c) over many positions.
+- Greedy: tests/test_generation.c cases; bitwise against the reference C.
+- exp: <= 2 ulp against libm over a dense sweep; closed-form edges.
+"""
+import ctypes
+import json
+import math
+import os
+
+import numpy as np
+import pytest
+
+import oracle_lib
+
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+
+
+def f32bits(value):
+    return int(np.array([value], dtype=np.float32).view(np.uint32)[0])
+
+
+def test_fp8_decode_matches_golden_all_codes(oracle):
+    bits = json.load(open(os.path.join(GOLDEN, "fp8_golden.json")))["bits"]
+    for code in range(256):
+        value = oracle.orc_fp8_decode(code)
+        if (code & 127) == 127:
+            assert math.isnan(value)
+        else:
+            assert f32bits(value) == bits[code], code
+
+
+def test_fp8_scaled_products_exact(oracle):
+    bits = np.array(json.load(open(os.path.join(GOLDEN, "fp8_golden.json")))["bits"],
+                    dtype=np.uint32)
+    golden = bits.view(np.float32)
+    for scale in (0.251953125, 1.0078125, 3.140625):
+        for code in range(256):
+            if (code & 127) == 127:
+                continue
+            expected = np.float32(golden[code]) * np.float32(scale)
+            got = np.float32(oracle.orc_fp8_decode(code)) * np.float32(scale)
+            assert got.view(np.uint32) == expected.view(np.uint32)
+
+
+def test_fp8_decode_matches_reference_c(oracle):
+    ref = oracle_lib.load_ref()
+    if ref is None:
+        pytest.skip("oracle/_ref not built (reference checkout absent)")
+    for code in range(256):
+        a, b = oracle.orc_fp8_decode(code), ref.st_f8_e4m3_to_f32(code)
+        if math.isnan(b):
+            assert math.isnan(a)
+        else:
+            assert f32bits(a) == f32bits(b), code
+
+
+def test_bf16_widen_and_round(oracle):
+    ref = oracle_lib.load_ref()
+    for bits in (0, 1, 0x3f80, 0x8000, 0x7f7f, 0xff7f, 0x0080, 0x39fb, 0x1234, 0xc2f7):
+        v = oracle.orc_bf16_widen(bits)
+        assert f32bits(v) == bits << 16
+        if ref is not None:
+            assert f32bits(ref.st_bf16_to_f32(bits)) == bits << 16
+        assert oracle.orc_bf16_round(v) == bits
+    # Round to nearest even at the halfway point.
+    assert oracle.orc_bf16_round(np.uint32(0x3f808000).view(np.float32)) == 0x3f80
+    assert oracle.orc_bf16_round(np.uint32(0x3f818000).view(np.float32)) == 0x3f82
+    assert oracle.orc_bf16_round(np.uint32(0x3f808001).view(np.float32)) == 0x3f81
+
+
+def test_yarn_matches_rope_golden(oracle):
+    g = json.load(open(os.path.join(GOLDEN, "rope_golden.json")))
+    for p, position in enumerate(g["positions"]):
+        rc, c, s = oracle_lib.yarn(position)
+        assert rc == 0
+        for j, half in enumerate(g["half_dims"]):
+            assert abs(c[half] - g["cos_sin"][p][j][0]) < 2e-6
+            assert abs(s[half] - g["cos_sin"][p][j][1]) < 2e-6
+            assert c[half + 64] == c[half] and s[half + 64] == s[half]
+    rc, c, s = oracle_lib.yarn(262144)
+    assert rc != 0
+
+
+def test_yarn_bitwise_against_reference_c(oracle):
+    ref = oracle_lib.load_ref()
+    if ref is None:
+        pytest.skip("oracle/_ref not built (reference checkout absent)")
+    fp = ctypes.POINTER(ctypes.c_float)
+    rc_ = np.empty(128, np.float32)
+    rs_ = np.empty(128, np.float32)
+    positions = list(range(0, 300)) + [4095, 4096, 4351, 4352, 16383, 16384, 16385, 17919,
+                                       100000, 262143]
+    positions += list(np.random.default_rng(7).integers(0, 262144, 300))
+    for position in positions:
+        rc, c, s = oracle_lib.yarn(int(position))
+        assert ref.lunelette_metal_yarn(int(position), rc_.ctypes.data_as(fp),
+                                        rs_.ctypes.data_as(fp)) == 0
+        assert np.array_equal(c.view(np.uint32), rc_.view(np.uint32)), position
+        assert np.array_equal(s.view(np.uint32), rs_.view(np.uint32)), position
+
+
+def test_query_factor_closed_form(oracle):
+    assert oracle.orc_query_factor(0) == 1.0
+    assert oracle.orc_query_factor(16383) == 1.0
+    f = oracle.orc_query_factor(16384)
+    assert f == oracle.orc_query_factor(32767)
+    assert abs(f - (1 + 0.1 * math.log(2))) < 1e-6
+    assert abs(oracle.orc_query_factor(32768) - (1 + 0.1 * math.log(3))) < 1e-6
+
+
+def greedy(lib_fn, logits):
+    token = ctypes.c_int64(-7)
+    rc = lib_fn(logits.ctypes.data, 131072, ctypes.byref(token))
+    return rc, token.value
+
+
+def test_greedy_cases(oracle):
+    ref = oracle_lib.load_ref()
+    cases = []
+    z = np.zeros(131072, np.float32)
+    cases.append(z.copy())
+    a = z.copy(); a[0] = -0.0; cases.append(a)
+    a = z.copy(); a[1] = -0.0; cases.append(a)
+    a = np.full(131072, -10, np.float32); a[42] = -1; a[43] = -1; cases.append(a)
+    rng = np.random.default_rng(3)
+    for _ in range(5):
+        cases.append(rng.normal(size=131072).astype(np.float32))
+    a = rng.normal(size=131072).astype(np.float32); a[77] = a[9000] = 50; cases.append(a)
+    for logits in cases:
+        rc, tok = greedy(oracle.orc_select_greedy, logits)
+        assert rc == 0
+        assert tok == int(np.argmax(logits))  # numpy argmax: first maximum
+        if ref is not None:
+            t = ctypes.c_int64(-1)
+            assert ref.lunelette_select_greedy(logits.ctypes.data, ctypes.byref(t), None, 0) == 0
+            assert t.value == tok
+    for bad in (np.nan, np.inf, -np.inf):
+        a = z.copy(); a[131071] = bad
+        rc, tok = greedy(oracle.orc_select_greedy, a)
+        assert rc != 0 and tok == -7
+
+
+def ulp_distance(a, b):
+    ia = np.array([a], np.float32).view(np.int32)[0].astype(np.int64)
+    ib = np.array([b], np.float32).view(np.int32)[0].astype(np.int64)
+    return abs(int(ia) - int(ib))
+
+
+def test_expf_accuracy_against_libm(oracle):
+    xs = np.concatenate([np.linspace(-87.3, 88.7, 20001, dtype=np.float32),
+                         np.linspace(-1, 1, 4001, dtype=np.float32),
+                         np.float32([0.0, -0.0, 1e-8, -1e-8, 0.5, -0.5, 10, -10, 80, -80])])
+    worst = 0
+    for x in xs:
+        got = oracle.orc_expf(float(x))
+        want = np.float32(math.exp(float(x)))
+        worst = max(worst, ulp_distance(got, want))
+    assert worst <= 2, worst
+
+
+def test_expf_edges(oracle):
+    assert oracle.orc_expf(0.0) == 1.0
+    assert oracle.orc_expf(-1e4) == 0.0
+    assert oracle.orc_expf(-88.0) == 0.0  # below the normal range flushes to +0
+    assert math.isinf(oracle.orc_expf(89.0))
+    assert math.isnan(oracle.orc_expf(float("nan")))
+    assert oracle.orc_expf(-87.3) > 0
+
+
+def test_silu_schedules_close(oracle):
+    for v in np.linspace(-30, 30, 601, dtype=np.float32):
+        exact = float(v) / (1 + math.exp(-float(v)))
+        for fn in (oracle.orc_silu_ref, oracle.orc_silu_mirror):
+            assert abs(fn(float(v)) - exact) <= 2e-6 * max(1.0, abs(exact))
+    assert oracle.orc_silu_mirror(-1e4) == 0.0 and math.copysign(1, oracle.orc_silu_mirror(-1e4)) < 0
