@@ -104,6 +104,18 @@ enum {
  * K/V rows are appended into d_keys/d_values ([8][capacity][128]). */
 int lh_layer_forward(const lh_layer_weights *w, float *d_x, float *d_keys, float *d_values,
     lh_workspace *ws, int path, void *stream);
+/* One operator of the decode-schedule layer (the analogue of
+ * lunelette_metal_encode_operator, src/metal_encode.m:5-50), for timing and
+ * tests. Same arguments as lh_layer_forward; compact FP8 weights. */
+enum {
+    LH_OP_QKV_ROPE = 0,      /* norm + q|k|v + RoPE + KV append */
+    LH_OP_ATTENTION = 1,     /* scores, softmax, P.V, combine */
+    LH_OP_O_RESIDUAL = 2,    /* o projection + residual add */
+    LH_OP_GATEUP_SILU = 3,   /* norm + gate/up + SiLU(gate)*up */
+    LH_OP_DOWN_RESIDUAL = 4  /* down projection + residual add */
+};
+int lh_layer_operator(int op, const lh_layer_weights *w, float *d_x, float *d_keys,
+    float *d_values, lh_workspace *ws, void *stream);
 /* Causal GQA attention (src/metal_kernels.metal:80-132 scores + attend) of
  * the workspace's count query rows d_q [count][4096] over positions
  * [0, length+t] of d_keys/d_values ([8][capacity][128]) into d_out. */

@@ -29,6 +29,7 @@ COMPACT_FP8_ARITHMETIC = 1
 COMPACT_FP8_LOOKUP = 2
 
 PATH_FUSED, PATH_LOOKUP, PATH_UNFUSED, PATH_RESIDENT, PATH_MFMA = range(5)
+OP_QKV_ROPE, OP_ATTENTION, OP_O_RESIDUAL, OP_GATEUP_SILU, OP_DOWN_RESIDUAL = range(5)
 
 _lib = None
 
@@ -122,6 +123,8 @@ def lib():
     _proto(l, "lh_layer_forward", i, ctypes.POINTER(LayerWeights), c_void, c_void, c_void,
            c_void, i, c_void)
     _proto(l, "lh_head_forward", i, c_void, c_void, c_void, c_void, c_void)
+    _proto(l, "lh_layer_operator", i, i, ctypes.POINTER(LayerWeights), c_void, c_void, c_void,
+           c_void, c_void)
     _proto(l, "lh_attention", i, c_void, c_void, c_void, c_void, c_void, c_void)
     _proto(l, "lh_embed_forward", i, c_void, c_void, c_void, c_void)
     _proto(l, "lh_yarn", i, ctypes.c_uint32, c_float_p, c_float_p)

@@ -202,6 +202,38 @@ static int layer_fused(const lh_layer_weights *w, float *x, float *keys, float *
     return 0;
 }
 
+int lh_layer_operator(int op, const lh_layer_weights *w, float *d_x, float *d_keys,
+    float *d_values, lh_workspace *ws, void *stream)
+{
+    if (!w || !d_x || !d_keys || !d_values || !ws || !ws->count) {
+        lh_set_error("layer_operator: missing argument or tokens not set");
+        return -1;
+    }
+    hipStream_t s = (hipStream_t)stream;
+    const uint32_t n = (uint32_t)ws->count, C = (uint32_t)ws->capacity;
+    switch (op) {
+    case LH_OP_QKV_ROPE:
+        return launched(lh_launch_qkv_rope(0, w->qkv, w->scale[0], w->scale[1], w->scale[2],
+            w->input_norm, d_x, ws->d_params, n, ws->d_q, d_keys, d_values, C, s), "qkv");
+    case LH_OP_ATTENTION:
+        return launched(lh_launch_attention(ws->d_q, d_keys, d_values, ws->d_params, n,
+            (uint32_t)(ws->length + n), C, ws->d_S, ws->d_BM, ws->d_PT, ws->d_PA, ws->d_attn, s),
+            "attention");
+    case LH_OP_O_RESIDUAL:
+        return launched(lh_launch_matvec(0, 0, w->o, w->scale[3], ws->d_attn, d_x, d_x, LH_HIDDEN,
+            LH_QUERY, n, s), "o");
+    case LH_OP_GATEUP_SILU:
+        return launched(lh_launch_gateup_silu(0, w->gate, w->up, w->scale[4], w->scale[5],
+            w->post_norm, d_x, n, ws->d_gated, s), "gate/up");
+    case LH_OP_DOWN_RESIDUAL:
+        return launched(lh_launch_matvec(0, 0, w->down, w->scale[6], ws->d_gated, d_x, d_x,
+            LH_HIDDEN, LH_INNER, n, s), "down");
+    default:
+        lh_set_error("layer_operator: unknown operator %d", op);
+        return -1;
+    }
+}
+
 int lh_layer_forward(const lh_layer_weights *w, float *d_x, float *d_keys, float *d_values,
     lh_workspace *ws, int path, void *stream)
 {
