@@ -121,6 +121,13 @@ int lh_layer_operator(int op, const lh_layer_weights *w, float *d_x, float *d_ke
  * [0, length+t] of d_keys/d_values ([8][capacity][128]) into d_out. */
 int lh_attention(const float *d_q, const float *d_keys, const float *d_values, lh_workspace *ws,
     float *d_out, void *stream);
+/* MFMA block projection (PREFILL_MPS; replaces convert_fp8 + MPS GEMM,
+ * src/metal_encode.m:94-110): y[t][r] = scale * sum_c dec(W[r][c]) x[t][c],
+ * FP8 decoded exactly to BF16 tiles, x split exactly into three BF16 parts,
+ * FP32 accumulation. rows % 512 == 0 (<= 3072), cols % 256 == 0 (<= 9216),
+ * tokens <= the workspace block. Uses the workspace's scratch. */
+int lh_fp8_gemm(lh_workspace *ws, const uint8_t *d_w, float scale, const float *d_x, float *d_y,
+    size_t rows, size_t cols, size_t tokens, void *stream);
 /* Final RMSNorm + tied BF16 head on one row (src/metal_encode.m:204-210). */
 int lh_head_forward(const uint16_t *d_embedding, const float *d_gamma, const float *d_xrow,
     float *d_logits, void *stream);

@@ -72,7 +72,8 @@ void lh_workspace_destroy(lh_workspace *ws)
         return;
     }
     void *device[] = {ws->d_params, ws->d_q, ws->d_attn, ws->d_gated, ws->d_up, ws->d_xn,
-        ws->d_qraw, ws->d_kraw, ws->d_vraw, ws->d_S, ws->d_BM, ws->d_PT, ws->d_PA};
+        ws->d_qraw, ws->d_kraw, ws->d_vraw, ws->d_S, ws->d_BM, ws->d_PT, ws->d_PA, ws->d_split,
+        ws->d_gemm};
     for (size_t i = 0; i < sizeof device / sizeof device[0]; i++) {
         if (device[i]) {
             (void)hipFree(device[i]);

@@ -21,7 +21,7 @@
 #include <string.h>
 
 #ifndef LH_HAVE_MFMA
-#define LH_HAVE_MFMA 0
+#define LH_HAVE_MFMA 1
 #endif
 
 struct lunelette_metal_checkpoint {
@@ -353,7 +353,7 @@ lunelette_metal *lunelette_metal_create_synthetic(const lunelette_synthetic_conf
         goto failure;
     }
     rt->ws = lh_workspace_create(C, B);
-    if (!rt->ws) {
+    if (!rt->ws || lh_mfma_prepare(rt->ws)) {
         snprintf(error, capacity, "workspace: %s", lh_last_error());
         goto failure;
     }

@@ -1,0 +1,124 @@
+"""MFMA block-projection path (PREFILL_MPS) on the GPU.
+
+The reference's own MPS path is pinned only by tolerance (tests/test_metal.m:
+200-259: |err| <= 2e-4 + 1e-4|ref| vs double); this path is held tighter:
+- lh_fp8_gemm vs double: |err| <= 2e-6 * sum_c |w x| (exact BF16 operands,
+  FP32 accumulation), output guard untouched;
+- one decoder layer at config 3 (256 tokens after a 4096 prefix) vs the
+  oracle: activations within 1e-3 of the row max-abs (median relative
+  <= 1e-5), appended K/V rows within 1e-5 of the row max-abs;
+- runtime prefill of a 2-layer model in MPS mode: logits within 1e-3 of the
+  logit range of the precise oracle and the same greedy token, continuing
+  into decode.
+"""
+import numpy as np
+import pytest
+
+import lunelette_amd as lh
+from lunelette_amd import synthetic as syn
+from lunelette_amd.runtime import Runtime
+
+import gpu_util
+import oracle_lib
+from oracle_lib import MIRROR, REF
+
+pytestmark = pytest.mark.gpu
+SEED = 99173
+
+
+def run_gemm(gpu, w, scale, x, rows, cols, tokens, block=256):
+    ws = gpu.lh_workspace_create(4352, block)
+    assert ws, lh.last_error()
+    try:
+        d_w = lh.DeviceBuffer.from_array(w)
+        d_x = lh.DeviceBuffer.from_array(x)
+        d_y = lh.DeviceBuffer(tokens * rows * 4 + 64)
+        lh.check(gpu.lh_memset_device(d_y.ptr, 0x5a, d_y.nbytes))
+        lh.check(gpu.lh_fp8_gemm(ws, d_w.ptr, scale, d_x.ptr, d_y.ptr, rows, cols, tokens, None),
+                 "fp8_gemm")
+        raw = d_y.download(np.uint8)
+        assert np.all(raw[tokens * rows * 4:] == 0x5a)
+        return raw[:tokens * rows * 4].view(np.float32).reshape(tokens, rows)
+    finally:
+        gpu.lh_workspace_destroy(ws)
+
+
+@pytest.mark.parametrize("rows,cols,tokens,block", [(3072, 3072, 256, 256), (1024, 4096, 37, 256),
+                                                    (512, 9216, 5, 5), (3072, 9216, 256, 256),
+                                                    (2048, 256, 100, 128)])
+def test_fp8_gemm_vs_double(gpu, rows, cols, tokens, block):
+    w = syn.fp8(SEED, 700 + rows, rows, cols)
+    x = (syn.normal_f32(SEED, 701, tokens * cols) * 3).astype(np.float32)
+    scale = 0.0146484375
+    got = run_gemm(gpu, w, scale, x, rows, cols, tokens, block)
+    table = gpu_util.decode_table() * np.float32(scale)
+    wf = table[w].astype(np.float64)
+    xx = x.reshape(tokens, cols).astype(np.float64)
+    expected = xx @ wf.T
+    magnitude = np.abs(xx) @ np.abs(wf).T
+    assert np.all(np.abs(got - expected) <= 2e-6 * magnitude)
+
+
+def test_rejects_unsupported_gemm_shapes(gpu):
+    ws = gpu.lh_workspace_create(256, 16)
+    try:
+        d = lh.DeviceBuffer(1 << 20)
+        for rows, cols, tokens in ((100, 3072, 1), (3072, 100, 1), (512, 256, 17), (4096, 256, 1)):
+            assert gpu.lh_fp8_gemm(ws, d.ptr, 1.0, d.ptr, d.ptr, rows, cols, tokens, None) == -1
+    finally:
+        gpu.lh_workspace_destroy(ws)
+
+
+def test_mfma_layer_config3(gpu):
+    from test_gpu_layer import oracle_layer, run_layer
+    host = syn.layer(SEED, 0)
+    length, count, capacity = 4096, 256, 4352
+    x = syn.normal_f32(SEED, 9001, count * 3072)
+    kpm = syn.normal_f32(SEED, 9002, length * 1024).reshape(length, 1024)
+    vpm = syn.normal_f32(SEED, 9003, length * 1024).reshape(length, 1024)
+    got = run_layer(gpu, host, x, kpm, vpm, length, count, capacity, lh.PATH_MFMA)
+    for schedule in (MIRROR, REF):
+        want = oracle_layer(host, x, kpm, vpm, length, count, capacity, schedule)
+        gx, wx = got[0].reshape(count, 3072), want[0].reshape(count, 3072)
+        rowmax = np.max(np.abs(wx), axis=1, keepdims=True)
+        assert np.max(np.abs(gx - wx) / rowmax) < 1e-3
+        assert np.median(np.abs(gx - wx) / np.maximum(np.abs(wx), 1e-30)) < 1e-5
+        for g, w_ in zip(got[1:], want[1:]):
+            assert np.max(np.abs(g - w_) / np.max(np.abs(w_), axis=1, keepdims=True)) < 1e-5
+
+
+def test_mfma_layer_small_odd_block(gpu):
+    from test_gpu_layer import oracle_layer, run_layer
+    host = syn.layer(SEED, 1)
+    length, count, capacity = 3, 5, 256
+    x = syn.normal_f32(SEED, 9101, count * 3072)
+    kpm = syn.normal_f32(SEED, 9102, length * 1024).reshape(length, 1024)
+    vpm = syn.normal_f32(SEED, 9103, length * 1024).reshape(length, 1024)
+    got = run_layer(gpu, host, x, kpm, vpm, length, count, capacity, lh.PATH_MFMA)
+    want = oracle_layer(host, x, kpm, vpm, length, count, capacity, MIRROR)
+    gx, wx = got[0].reshape(count, 3072), want[0].reshape(count, 3072)
+    assert np.max(np.abs(gx - wx) / np.max(np.abs(wx), axis=1, keepdims=True)) < 1e-3
+
+
+def test_runtime_mps_prefill_then_decode(gpu):
+    from test_gpu_runtime import LAYERS, SEED as RSEED, oracle_model
+    embedding = syn.embedding(RSEED)
+    host = (embedding, syn.final_norm(RSEED), [syn.layer(RSEED, i) for i in range(LAYERS)])
+    model = oracle_model(host)
+    ids = syn.tokens(RSEED, 11, 64)
+    with Runtime(seed=RSEED, layers=LAYERS, context=256, block=256,
+                 prefill=lh.PREFILL_MPS) as rt:
+        got = rt.prefill(ids)
+        want = model.forward(MIRROR, ids, 0)
+        span = float(want.max() - want.min())
+        assert np.max(np.abs(got - want)) <= 1e-3 * span
+        token = rt.greedy()
+        assert token == int(np.argmax(want))
+        length = len(ids)
+        for _ in range(4):
+            got = rt.decode(token)
+            want = model.forward(MIRROR, [token], length)
+            assert np.max(np.abs(got - want)) <= 1e-3 * float(want.max() - want.min())
+            assert rt.greedy() == int(np.argmax(want))
+            token = rt.greedy()
+            length += 1
