@@ -33,16 +33,42 @@ __device__ __forceinline__ float bf16_to_f32(uint32_t bits16)
 }
 
 // Pairwise halving tree over the 64 lanes of a wave: after the step with
-// distance s, lane i < s holds v_i + v_{i+s}. Lane 0 returns the total.
+// distance s, lane i < s holds v_i + v_{i+s}; lane 0 returns the total.
+// Distances 32 and 16 use gfx950's v_permlane32_swap / v_permlane16_swap,
+// 8..1 a DPP row_shl (lane i reads lane i+s inside its 16-lane row), so the
+// whole tree stays in VALU; only lane 0's value is meaningful.
+__device__ __forceinline__ float dpp_row_shl(float v, int s)
+{
+    const int iv = __float_as_int(v);
+    int r;
+    switch (s) {
+    case 8: r = __builtin_amdgcn_update_dpp(0, iv, 0x108, 0xf, 0xf, false); break;
+    case 4: r = __builtin_amdgcn_update_dpp(0, iv, 0x104, 0xf, 0xf, false); break;
+    case 2: r = __builtin_amdgcn_update_dpp(0, iv, 0x102, 0xf, 0xf, false); break;
+    default: r = __builtin_amdgcn_update_dpp(0, iv, 0x101, 0xf, 0xf, false); break;
+    }
+    return __int_as_float(r);
+}
+
 __device__ __forceinline__ float wave_tree64(float v)
 {
-    v = v + __shfl_down(v, 32, 64);
-    v = v + __shfl_down(v, 16, 64);
-    v = v + __shfl_down(v, 8, 64);
-    v = v + __shfl_down(v, 4, 64);
-    v = v + __shfl_down(v, 2, 64);
-    v = v + __shfl_down(v, 1, 64);
+    const uint32_t u = __float_as_uint(v);
+    const auto p32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    v = v + __uint_as_float(p32[1]);
+    const uint32_t w = __float_as_uint(v);
+    const auto p16 = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+    v = v + __uint_as_float(p16[1]);
+    v = v + dpp_row_shl(v, 8);
+    v = v + dpp_row_shl(v, 4);
+    v = v + dpp_row_shl(v, 2);
+    v = v + dpp_row_shl(v, 1);
     return v;
+}
+
+// Lane 0's value to every lane (scalar read; lane 0 is active in every caller).
+__device__ __forceinline__ float wave_lane0(float v)
+{
+    return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
 }
 
 __device__ __forceinline__ float wave_max64(float v)

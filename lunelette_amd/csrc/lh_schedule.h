@@ -3,11 +3,12 @@
  *
  * Canonical schedule (the CPU oracle's ORC_MIRROR restates it):
  *   row dot  : columns in chunks of 1024; lane l of a 64-lane wave owns columns
- *              [16l, 16l+16) of each chunk and runs acc = fma(w, x, acc) from 0
- *              over them in column order; the chunk's 64 lane values reduce by
- *              the pairwise halving tree (32,16,8,4,2,1); chunk totals are
- *              added in chunk order starting from chunk 0. FP8 elements are
- *              w = fl(dec(code) * scale) (src/metal_kernels.metal:136-144).
+ *              [16l, 16l+16) of every chunk and runs acc = fma(w, x, acc) from
+ *              0 over all of them (chunk by chunk, column order); the 64 lane
+ *              values reduce by the pairwise halving tree (32,16,8,4,2,1);
+ *              the row total is multiplied by the per-tensor scale once. w is
+ *              the exact unscaled E4M3FN decode (FP8), the exact BF16 widening
+ *              (head) or the stored FP32 decode (resident strategy).
  *   RMSNorm  : ss by the row-dot schedule with w = x; r = 1/sqrt(ss/n + 1e-5);
  *              out = gamma * (x * r).
  *   attention: per (token, head) s_p = fl(chain_d fma(q_d, k_pd) * 1/sqrt(128));

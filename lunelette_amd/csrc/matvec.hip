@@ -1,14 +1,14 @@
 // Decode / precise-path projections for gfx950. Every output row is a
-// canonical row dot (lh_schedule.h): lane l of a wave owns 16 consecutive
-// columns of each 1024-column chunk, loads them with one 16-byte load per
-// 16 FP8 codes (32 B for BF16, 64 B for FP32), decodes in registers, chains
-// fused multiply-adds, and the chunk reduces by the fixed 64-lane tree. Chunks
-// are spread over the waves of a workgroup and summed in chunk order.
+// canonical row dot (lh_schedule.h): lane l of one wave owns columns
+// [16l, 16l+16) of every 1024-column chunk, issues one 16-byte load per 16 FP8
+// codes (32 B for BF16, 64 B for FP32) for all of its rows up front, decodes in
+// registers with v_cvt_pk_f32_fp8, chains one fused multiply-add per element
+// across all its chunks, and the 64 lane sums reduce by one fixed tree. The
+// per-tensor scale multiplies the row total once.
 //
-// The FP8 element is w = fl(dec(code) * scale) exactly as the reference's
-// weight() (src/metal_kernels.metal:136-144), so compact FP8 and resident FP32
-// weights give identical bits. The reference sums fl(w*x) with per-lane Kahan
-// (:153-177); here the product and sum are one fused multiply-add.
+// One wave owns whole rows, so there is no LDS and no barrier: a workgroup is
+// four independent waves. The RMSNorm prologue (qkv, gate/up, head) is
+// recomputed per wave from the 12 KiB input row in L2.
 #include "lh_device.h"
 #include "lh_internal.h"
 
@@ -25,7 +25,6 @@ template <> struct WVec<K_F32> { u32x4 v[4]; };
 
 template <int KIND> constexpr int elem_bytes() { return KIND == K_FP8 ? 1 : (KIND == K_BF16 ? 2 : 4); }
 
-// Vector load of the 16 elements a lane owns at column `col` of `row`.
 template <int KIND>
 __device__ __forceinline__ void load_w(WVec<KIND>& w, const void* base, size_t row, uint32_t cols,
     uint32_t col)
@@ -38,10 +37,11 @@ __device__ __forceinline__ void load_w(WVec<KIND>& w, const void* base, size_t r
     }
 }
 
-// Decode the 16 elements held in `w` to FP32 weights (scaled for FP8).
+// acc = fma(w_j, x_j, acc) for the lane's 16 columns in order; FP8 codes are
+// decoded unscaled (exact), BF16 widened exactly, FP32 used as stored.
 template <int KIND, bool LUT>
-__device__ __forceinline__ void decode16(const WVec<KIND>& w, float scale, const float* lut,
-    float out[16])
+__device__ __forceinline__ float chain16(const WVec<KIND>& w, const float x[16], const float* lut,
+    float acc)
 {
     if constexpr (KIND == K_FP8) {
         const uint32_t words[4] = {w.v[0].x, w.v[0].y, w.v[0].z, w.v[0].w};
@@ -58,7 +58,7 @@ __device__ __forceinline__ void decode16(const WVec<KIND>& w, float scale, const
             }
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                out[4 * i + j] = d[j] * scale;
+                acc = __builtin_fmaf(d[j], x[4 * i + j], acc);
             }
         }
     } else if constexpr (KIND == K_BF16) {
@@ -67,37 +67,35 @@ __device__ __forceinline__ void decode16(const WVec<KIND>& w, float scale, const
             const uint32_t words[4] = {w.v[i].x, w.v[i].y, w.v[i].z, w.v[i].w};
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                out[8 * i + 2 * j] = __uint_as_float(words[j] << 16);
-                out[8 * i + 2 * j + 1] = __uint_as_float(words[j] & 0xffff0000u);
+                acc = __builtin_fmaf(__uint_as_float(words[j] << 16), x[8 * i + 2 * j], acc);
+                acc = __builtin_fmaf(__uint_as_float(words[j] & 0xffff0000u), x[8 * i + 2 * j + 1],
+                    acc);
             }
         }
     } else {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            out[4 * i + 0] = __uint_as_float(w.v[i].x);
-            out[4 * i + 1] = __uint_as_float(w.v[i].y);
-            out[4 * i + 2] = __uint_as_float(w.v[i].z);
-            out[4 * i + 3] = __uint_as_float(w.v[i].w);
+            acc = __builtin_fmaf(__uint_as_float(w.v[i].x), x[4 * i + 0], acc);
+            acc = __builtin_fmaf(__uint_as_float(w.v[i].y), x[4 * i + 1], acc);
+            acc = __builtin_fmaf(__uint_as_float(w.v[i].z), x[4 * i + 2], acc);
+            acc = __builtin_fmaf(__uint_as_float(w.v[i].w), x[4 * i + 3], acc);
         }
     }
+    return acc;
 }
 
-// Scalar element fetch for unaligned shapes (partial lanes only).
 template <int KIND, bool LUT>
-__device__ __forceinline__ float load_elem(const void* base, size_t index, float scale,
-    const float* lut)
+__device__ __forceinline__ float load_elem(const void* base, size_t index, const float* lut)
 {
     if constexpr (KIND == K_FP8) {
-        uint32_t code = static_cast<const uint8_t*>(base)[index];
-        float d;
+        const uint32_t code = static_cast<const uint8_t*>(base)[index];
         if constexpr (LUT) {
-            d = lut[code];
+            return lut[code];
         } else {
             float four[4];
             fp8x4_to_f32(code, four);
-            d = four[0];
+            return four[0];
         }
-        return d * scale;
     } else if constexpr (KIND == K_BF16) {
         return __uint_as_float((uint32_t)static_cast<const uint16_t*>(base)[index] << 16);
     } else {
@@ -105,22 +103,12 @@ __device__ __forceinline__ float load_elem(const void* base, size_t index, float
     }
 }
 
-__device__ __forceinline__ float chain16(const float w[16], const float x[16])
-{
-    float acc = 0.0f;
-#pragma unroll
-    for (int j = 0; j < 16; j++) {
-        acc = __builtin_fmaf(w[j], x[j], acc);
-    }
-    return acc;
-}
-
 __device__ __forceinline__ void load_x16(const float* x, float out[16])
 {
     const float4* p = reinterpret_cast<const float4*>(x);
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        float4 v = p[i];
+        const float4 v = p[i];
         out[4 * i + 0] = v.x;
         out[4 * i + 1] = v.y;
         out[4 * i + 2] = v.z;
@@ -128,7 +116,7 @@ __device__ __forceinline__ void load_x16(const float* x, float out[16])
     }
 }
 
-// Unscaled E4M3FN table for the lookup strategy, filled from the arithmetic
+// Unscaled E4M3FN table (the lookup strategy), filled from the arithmetic
 // decode so both strategies agree bit for bit.
 __device__ __forceinline__ void fill_lut(float* lut)
 {
@@ -139,165 +127,280 @@ __device__ __forceinline__ void fill_lut(float* lut)
     }
 }
 
-// Canonical RMSNorm prologue for a 3-chunk (3072-wide) row held as one chunk
-// per wave: every thread ends with r; lane values are normalized in place.
-template <int NW>
-__device__ __forceinline__ void rmsnorm_chunk_prologue(float xs[16], const float* gamma,
-    uint32_t col, float* lds_ss, uint32_t nchunks, uint32_t width)
+// Canonical RMSNorm of the lane's NCH x 16 values held in xs (row width
+// NCH*1024): ss by the row-dot schedule with w = x, r = 1/sqrt(ss/n + 1e-5),
+// xs = gamma * (xs * r). Wave-local; every lane ends with the same r.
+template <int NCH>
+__device__ __forceinline__ void rmsnorm_wave(float (&xs)[NCH][16], const float* gamma)
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int lane = threadIdx.x & 63;
     float acc = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 16; j++) {
-        acc = __builtin_fmaf(xs[j], xs[j], acc);
+    for (int c = 0; c < NCH; c++) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            acc = __builtin_fmaf(xs[c][j], xs[c][j], acc);
+        }
     }
-    acc = wave_tree64(acc);
-    if (lane == 0) {
-        lds_ss[wave] = acc;
+    const float ss = wave_lane0(wave_tree64(acc));
+    const float r = 1.0f / __builtin_sqrtf(ss / (float)(NCH * LH_CHUNK) + 1e-5f);
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        float g[16];
+        load_x16(gamma + c * LH_CHUNK + lane * LH_LANE_COLS, g);
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            xs[c][j] = g[j] * (xs[c][j] * r);
+        }
+    }
+}
+
+template <int NCH>
+__device__ __forceinline__ void load_row_slices(const float* row, float (&xs)[NCH][16])
+{
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+        load_x16(row + c * LH_CHUNK + lane * LH_LANE_COLS, xs[c]);
+    }
+}
+
+// Workgroup-shared input slices, in two phases around the weight loads.
+// Phase 1 (wave 0): load the lane slices of the input row and of gamma. Vector
+// loads retire in issue order, so these must precede the weight loads or the
+// normalization would wait for the weights too.
+template <int NCH>
+__device__ __forceinline__ void wg_input_load(const float* row, const float* gamma,
+    float (&xs)[NCH][16], float (&gs)[NCH][16])
+{
+    if ((threadIdx.x >> 6) == 0) {
+        load_row_slices<NCH>(row, xs);
+        if (gamma) {
+            load_row_slices<NCH>(gamma, gs);
+        }
+    }
+}
+
+// Phase 2: wave 0 RMS-normalizes (when gamma is given) and publishes through
+// LDS laid out [chunk][quad][lane] (16-byte words, conflict-free); every wave
+// reads its copy back.
+template <int NCH>
+__device__ __forceinline__ void wg_input_publish(bool norm, float (&xs)[NCH][16],
+    const float (&gs)[NCH][16], float4* lds)
+{
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    if (wave == 0) {
+        if (norm) {
+            float acc = 0.0f;
+#pragma unroll
+            for (int c = 0; c < NCH; c++) {
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    acc = __builtin_fmaf(xs[c][j], xs[c][j], acc);
+                }
+            }
+            const float ss = wave_lane0(wave_tree64(acc));
+            const float r = 1.0f / __builtin_sqrtf(ss / (float)(NCH * LH_CHUNK) + 1e-5f);
+#pragma unroll
+            for (int c = 0; c < NCH; c++) {
+#pragma unroll
+                for (int j = 0; j < 16; j++) {
+                    xs[c][j] = gs[c][j] * (xs[c][j] * r);
+                }
+            }
+        }
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                lds[(c * 4 + q) * 64 + lane] =
+                    make_float4(xs[c][4 * q], xs[c][4 * q + 1], xs[c][4 * q + 2], xs[c][4 * q + 3]);
+            }
+        }
     }
     __syncthreads();
-    float ss = lds_ss[0];
-    for (uint32_t c = 1; c < nchunks; c++) {
-        ss = ss + lds_ss[c];
-    }
-    float r = 1.0f / __builtin_sqrtf(ss / (float)width + 1e-5f);
-    float g[16];
-    load_x16(gamma + col, g);
+    if (wave != 0) {
 #pragma unroll
-    for (int j = 0; j < 16; j++) {
-        xs[j] = g[j] * (xs[j] * r);
+        for (int c = 0; c < NCH; c++) {
+#pragma unroll
+            for (int q = 0; q < 4; q++) {
+                const float4 v = lds[(c * 4 + q) * 64 + lane];
+                xs[c][4 * q] = v.x;
+                xs[c][4 * q + 1] = v.y;
+                xs[c][4 * q + 2] = v.z;
+                xs[c][4 * q + 3] = v.w;
+            }
+        }
+    }
+}
+
+// Issue the lane's loads for R rows (row-major, NCH*1024 columns) before any
+// other memory traffic of the wave, so weight latency overlaps the input-row
+// loads and the RMSNorm prologue.
+template <int KIND, int NCH, int R>
+__device__ __forceinline__ void issue_rows(const void* W, const uint32_t (&rows)[R],
+    WVec<KIND> (&wv)[R][NCH])
+{
+    const int lane = threadIdx.x & 63;
+    constexpr uint32_t K = NCH * LH_CHUNK;
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            load_w<KIND>(wv[r][c], W, rows[r], K, c * LH_CHUNK + lane * LH_LANE_COLS);
+        }
+    }
+}
+
+// R canonical dots (unscaled) of the issued rows against the lane's x
+// slices; lane 0 holds the wave totals. The R chains are interleaved element
+// by element (each row's own order is unchanged) for instruction-level
+// parallelism.
+template <int KIND, bool LUT, int NCH, int R>
+__device__ __forceinline__ void dot_rows(const WVec<KIND> (&wv)[R][NCH],
+    const float (&xs)[NCH][16], const float* lut, float (&out)[R])
+{
+    float acc[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        acc[r] = 0.0f;
+    }
+#pragma unroll
+    for (int c = 0; c < NCH; c++) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            acc[r] = chain16<KIND, LUT>(wv[r][c], xs[c], lut, acc[r]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        out[r] = wave_tree64(acc[r]);
     }
 }
 
 // ---------------------------------------------------------------------------
-// Generic row dots: y[t][r] = (residual ? residual[t][r] : 0 +) dot(W[r], x[t]).
-// grid (ceil(rows/R), tokens), block NW waves. VEC requires cols*elem % 16 == 0.
-template <int KIND, bool LUT, bool VEC, int NW, int R>
-__global__ void __launch_bounds__(NW * 64)
-k_matvec(const void* __restrict__ W, float scale, const float* __restrict__ x,
-    float* y, const float* residual, uint32_t rows, uint32_t cols)
+// Model-shape row dots: y[t][row] = (residual ? residual[t][row] + : ) s * dot.
+// Wave w of workgroup b owns rows R*(4b + w) .. +R. grid (rows/(4R), tokens).
+template <int KIND, bool LUT, int NCH, int R>
+__global__ void __launch_bounds__(256)
+k_rows(const void* __restrict__ W, float scale, const float* __restrict__ x, float* y,
+    const float* residual, uint32_t rows)
 {
-    extern __shared__ float smem[];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t t = blockIdx.y;
-    const uint32_t row0 = blockIdx.x * R;
-    const uint32_t nch = (cols + LH_CHUNK - 1) / LH_CHUNK;
-    float* Q = smem;
-    float* lut = smem + R * nch;
+    __shared__ float lut_s[LUT ? 256 : 1];
     if constexpr (LUT) {
-        fill_lut(lut);
+        fill_lut(lut_s);
         __syncthreads();
     }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t t = blockIdx.y;
+    const uint32_t row0 = (blockIdx.x * 4 + wave) * R;
+    uint32_t rr[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        rr[r] = row0 + r;
+    }
+    __shared__ float4 xin_s[NCH * 4 * 64];
+    float xs[NCH][16], gs[NCH][16];
+    wg_input_load<NCH>(x + (size_t)t * NCH * LH_CHUNK, nullptr, xs, gs);
+    WVec<KIND> wv[R][NCH];
+    issue_rows<KIND, NCH, R>(W, rr, wv);
+    wg_input_publish<NCH>(false, xs, gs, xin_s);
+    float dots[R];
+    dot_rows<KIND, LUT, NCH, R>(wv, xs, lut_s, dots);
+    if (lane == 0) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const size_t o = (size_t)t * rows + row0 + r;
+            const float v = dots[r] * scale;
+            y[o] = residual ? residual[o] + v : v;
+        }
+    }
+}
+
+// Generic shapes (kernel-level ABI): one wave per row, chunks in a loop,
+// vector loads where the lane's 16 columns are whole and aligned.
+template <int KIND, bool LUT, bool VEC>
+__global__ void __launch_bounds__(256)
+k_rows_generic(const void* __restrict__ W, float scale, const float* __restrict__ x, float* y,
+    const float* residual, uint32_t rows, uint32_t cols)
+{
+    __shared__ float lut_s[LUT ? 256 : 1];
+    if constexpr (LUT) {
+        fill_lut(lut_s);
+        __syncthreads();
+    }
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t t = blockIdx.y;
+    const uint32_t row = blockIdx.x * 4 + wave;
+    if (row >= rows) {
+        return;
+    }
     const float* xt = x + (size_t)t * cols;
-    for (uint32_t c = wave; c < nch; c += NW) {
-        const uint32_t col = c * LH_CHUNK + lane * LH_LANE_COLS;
+    float acc = 0.0f;
+    for (uint32_t c0 = 0; c0 < cols; c0 += LH_CHUNK) {
+        const uint32_t col = c0 + lane * LH_LANE_COLS;
         const int valid = col >= cols ? 0 : (cols - col >= 16 ? 16 : (int)(cols - col));
-        float acc[R];
         if (VEC && valid == 16) {
             float xs[16];
             load_x16(xt + col, xs);
-            WVec<KIND> wv[R];
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                if (row0 + r < rows) {
-                    load_w<KIND>(wv[r], W, row0 + r, cols, col);
-                }
-            }
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                float w[16];
-                decode16<KIND, LUT>(wv[r], scale, lut, w);
-                acc[r] = row0 + r < rows ? chain16(w, xs) : 0.0f;
-            }
+            WVec<KIND> wv;
+            load_w<KIND>(wv, W, row, cols, col);
+            acc = chain16<KIND, LUT>(wv, xs, lut_s, acc);
         } else {
-#pragma unroll
-            for (int r = 0; r < R; r++) {
-                float a = 0.0f;
-                if (row0 + r < rows) {
-                    for (int j = 0; j < valid; j++) {
-                        float w = load_elem<KIND, LUT>(W, (size_t)(row0 + r) * cols + col + j,
-                            scale, lut);
-                        a = __builtin_fmaf(w, xt[col + j], a);
-                    }
-                }
-                acc[r] = a;
-            }
-        }
-        // Trees run with the whole wave converged.
-#pragma unroll
-        for (int r = 0; r < R; r++) {
-            float total = wave_tree64(acc[r]);
-            if (lane == 0) {
-                Q[r * nch + c] = total;
+            for (int j = 0; j < valid; j++) {
+                acc = __builtin_fmaf(load_elem<KIND, LUT>(W, (size_t)row * cols + col + j, lut_s),
+                    xt[col + j], acc);
             }
         }
     }
-    __syncthreads();
-    const uint32_t r = threadIdx.x;
-    if (r < R && row0 + r < rows) {
-        float v = Q[r * nch];
-        for (uint32_t c = 1; c < nch; c++) {
-            v = v + Q[r * nch + c];
-        }
-        const size_t o = (size_t)t * rows + row0 + r;
+    const float total = wave_tree64(acc);
+    if (lane == 0) {
+        const size_t o = (size_t)t * rows + row;
+        const float v = total * scale;
         y[o] = residual ? residual[o] + v : v;
     }
 }
 
 // ---------------------------------------------------------------------------
-// Fused RMSNorm -> q|k|v rows -> RoPE (+ query factor on Q) -> Q scratch and
-// KV cache append (src/metal_encode.m:129-153). Workgroup g covers one head
-// (g/16 of 48: 32 q, 8 k, 8 v) and the four RoPE pairs (i, i+64) for
-// i = 4*(g%16) .. +3. grid (768, count), block 192 (one chunk per wave).
+// RMSNorm -> q|k|v -> RoPE (+ query factor on Q) -> Q scratch and KV append
+// (src/metal_encode.m:129-153). Wave g owns RoPE pairs i, i+1 (i = 2*(g%32))
+// of head g/32 (48 heads: 32 q, 8 k, 8 v): rows head*128 + {i, i+1} and + 64.
+// grid (48*32/4, count), block 256.
 template <bool LUT>
-__global__ void __launch_bounds__(192)
+__global__ void __launch_bounds__(256)
 k_qkv_rope(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restrict__ gamma,
     const float* __restrict__ xin, const lh_step_params* __restrict__ params,
     float* __restrict__ qout, float* __restrict__ kcache, float* __restrict__ vcache,
     uint32_t capacity)
 {
-    __shared__ float Q[8][3];
-    __shared__ float lds_ss[3];
     __shared__ float lut_s[LUT ? 256 : 1];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t t = blockIdx.y;
-    const uint32_t head = blockIdx.x >> 4;
-    const uint32_t i0 = (blockIdx.x & 15) * 4;
-    const float scale = head < 32 ? scales.x : (head < 40 ? scales.y : scales.z);
     if constexpr (LUT) {
         fill_lut(lut_s);
+        __syncthreads();
     }
-    const uint32_t col = wave * LH_CHUNK + lane * LH_LANE_COLS;
-    float xs[16];
-    load_x16(xin + (size_t)t * LH_HIDDEN + col, xs);
-    WVec<K_FP8> wv[8];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t t = blockIdx.y;
+    const uint32_t g = blockIdx.x * 4 + wave;
+    const uint32_t head = g >> 5, i0 = 2 * (g & 31);
+    const uint32_t base = head * 128 + i0;
+    const uint32_t rr[4] = {base, base + 1, base + 64, base + 65};
+    __shared__ float4 xin_s[3 * 4 * 64];
+    float xs[3][16], gs[3][16];
+    wg_input_load<3>(xin + (size_t)t * LH_HIDDEN, gamma, xs, gs);
+    WVec<K_FP8> wv[4][3];
+    issue_rows<K_FP8, 3, 4>(Wqkv, rr, wv);
+    wg_input_publish<3>(true, xs, gs, xin_s);
+    float dots[4];
+    dot_rows<K_FP8, LUT, 3, 4>(wv, xs, lut_s, dots);
+    const float scale = head < 32 ? scales.x : (head < 40 ? scales.y : scales.z);
+    const lh_token_params* tp = &params->tokens[t];
+    const uint32_t position = params->length + t;
+    if (lane == 0) {
 #pragma unroll
-    for (int r = 0; r < 8; r++) {
-        const uint32_t row = head * 128 + i0 + (r & 3) + (r >= 4 ? 64 : 0);
-        load_w<K_FP8>(wv[r], Wqkv, row, LH_HIDDEN, col);
-    }
-    rmsnorm_chunk_prologue<3>(xs, gamma, col, lds_ss, 3, LH_HIDDEN);
-#pragma unroll
-    for (int r = 0; r < 8; r++) {
-        float w[16];
-        decode16<K_FP8, LUT>(wv[r], scale, lut_s, w);
-        float acc = wave_tree64(chain16(w, xs));
-        if (lane == 0) {
-            Q[r][wave] = acc;
-        }
-    }
-    __syncthreads();
-    if (threadIdx.x < 4) {
-        const uint32_t j = threadIdx.x;
-        float lo = Q[j][0];
-        lo = lo + Q[j][1];
-        lo = lo + Q[j][2];
-        float hi = Q[4 + j][0];
-        hi = hi + Q[4 + j][1];
-        hi = hi + Q[4 + j][2];
-        const uint32_t i = i0 + j;
-        const lh_token_params* tp = &params->tokens[t];
-        const uint32_t position = params->length + t;
+        for (int p = 0; p < 2; p++) {
+        const uint32_t i = i0 + p;
+        const float lo = dots[p] * scale;
+        const float hi = dots[2 + p] * scale;
         if (head < 40) {
             // column i < 64 rotates with -x[i+64]; column i+64 with x[i].
             float out_lo = lo * tp->cosine[i] + (-hi) * tp->sine[i];
@@ -318,129 +421,89 @@ k_qkv_rope(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restr
             vr[i] = lo;
             vr[i + 64] = hi;
         }
+        }
     }
 }
 
-// Fused RMSNorm -> gate and up rows -> SiLU(gate)*up (src/metal_encode.m:162-171).
-// grid (2304, count), block 192; workgroup g covers inner rows 4g..4g+3.
+// RMSNorm -> gate and up rows -> SiLU(gate)*up (src/metal_encode.m:162-171).
+// Wave g owns inner rows 2g, 2g+1 (gate and up). grid (9216/8, count).
 template <bool LUT>
-__global__ void __launch_bounds__(192)
+__global__ void __launch_bounds__(256)
 k_gateup_silu(const uint8_t* __restrict__ Wgate, const uint8_t* __restrict__ Wup, float2 scales,
     const float* __restrict__ gamma, const float* __restrict__ xin, float* __restrict__ gated)
 {
-    __shared__ float Q[8][3];
-    __shared__ float lds_ss[3];
     __shared__ float lut_s[LUT ? 256 : 1];
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t t = blockIdx.y;
-    const uint32_t row0 = blockIdx.x * 4;
     if constexpr (LUT) {
         fill_lut(lut_s);
+        __syncthreads();
     }
-    const uint32_t col = wave * LH_CHUNK + lane * LH_LANE_COLS;
-    float xs[16];
-    load_x16(xin + (size_t)t * LH_HIDDEN + col, xs);
-    WVec<K_FP8> wv[8];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t t = blockIdx.y;
+    const uint32_t row0 = (blockIdx.x * 4 + wave) * 2;
+    const uint32_t rr[2] = {row0, row0 + 1};
+    __shared__ float4 xin_s[3 * 4 * 64];
+    float xs[3][16], gs[3][16];
+    wg_input_load<3>(xin + (size_t)t * LH_HIDDEN, gamma, xs, gs);
+    WVec<K_FP8> wg[2][3], wu[2][3];
+    issue_rows<K_FP8, 3, 2>(Wgate, rr, wg);
+    issue_rows<K_FP8, 3, 2>(Wup, rr, wu);
+    wg_input_publish<3>(true, xs, gs, xin_s);
+    float g[2], u[2];
+    dot_rows<K_FP8, LUT, 3, 2>(wg, xs, lut_s, g);
+    dot_rows<K_FP8, LUT, 3, 2>(wu, xs, lut_s, u);
+    if (lane == 0) {
 #pragma unroll
-    for (int r = 0; r < 4; r++) {
-        load_w<K_FP8>(wv[r], Wgate, row0 + r, LH_HIDDEN, col);
-        load_w<K_FP8>(wv[4 + r], Wup, row0 + r, LH_HIDDEN, col);
-    }
-    rmsnorm_chunk_prologue<3>(xs, gamma, col, lds_ss, 3, LH_HIDDEN);
-#pragma unroll
-    for (int r = 0; r < 8; r++) {
-        float w[16];
-        decode16<K_FP8, LUT>(wv[r], r < 4 ? scales.x : scales.y, lut_s, w);
-        float acc = wave_tree64(chain16(w, xs));
-        if (lane == 0) {
-            Q[r][wave] = acc;
+        for (int r = 0; r < 2; r++) {
+            const float gv = g[r] * scales.x;
+            const float uv = u[r] * scales.y;
+            gated[(size_t)t * LH_INNER + row0 + r] = silu(gv) * uv;
         }
-    }
-    __syncthreads();
-    if (threadIdx.x < 4) {
-        const uint32_t j = threadIdx.x;
-        float g = Q[j][0];
-        g = g + Q[j][1];
-        g = g + Q[j][2];
-        float u = Q[4 + j][0];
-        u = u + Q[4 + j][1];
-        u = u + Q[4 + j][2];
-        gated[(size_t)t * LH_INNER + row0 + j] = silu(g) * u;
     }
 }
 
-// Fused final RMSNorm -> tied BF16 head (src/metal_encode.m:204-210): the
-// embedding stays BF16 in HBM and widens exactly in registers.
-// grid (VOCAB/8), block 192.
-__global__ void __launch_bounds__(192)
+// Final RMSNorm -> tied BF16 head (src/metal_encode.m:204-210); the embedding
+// stays BF16 in HBM and widens exactly in registers. grid (VOCAB/16).
+__global__ void __launch_bounds__(256)
 k_head(const uint16_t* __restrict__ E, const float* __restrict__ gamma,
     const float* __restrict__ xrow, float* __restrict__ logits)
 {
-    __shared__ float Q[8][3];
-    __shared__ float lds_ss[3];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t row0 = blockIdx.x * 8;
-    const uint32_t col = wave * LH_CHUNK + lane * LH_LANE_COLS;
-    float xs[16];
-    load_x16(xrow + col, xs);
-    WVec<K_BF16> wv[8];
+    const uint32_t row0 = (blockIdx.x * 4 + wave) * 4;
+    const uint32_t rr[4] = {row0, row0 + 1, row0 + 2, row0 + 3};
+    __shared__ float4 xin_s[3 * 4 * 64];
+    float xs[3][16], gs[3][16];
+    wg_input_load<3>(xrow, gamma, xs, gs);
+    WVec<K_BF16> wv[4][3];
+    issue_rows<K_BF16, 3, 4>(E, rr, wv);
+    wg_input_publish<3>(true, xs, gs, xin_s);
+    float dots[4];
+    dot_rows<K_BF16, false, 3, 4>(wv, xs, nullptr, dots);
+    if (lane == 0) {
 #pragma unroll
-    for (int r = 0; r < 8; r++) {
-        load_w<K_BF16>(wv[r], E, row0 + r, LH_HIDDEN, col);
-    }
-    rmsnorm_chunk_prologue<3>(xs, gamma, col, lds_ss, 3, LH_HIDDEN);
-#pragma unroll
-    for (int r = 0; r < 8; r++) {
-        float w[16];
-        decode16<K_BF16, false>(wv[r], 1.0f, nullptr, w);
-        float acc = wave_tree64(chain16(w, xs));
-        if (lane == 0) {
-            Q[r][wave] = acc;
+        for (int r = 0; r < 4; r++) {
+            logits[row0 + r] = dots[r];
         }
-    }
-    __syncthreads();
-    if (threadIdx.x < 8) {
-        const uint32_t r = threadIdx.x;
-        float v = Q[r][0];
-        v = v + Q[r][1];
-        v = v + Q[r][2];
-        logits[row0 + r] = v;
     }
 }
 
-// Standalone canonical RMSNorm (tests and the multi-token MFMA path).
-// grid (tokens), block 64*ceil(width/1024) up to 16 waves.
-__global__ void __launch_bounds__(1024)
+// Standalone canonical RMSNorm, one wave per token row (width <= 16384).
+__global__ void __launch_bounds__(64)
 k_rmsnorm(const float* __restrict__ gamma, const float* __restrict__ x, float* __restrict__ out,
     uint32_t width)
 {
-    __shared__ float lds_ss[16];
-    __shared__ float r_s;
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t t = blockIdx.x;
-    const uint32_t nch = (width + LH_CHUNK - 1) / LH_CHUNK;
-    const float* row = x + (size_t)t * width;
-    const uint32_t col = wave * LH_CHUNK + lane * LH_LANE_COLS;
+    const int lane = threadIdx.x & 63;
+    const float* row = x + (size_t)blockIdx.x * width;
     float acc = 0.0f;
-    for (uint32_t j = 0; j < 16 && col + j < width; j++) {
-        acc = __builtin_fmaf(row[col + j], row[col + j], acc);
-    }
-    acc = wave_tree64(acc);
-    if (lane == 0) {
-        lds_ss[wave] = acc;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        float ss = lds_ss[0];
-        for (uint32_t c = 1; c < nch; c++) {
-            ss = ss + lds_ss[c];
+    for (uint32_t c0 = 0; c0 < width; c0 += LH_CHUNK) {
+        const uint32_t col = c0 + lane * LH_LANE_COLS;
+        for (uint32_t j = 0; j < 16 && col + j < width; j++) {
+            acc = __builtin_fmaf(row[col + j], row[col + j], acc);
         }
-        r_s = 1.0f / __builtin_sqrtf(ss / (float)width + 1e-5f);
     }
-    __syncthreads();
-    const float r = r_s;
-    for (uint32_t c = threadIdx.x; c < width; c += blockDim.x) {
-        out[(size_t)t * width + c] = gamma[c] * (row[c] * r);
+    const float ss = wave_lane0(wave_tree64(acc));
+    const float r = 1.0f / __builtin_sqrtf(ss / (float)width + 1e-5f);
+    for (uint32_t c = lane; c < width; c += 64) {
+        out[(size_t)blockIdx.x * width + c] = gamma[c] * (row[c] * r);
     }
 }
 
@@ -451,17 +514,56 @@ using namespace lh;
 // ---------------------------------------------------------------------------
 // Launchers (C ABI, internal).
 
-template <int KIND, bool LUT, bool VEC>
-static int launch_matvec(const void* W, float scale, const float* x, float* y,
+template <int KIND, bool LUT, int NCH, int R>
+static int launch_rows(const void* W, float scale, const float* x, float* y, const float* residual,
+    uint32_t rows, uint32_t tokens, hipStream_t s)
+{
+    dim3 grid(rows / (4 * R), tokens);
+    hipLaunchKernelGGL((k_rows<KIND, LUT, NCH, R>), grid, dim3(256), 0, s, W, scale, x, y,
+        residual, rows);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// Model shapes (3072, 4096 or 9216 columns, rows a multiple of 4R) use the
+// unrolled kernel; returns 1 when the shape is not one of them.
+template <int KIND, bool LUT>
+static int launch_model_rows(const void* W, float scale, const float* x, float* y,
     const float* residual, uint32_t rows, uint32_t cols, uint32_t tokens, hipStream_t s)
 {
-    constexpr int NW = 4, R = 4;
-    const uint32_t nch = (cols + LH_CHUNK - 1) / LH_CHUNK;
-    const size_t lds = (R * nch + (LUT ? 256 : 0)) * sizeof(float);
-    dim3 grid((rows + R - 1) / R, tokens);
-    hipLaunchKernelGGL((k_matvec<KIND, LUT, VEC, NW, R>), grid, dim3(NW * 64), lds, s,
-        W, scale, x, y, residual, rows, cols);
+    if (cols == 3072 && rows % 16 == 0) {
+        return launch_rows<KIND, LUT, 3, 4>(W, scale, x, y, residual, rows, tokens, s);
+    }
+    if (cols == 4096 && rows % 8 == 0) {
+        return launch_rows<KIND, LUT, 4, 2>(W, scale, x, y, residual, rows, tokens, s);
+    }
+    if (cols == 9216 && rows % 8 == 0) {
+        return launch_rows<KIND, LUT, 9, 2>(W, scale, x, y, residual, rows, tokens, s);
+    }
+    return 1;
+}
+
+template <int KIND, bool LUT, bool VEC>
+static int launch_generic(const void* W, float scale, const float* x, float* y,
+    const float* residual, uint32_t rows, uint32_t cols, uint32_t tokens, hipStream_t s)
+{
+    dim3 grid((rows + 3) / 4, tokens);
+    hipLaunchKernelGGL((k_rows_generic<KIND, LUT, VEC>), grid, dim3(256), 0, s, W, scale, x, y,
+        residual, rows, cols);
     return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+template <int KIND, bool LUT>
+static int dispatch(const void* W, float scale, const float* x, float* y, const float* residual,
+    uint32_t rows, uint32_t cols, uint32_t tokens, bool vec, hipStream_t s)
+{
+    if (vec) {
+        const int rc = launch_model_rows<KIND, LUT>(W, scale, x, y, residual, rows, cols, tokens, s);
+        if (rc <= 0) {
+            return rc;
+        }
+        return launch_generic<KIND, LUT, true>(W, scale, x, y, residual, rows, cols, tokens, s);
+    }
+    return launch_generic<KIND, LUT, false>(W, scale, x, y, residual, rows, cols, tokens, s);
 }
 
 extern "C" int lh_launch_matvec(int kind, int lookup, const void* W, float scale,
@@ -473,22 +575,16 @@ extern "C" int lh_launch_matvec(int kind, int lookup, const void* W, float scale
     }
     const size_t esize = kind == K_FP8 ? 1 : (kind == K_BF16 ? 2 : 4);
     const bool vec = ((size_t)cols * esize) % 16 == 0 && ((uintptr_t)W % 16) == 0 &&
-        ((uintptr_t)x % 16) == 0;
+        ((uintptr_t)x % 16) == 0 && cols % 4 == 0;
     if (kind == K_FP8) {
-        if (lookup) {
-            return vec ? launch_matvec<K_FP8, true, true>(W, scale, x, y, residual, rows, cols, tokens, s)
-                       : launch_matvec<K_FP8, true, false>(W, scale, x, y, residual, rows, cols, tokens, s);
-        }
-        return vec ? launch_matvec<K_FP8, false, true>(W, scale, x, y, residual, rows, cols, tokens, s)
-                   : launch_matvec<K_FP8, false, false>(W, scale, x, y, residual, rows, cols, tokens, s);
+        return lookup ? dispatch<K_FP8, true>(W, scale, x, y, residual, rows, cols, tokens, vec, s)
+                      : dispatch<K_FP8, false>(W, scale, x, y, residual, rows, cols, tokens, vec, s);
     }
     if (kind == K_BF16) {
-        return vec ? launch_matvec<K_BF16, false, true>(W, 1.0f, x, y, residual, rows, cols, tokens, s)
-                   : launch_matvec<K_BF16, false, false>(W, 1.0f, x, y, residual, rows, cols, tokens, s);
+        return dispatch<K_BF16, false>(W, scale, x, y, residual, rows, cols, tokens, vec, s);
     }
     if (kind == K_F32) {
-        return vec ? launch_matvec<K_F32, false, true>(W, 1.0f, x, y, residual, rows, cols, tokens, s)
-                   : launch_matvec<K_F32, false, false>(W, 1.0f, x, y, residual, rows, cols, tokens, s);
+        return dispatch<K_F32, false>(W, scale, x, y, residual, rows, cols, tokens, vec, s);
     }
     return -1;
 }
@@ -497,13 +593,13 @@ extern "C" int lh_launch_qkv_rope(int lookup, const uint8_t* Wqkv, float sq, flo
     const float* gamma, const float* x, const lh_step_params* params, uint32_t count,
     float* q, float* kcache_layer, float* vcache_layer, uint32_t capacity, hipStream_t s)
 {
-    dim3 grid(48 * 16, count);
+    dim3 grid(48 * 32 / 4, count);
     float3 scales = make_float3(sq, sk, sv);
     if (lookup) {
-        hipLaunchKernelGGL(k_qkv_rope<true>, grid, dim3(192), 0, s, Wqkv, scales, gamma, x, params,
+        hipLaunchKernelGGL(k_qkv_rope<true>, grid, dim3(256), 0, s, Wqkv, scales, gamma, x, params,
             q, kcache_layer, vcache_layer, capacity);
     } else {
-        hipLaunchKernelGGL(k_qkv_rope<false>, grid, dim3(192), 0, s, Wqkv, scales, gamma, x, params,
+        hipLaunchKernelGGL(k_qkv_rope<false>, grid, dim3(256), 0, s, Wqkv, scales, gamma, x, params,
             q, kcache_layer, vcache_layer, capacity);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
@@ -513,12 +609,12 @@ extern "C" int lh_launch_gateup_silu(int lookup, const uint8_t* Wgate, const uin
     float sg, float su, const float* gamma, const float* x, uint32_t count, float* gated,
     hipStream_t s)
 {
-    dim3 grid(LH_INNER / 4, count);
+    dim3 grid(LH_INNER / 8, count);
     float2 scales = make_float2(sg, su);
     if (lookup) {
-        hipLaunchKernelGGL(k_gateup_silu<true>, grid, dim3(192), 0, s, Wgate, Wup, scales, gamma, x, gated);
+        hipLaunchKernelGGL(k_gateup_silu<true>, grid, dim3(256), 0, s, Wgate, Wup, scales, gamma, x, gated);
     } else {
-        hipLaunchKernelGGL(k_gateup_silu<false>, grid, dim3(192), 0, s, Wgate, Wup, scales, gamma, x, gated);
+        hipLaunchKernelGGL(k_gateup_silu<false>, grid, dim3(256), 0, s, Wgate, Wup, scales, gamma, x, gated);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
@@ -526,7 +622,7 @@ extern "C" int lh_launch_gateup_silu(int lookup, const uint8_t* Wgate, const uin
 extern "C" int lh_launch_head(const uint16_t* E, const float* gamma, const float* xrow,
     float* logits, hipStream_t s)
 {
-    hipLaunchKernelGGL(k_head, dim3(LH_VOCAB / 8), dim3(192), 0, s, E, gamma, xrow, logits);
+    hipLaunchKernelGGL(k_head, dim3(LH_VOCAB / 16), dim3(256), 0, s, E, gamma, xrow, logits);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -536,7 +632,6 @@ extern "C" int lh_launch_rmsnorm(const float* gamma, const float* x, float* out,
     if (!width || width > 16 * LH_CHUNK || !tokens) {
         return -1;
     }
-    const uint32_t nch = (width + LH_CHUNK - 1) / LH_CHUNK;
-    hipLaunchKernelGGL(k_rmsnorm, dim3(tokens), dim3(64 * nch), 0, s, gamma, x, out, width);
+    hipLaunchKernelGGL(k_rmsnorm, dim3(tokens), dim3(64), 0, s, gamma, x, out, width);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

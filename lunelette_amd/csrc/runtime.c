@@ -208,8 +208,9 @@ static int stage_push(uploader *up, void *dst, size_t bytes, char *error, size_t
     return 0;
 }
 
-/* FP8 tensor `tensor` of n codes: admit, then store codes (compact) or
- * fl(dec*scale) FP32 (resident, src/safetensors.c:521-548). */
+/* FP8 tensor `tensor` of n codes: admit, then store the codes (compact) or
+ * their exact FP32 decode (resident); both strategies multiply the row total
+ * by the per-tensor scale, so their results are bitwise identical. */
 static int upload_fp8(uploader *up, uint64_t seed, uint32_t tensor, float scale, size_t n,
     bool resident, void *dst, char *error, size_t capacity)
 {
@@ -223,7 +224,7 @@ static int upload_fp8(uploader *up, uint64_t seed, uint32_t tensor, float scale,
     }
     float table[256];
     for (int b = 0; b < 256; b++) {
-        table[b] = fp8_value((unsigned char)b) * scale;
+        table[b] = fp8_value((unsigned char)b);
     }
     const size_t chunk = resident ? STAGE_BYTES / 4 / 2 : STAGE_BYTES / 2;
     uint8_t *codes = malloc(chunk);

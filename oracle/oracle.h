@@ -12,9 +12,10 @@
  *     per-lane squares (:29-44); two-pass softmax and sequential P.V
  *     (:80-132); SiLU v/(1+exp(-v)) (:46-57), libm exp.
  *   - ORC_MIRROR: the exact order of the gfx950 kernels (per-lane FMA chains over
- *     16-column slices of 1024-column chunks, a 64-lane pairwise tree, chunks
- *     summed in order; Cody-Waite exp; split-KV attention combined in a fixed
- *     order). GPU results are compared to it bit for bit.
+ *     the lane's 16-column slice of every 1024-column chunk, one 64-lane
+ *     pairwise tree, the per-tensor scale applied to the row total; Cody-Waite
+ *     exp; split-KV attention combined in a fixed order). GPU results are
+ *     compared to it bit for bit.
  *
  * Parity pins (each function header names its own):
  *   fp8 decode   -- tests/fp8_golden.h (all 256 codes) + oracle/_ref build
@@ -57,8 +58,9 @@ float orc_silu_ref(float v);
 float orc_silu_mirror(float v);
 
 /* ---- kernels ----
- * matvec: y[t*rows + r] = sum_c w(r,c) * x[t*cols + c], w = fl(dec(W)*scale) for
- * FP8, widened BF16, or stored FP32. */
+ * matvec: y[t*rows + r] = scale * sum_c w(r,c) * x[t*cols + c] with w the
+ * decoded FP8 code, widened BF16, or stored FP32. REF applies an FP8 scale per
+ * element (fl(dec*scale)) as the reference does; MIRROR scales the row total. */
 void orc_matvec(int schedule, int kind, const void *weights, float scale,
     const float *x, float *y, size_t rows, size_t cols, size_t tokens);
 void orc_rmsnorm(int schedule, const float *gamma, const float *x, float *out,

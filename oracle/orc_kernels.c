@@ -98,46 +98,43 @@ static float dot_ref(const float *w, const float *x, size_t cols)
     return tree32(sum);
 }
 
-/* Device-mirror row dot: 1024-column chunks; lane l owns columns
- * [16l, 16l+16) of each chunk and runs acc = fma(w, x, acc) from 0 over its
- * valid columns; the 64 lanes reduce by tree64; chunk results are summed in
- * chunk order starting from chunk 0. */
+/* Device-mirror row dot: columns in chunks of 1024; lane l owns columns
+ * [16l, 16l+16) of every chunk and runs acc = fma(w, x, acc) from 0 over all
+ * of them (chunk by chunk, column order); the 64 lane sums reduce by tree64. */
 static float dot_mirror(const float *w, const float *x, size_t cols)
 {
-    float y = 0.0f;
-    for (size_t chunk = 0; chunk * 1024 < cols; chunk++) {
-        size_t base = chunk * 1024;
-        size_t valid = cols - base < 1024 ? cols - base : 1024;
-        float lanes[64];
-        if (valid == 1024) {
-            float acc[64] = {0};
+    float acc[64] = {0};
+    for (size_t base = 0; base < cols; base += 1024) {
+        if (base + 1024 <= cols) {
+            /* 64 independent chains interleaved; each lane's order is kept. */
             for (int j = 0; j < 16; j++) {
                 for (int l = 0; l < 64; l++) {
                     acc[l] = fmaf(w[base + 16 * l + j], x[base + 16 * l + j], acc[l]);
                 }
             }
-            memcpy(lanes, acc, sizeof lanes);
         } else {
             for (int l = 0; l < 64; l++) {
-                float acc = 0.0f;
-                for (size_t j = 16 * (size_t)l; j < 16 * (size_t)l + 16 && j < valid; j++) {
-                    acc = fmaf(w[base + j], x[base + j], acc);
+                size_t first = base + 16 * (size_t)l;
+                for (size_t c = first; c < first + 16 && c < cols; c++) {
+                    acc[l] = fmaf(w[c], x[c], acc[l]);
                 }
-                lanes[l] = acc;
             }
         }
-        float q = tree64(lanes);
-        y = chunk == 0 ? q : y + q;
     }
-    return y;
+    return tree64(acc);
 }
 
+/* REF: per-element w = fl(dec*scale) (weight(), src/metal_kernels.metal:136-144)
+ * then the Kahan lane dot. MIRROR: unscaled exact decode in the dot, the row
+ * total times scale once. BF16 and FP32 weights use scale as given (1 for the
+ * tied head and plain FP32 projections). */
 void orc_matvec(int schedule, int kind, const void *weights, float scale,
     const float *x, float *y, size_t rows, size_t cols, size_t tokens)
 {
     float lut[256];
     for (int b = 0; b < 256; b++) {
-        lut[b] = orc_fp8_decode((uint8_t)b) * scale;
+        lut[b] = schedule == ORC_REF ? orc_fp8_decode((uint8_t)b) * scale :
+            orc_fp8_decode((uint8_t)b);
     }
     #pragma omp parallel
     {
@@ -146,8 +143,12 @@ void orc_matvec(int schedule, int kind, const void *weights, float scale,
         for (size_t r = 0; r < rows; r++) {
             weight_row(kind, weights, lut, r, cols, w);
             for (size_t t = 0; t < tokens; t++) {
-                y[t * rows + r] = schedule == ORC_REF ? dot_ref(w, x + t * cols, cols) :
-                    dot_mirror(w, x + t * cols, cols);
+                if (schedule == ORC_REF) {
+                    float dot = dot_ref(w, x + t * cols, cols);
+                    y[t * rows + r] = kind == ORC_W_FP8 ? dot : dot * scale;
+                } else {
+                    y[t * rows + r] = dot_mirror(w, x + t * cols, cols) * scale;
+                }
             }
         }
         free(w);

@@ -28,12 +28,11 @@ class DeviceLayer:
             self.keep.append(buf)
             setattr(w, name, buf.ptr)
         if resident:
+            # Resident strategy: exact FP32 decode, scale applied per row total.
             dec = decode_table()
-            scales = {"q": host["scale_q"], "k": host["scale_k"], "v": host["scale_v"]}
-            qkv32 = np.concatenate([dec[host[n]] * np.float32(scales[n]) for n in ("q", "k", "v")])
-            mats32 = {"qkv": qkv32}
+            mats32 = {"qkv": dec[qkv]}
             for n in ("o", "gate", "up", "down"):
-                mats32[n] = dec[host[n]] * np.float32(host["scale_" + n])
+                mats32[n] = dec[host[n]]
             for name in names:
                 buf = lh.DeviceBuffer.from_array(mats32[name].astype(np.float32))
                 self.keep.append(buf)
