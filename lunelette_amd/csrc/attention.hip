@@ -2,154 +2,218 @@
 // workgroups by 64-position blocks (src/metal_kernels.metal:80-132 computes the
 // same softmax(q.k/sqrt(128)).V with one SIMD group walking every position).
 //
-//   k_attn_scores : (block, kv_head, token) -> s_p for the 4 query heads that
-//                   share the kv head (K tile staged once in LDS), block max.
-//   k_attn_pv     : global max over block maxima, e_p = exp(s_p - M), block
-//                   sum by the 64-lane tree, block partial A_b[d] = sum e_p v_pd.
-//   k_attn_combine: blocks -> 256-position tiles -> tiles, in order; out = A/T.
+// k_attn_blocks  (block b, kv head, token t): the four query heads sharing the
+//   kv head, over the block's valid positions p:
+//     c_i  = chain over d in [32i, 32i+32) of fma(q_d, k_pd)   (i = 0..3)
+//     s_p  = fl(((c_0 + c_1) + (c_2 + c_3)) * 1/sqrt(128))
+//     m_b  = max_p s_p,  e_p = exp(s_p - m_b),  T_b = 64-lane tree of e,
+//     A_b[d] = chain_p fma(e_p, v_pd)  (from 0, position order).
+// k_attn_combine (head, token): M = max_b m_b, f_b = exp(m_b - M); groups of
+//   8 consecutive blocks chain S_g[d] = fma(f_b, A_b[d], .) and
+//   U_g = fma(f_b, T_b, .) from 0; A = S_0 + S_1 + ..., T = U_0 + U_1 + ...
+//   left to right; out[d] = A[d] / T.
 //
-// KV layout [kv_head][capacity][128] per layer keeps each block's K or V tile
-// one contiguous 32 KiB read. Positions at or beyond length+t+1 are never read
-// into arithmetic.
+// KV layout [kv_head][capacity][128] per layer: a block's K or V tile is one
+// contiguous 32 KiB read. K goes straight to registers (lane = position,
+// quarter of the head dimension), V is staged in LDS for the P.V chains, so a
+// workgroup holds 35 KiB of LDS and four fit on a CU. Rows at or past
+// length+t+1 never enter arithmetic. The combine runs as its own kernel: the
+// kernel boundary publishes the partials device-wide, where an in-kernel
+// hand-off costs an L2 write-back or same-address atomics per workgroup.
 #include "lh_device.h"
 #include "lh_internal.h"
 
 namespace lh {
 
-__global__ void __launch_bounds__(256)
-k_attn_scores(const float* __restrict__ q, const float* __restrict__ kcache,
-    const lh_step_params* __restrict__ params, uint32_t capacity, float* __restrict__ S,
-    float* __restrict__ BM)
-{
-    __shared__ float Kt[LH_ATTN_BLOCK][LH_HEAD_DIM + 1];
-    __shared__ float qs[4][LH_HEAD_DIM];
-    const uint32_t b = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
-    const uint32_t n = params->length + t + 1;
-    if (b * LH_ATTN_BLOCK >= n) {
-        return;
-    }
-    const uint32_t valid = n - b * LH_ATTN_BLOCK < LH_ATTN_BLOCK ? n - b * LH_ATTN_BLOCK : LH_ATTN_BLOCK;
-    const float* kb = kcache + lh_kv_index(capacity, 0, kvh, (uint64_t)b * LH_ATTN_BLOCK);
-    for (uint32_t i = threadIdx.x; i < LH_ATTN_BLOCK * 32; i += 256) {
-        const uint32_t r = i >> 5, c4 = i & 31;
-        if (r < valid) {
-            float4 v = reinterpret_cast<const float4*>(kb + (size_t)r * LH_HEAD_DIM)[c4];
-            Kt[r][4 * c4 + 0] = v.x;
-            Kt[r][4 * c4 + 1] = v.y;
-            Kt[r][4 * c4 + 2] = v.z;
-            Kt[r][4 * c4 + 3] = v.w;
-        }
-    }
-    for (uint32_t i = threadIdx.x; i < 4 * LH_HEAD_DIM; i += 256) {
-        qs[i >> 7][i & 127] = q[(size_t)t * LH_QUERY + kvh * 4 * LH_HEAD_DIM + i];
-    }
-    __syncthreads();
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t h = kvh * 4 + wave;
-    const uint32_t nbc = capacity / LH_ATTN_BLOCK;
-    float s = -__builtin_inff();
-    if (lane < valid) {
-        float acc = 0.0f;
-#pragma unroll 8
-        for (int d = 0; d < LH_HEAD_DIM; d++) {
-            acc = __builtin_fmaf(qs[wave][d], Kt[lane][d], acc);
-        }
-        s = acc * LH_SCORE_SCALE;
-        S[((size_t)t * LH_HEADS + h) * capacity + b * LH_ATTN_BLOCK + lane] = s;
-    }
-    const float m = wave_max64(s);
-    if (lane == 0) {
-        BM[((size_t)t * LH_HEADS + h) * nbc + b] = m;
-    }
-}
+constexpr uint32_t GROUP = 8;     // blocks chained per combine group
+constexpr uint32_t ROUND = 128;   // blocks per combine round (16 groups)
 
 __global__ void __launch_bounds__(256)
-k_attn_pv(const float* __restrict__ S, const float* __restrict__ BM,
+k_attn_blocks(const float* __restrict__ q, const float* __restrict__ kcache,
     const float* __restrict__ vcache, const lh_step_params* __restrict__ params,
-    uint32_t capacity, float* __restrict__ PT, float* __restrict__ PA)
+    uint32_t capacity, float* __restrict__ PM, float* __restrict__ PT, float* __restrict__ PA)
 {
-    __shared__ float Vt[LH_ATTN_BLOCK][LH_HEAD_DIM];
-    __shared__ float es[4][LH_ATTN_BLOCK];
+    __shared__ float4 Vt[LH_ATTN_BLOCK][LH_HEAD_DIM / 4];
+    __shared__ float4 qs[4][LH_HEAD_DIM / 4];
+    __shared__ float S[4][LH_ATTN_BLOCK];
     const uint32_t b = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
+    const uint64_t tile = lh_kv_index(capacity, 0, kvh, (uint64_t)b * LH_ATTN_BLOCK);
+    const float4* kb = reinterpret_cast<const float4*>(kcache + tile);
+    const float4* vb = reinterpret_cast<const float4*>(vcache + tile);
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    // The tile loads do not wait for the step record: the launch grid covers
+    // ceil((length + count) / 64) blocks of a capacity that is a multiple of
+    // 64, so all 64 rows are in bounds; rows past the valid count are never
+    // used in arithmetic.
+    // K: wave w covers positions 16w..16w+15; lane = 4 * (position - 16w) + quarter.
+    const uint32_t p = 16 * wave + (lane >> 2), quarter = lane & 3;
+    float4 k[8];
+    const float4* krow = kb + (size_t)p * (LH_HEAD_DIM / 4) + 8 * quarter;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        k[i] = krow[i];
+    }
+    float4 vr[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        vr[i] = vb[tid + 256 * i];   // row (tid + 256 i) >> 5, float4 column tid & 31
+    }
     const uint32_t n = params->length + t + 1;
     if (b * LH_ATTN_BLOCK >= n) {
         return;
     }
-    const uint32_t valid = n - b * LH_ATTN_BLOCK < LH_ATTN_BLOCK ? n - b * LH_ATTN_BLOCK : LH_ATTN_BLOCK;
-    const uint32_t nb = (n + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
     const uint32_t nbc = capacity / LH_ATTN_BLOCK;
-    const float* vb = vcache + lh_kv_index(capacity, 0, kvh, (uint64_t)b * LH_ATTN_BLOCK);
-    for (uint32_t i = threadIdx.x; i < LH_ATTN_BLOCK * 32; i += 256) {
-        const uint32_t r = i >> 5, c4 = i & 31;
-        if (r < valid) {
-            reinterpret_cast<float4*>(&Vt[r][0])[c4] =
-                reinterpret_cast<const float4*>(vb + (size_t)r * LH_HEAD_DIM)[c4];
-        }
+    const uint32_t rest = n - b * LH_ATTN_BLOCK;
+    const uint32_t valid = rest < LH_ATTN_BLOCK ? rest : LH_ATTN_BLOCK;
+    if (tid < 128) {
+        reinterpret_cast<float4*>(qs)[tid] = reinterpret_cast<const float4*>(
+            q + (size_t)t * LH_QUERY + kvh * 4 * LH_HEAD_DIM)[tid];
     }
-    const uint32_t lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t h = kvh * 4 + wave;
-    const size_t th = (size_t)t * LH_HEADS + h;
-    float m = -__builtin_inff();
-    for (uint32_t j = lane; j < nb; j += 64) {
-        m = fmaxf(m, BM[th * nbc + j]);
-    }
-    m = wave_max64(m);
-    float e = 0.0f;
-    if (lane < valid) {
-        e = expf_cw(S[th * capacity + b * LH_ATTN_BLOCK + lane] - m);
-    }
-    es[wave][lane] = e;
-    const float total = wave_tree64(e);
-    if (lane == 0) {
-        PT[th * nbc + b] = total;
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        reinterpret_cast<float4*>(Vt)[tid + 256 * i] = vr[i];
     }
     __syncthreads();
-    float a0 = 0.0f, a1 = 0.0f;
+    float c[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+#pragma unroll
+        for (int hh = 0; hh < 4; hh++) {
+            const float4 qq = qs[hh][8 * quarter + i];
+            c[hh] = __builtin_fmaf(qq.x, k[i].x, c[hh]);
+            c[hh] = __builtin_fmaf(qq.y, k[i].y, c[hh]);
+            c[hh] = __builtin_fmaf(qq.z, k[i].z, c[hh]);
+            c[hh] = __builtin_fmaf(qq.w, k[i].w, c[hh]);
+        }
+    }
+#pragma unroll
+    for (int hh = 0; hh < 4; hh++) {
+        // (c0 + c1) + (c2 + c3); IEEE addition is commutative, so every lane of
+        // the quad ends with the same bits.
+        float v = c[hh] + __shfl_xor(c[hh], 1, 64);
+        v = v + __shfl_xor(v, 2, 64);
+        if (quarter == 0 && p < valid) {
+            S[hh][p] = v * LH_SCORE_SCALE;
+        }
+    }
+    __syncthreads();
+    // Wave w = head kvh*4 + w from here on; lane = position.
+    const float s = lane < valid ? S[wave][lane] : -__builtin_inff();
+    const float m = wave_max64(s);
+    const float e = lane < valid ? expf_cw(s - m) : 0.0f;
+    const float total = wave_tree64(e);
+    __syncthreads();
+    S[wave][lane] = e;
+    __syncthreads();
     const uint32_t d0 = 2 * lane;
+    float a0 = 0.0f, a1 = 0.0f;
+    const float* vt = reinterpret_cast<const float*>(Vt) + d0;
     for (uint32_t j = 0; j < valid; j++) {
-        const float ej = es[wave][j];
-        const float2 v = *reinterpret_cast<const float2*>(&Vt[j][d0]);
+        const float ej = S[wave][j];
+        const float2 v = *reinterpret_cast<const float2*>(vt + j * LH_HEAD_DIM);
         a0 = __builtin_fmaf(ej, v.x, a0);
         a1 = __builtin_fmaf(ej, v.y, a1);
     }
-    float2* pa = reinterpret_cast<float2*>(PA + (th * nbc + b) * LH_HEAD_DIM + d0);
-    *pa = make_float2(a0, a1);
+    const size_t th = (size_t)t * LH_HEADS + kvh * 4 + wave;
+    if (lane == 0) {
+        PM[th * nbc + b] = m;
+        PT[th * nbc + b] = total;
+    }
+    *reinterpret_cast<float2*>(PA + (th * nbc + b) * LH_HEAD_DIM + d0) = make_float2(a0, a1);
 }
 
-// grid (32 heads, count), block 64.
-__global__ void __launch_bounds__(64)
-k_attn_combine(const float* __restrict__ PT, const float* __restrict__ PA,
-    const lh_step_params* __restrict__ params, uint32_t capacity, float* __restrict__ out)
+// grid (32 heads, count), 256 threads: thread (c = tid & 31, s = tid >> 5)
+// owns dims 4c..4c+3 of groups s and s + 8 of each 128-block round.
+__global__ void __launch_bounds__(256)
+k_attn_combine(const float* __restrict__ PM, const float* __restrict__ PT,
+    const float* __restrict__ PA, const lh_step_params* __restrict__ params, uint32_t capacity,
+    float* __restrict__ out)
 {
+    __shared__ float wmax[4];
+    __shared__ float fs[ROUND], ts[ROUND];
+    __shared__ float4 sg[ROUND / GROUP][LH_HEAD_DIM / 4];
+    __shared__ float ug[ROUND / GROUP];
     const uint32_t h = blockIdx.x, t = blockIdx.y;
     const uint32_t n = params->length + t + 1;
     const uint32_t nb = (n + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
     const uint32_t nbc = capacity / LH_ATTN_BLOCK;
     const size_t th = (size_t)t * LH_HEADS + h;
-    const uint32_t d0 = 2 * threadIdx.x;
-    float T = 0.0f, A0 = 0.0f, A1 = 0.0f;
-    for (uint32_t tile = 0; tile * LH_ATTN_TILE < nb; tile++) {
-        const uint32_t b0 = tile * LH_ATTN_TILE;
-        float tT = PT[th * nbc + b0];
-        float2 tA = *reinterpret_cast<const float2*>(PA + (th * nbc + b0) * LH_HEAD_DIM + d0);
-        for (uint32_t b = b0 + 1; b < b0 + LH_ATTN_TILE && b < nb; b++) {
-            const float2 a = *reinterpret_cast<const float2*>(PA + (th * nbc + b) * LH_HEAD_DIM + d0);
-            tT = tT + PT[th * nbc + b];
-            tA.x = tA.x + a.x;
-            tA.y = tA.y + a.y;
-        }
-        if (tile == 0) {
-            T = tT;
-            A0 = tA.x;
-            A1 = tA.y;
-        } else {
-            T = T + tT;
-            A0 = A0 + tA.x;
-            A1 = A1 + tA.y;
-        }
+    const float* pm = PM + th * nbc;
+    const float* pt = PT + th * nbc;
+    const float4* pa = reinterpret_cast<const float4*>(PA + th * nbc * LH_HEAD_DIM);
+    const uint32_t tid = threadIdx.x, c = tid & 31, s = tid >> 5;
+    float M = -__builtin_inff();
+    for (uint32_t j = tid; j < nb; j += 256) {
+        M = fmaxf(M, pm[j]);
     }
-    float2* o = reinterpret_cast<float2*>(out + (size_t)t * LH_QUERY + h * LH_HEAD_DIM + d0);
-    *o = make_float2(A0 / T, A1 / T);
+    M = wave_max64(M);
+    if ((tid & 63) == 0) {
+        wmax[tid >> 6] = M;
+    }
+    __syncthreads();
+    M = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
+    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+    float T = 0.0f;
+    for (uint32_t r0 = 0; r0 < nb; r0 += ROUND) {
+        // Every load of the round issues before the first wait (clamped rows).
+        float4 a[2][GROUP];
+#pragma unroll
+        for (int gi = 0; gi < 2; gi++) {
+#pragma unroll
+            for (uint32_t k = 0; k < GROUP; k++) {
+                const uint32_t bb = r0 + (s + 8 * gi) * GROUP + k;
+                a[gi][k] = pa[(size_t)(bb < nb ? bb : nb - 1) * (LH_HEAD_DIM / 4) + c];
+            }
+        }
+        if (tid < ROUND) {
+            const uint32_t bb = r0 + tid;
+            fs[tid] = bb < nb ? expf_cw(pm[bb] - M) : 0.0f;
+            ts[tid] = bb < nb ? pt[bb] : 0.0f;
+        }
+        __syncthreads();
+#pragma unroll
+        for (int gi = 0; gi < 2; gi++) {
+            const uint32_t g = s + 8 * gi;
+            float4 Sg = make_float4(0.f, 0.f, 0.f, 0.f);
+            float Ug = 0.0f;
+#pragma unroll
+            for (uint32_t k = 0; k < GROUP; k++) {
+                if (r0 + g * GROUP + k < nb) {
+                    const float f = fs[g * GROUP + k];
+                    Sg.x = __builtin_fmaf(f, a[gi][k].x, Sg.x);
+                    Sg.y = __builtin_fmaf(f, a[gi][k].y, Sg.y);
+                    Sg.z = __builtin_fmaf(f, a[gi][k].z, Sg.z);
+                    Sg.w = __builtin_fmaf(f, a[gi][k].w, Sg.w);
+                    Ug = __builtin_fmaf(f, ts[g * GROUP + k], Ug);
+                }
+            }
+            sg[g][c] = Sg;
+            if (c == 0) {
+                ug[g] = Ug;
+            }
+        }
+        __syncthreads();
+        if (tid < 32) {
+            for (uint32_t g = 0; g < ROUND / GROUP && r0 + g * GROUP < nb; g++) {
+                const float4 v = sg[g][c];
+                if (r0 == 0 && g == 0) {
+                    A = v;
+                    T = ug[0];
+                } else {
+                    A.x = A.x + v.x;
+                    A.y = A.y + v.y;
+                    A.z = A.z + v.z;
+                    A.w = A.w + v.w;
+                    T = T + ug[g];
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (tid < 32) {
+        reinterpret_cast<float4*>(out + (size_t)t * LH_QUERY + h * LH_HEAD_DIM)[c] =
+            make_float4(A.x / T, A.y / T, A.z / T, A.w / T);
+    }
 }
 
 // Embedding gather with exact BF16 widening (src/metal_runtime.m:388-395 copies
@@ -169,21 +233,31 @@ k_embed(const uint16_t* __restrict__ E, const lh_step_params* __restrict__ param
 
 using namespace lh;
 
+// The kernels read the step length from params (device memory, so a captured
+// graph replays with new lengths); `length` here must equal params->length and
+// only sizes the block grid.
 extern "C" int lh_launch_attention(const float* q, const float* kcache_layer,
-    const float* vcache_layer, const lh_step_params* params, uint32_t count,
-    uint32_t max_positions, uint32_t capacity, float* S, float* BM, float* PT, float* PA,
-    float* out, hipStream_t s)
+    const float* vcache_layer, const lh_step_params* params, uint32_t length, uint32_t count,
+    uint32_t capacity, float* PM, float* PT, float* PA, float* out, hipStream_t s)
 {
-    if (!count || capacity % LH_ATTN_BLOCK || max_positions > capacity || !max_positions) {
+    if (!count || capacity % LH_ATTN_BLOCK || length + count > capacity) {
         return -1;
     }
-    const uint32_t blocks = (max_positions + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
-    dim3 grid(blocks, LH_KV_HEADS, count);
-    hipLaunchKernelGGL(k_attn_scores, grid, dim3(256), 0, s, q, kcache_layer, params, capacity, S, BM);
-    hipLaunchKernelGGL(k_attn_pv, grid, dim3(256), 0, s, S, BM, vcache_layer, params, capacity, PT, PA);
-    hipLaunchKernelGGL(k_attn_combine, dim3(LH_HEADS, count), dim3(64), 0, s, PT, PA, params,
+    hipLaunchKernelGGL(k_attn_blocks, dim3(lh_attention_blocks(length, count), LH_KV_HEADS, count),
+        dim3(256), 0, s, q, kcache_layer, vcache_layer, params, capacity, PM, PT, PA);
+    hipLaunchKernelGGL(k_attn_combine, dim3(LH_HEADS, count), dim3(256), 0, s, PM, PT, PA, params,
         capacity, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" uint32_t lh_attention_blocks(uint32_t length, uint32_t count)
+{
+    return (length + count + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
+}
+
+extern "C" const void* lh_attention_blocks_kernel(void)
+{
+    return reinterpret_cast<const void*>(&k_attn_blocks);
 }
 
 extern "C" int lh_launch_embed(const uint16_t* E, const lh_step_params* params, uint32_t count,

@@ -54,8 +54,7 @@ lh_workspace *lh_workspace_create(size_t capacity, size_t block)
         alloc_device((void **)&ws->d_qraw, B * LH_QUERY * sizeof(float), &ws->bytes) ||
         alloc_device((void **)&ws->d_kraw, B * LH_KV * sizeof(float), &ws->bytes) ||
         alloc_device((void **)&ws->d_vraw, B * LH_KV * sizeof(float), &ws->bytes) ||
-        alloc_device((void **)&ws->d_S, B * LH_HEADS * capacity * sizeof(float), &ws->bytes) ||
-        alloc_device((void **)&ws->d_BM, B * LH_HEADS * nbc * sizeof(float), &ws->bytes) ||
+        alloc_device((void **)&ws->d_PM, B * LH_HEADS * nbc * sizeof(float), &ws->bytes) ||
         alloc_device((void **)&ws->d_PT, B * LH_HEADS * nbc * sizeof(float), &ws->bytes) ||
         alloc_device((void **)&ws->d_PA, B * LH_HEADS * nbc * LH_HEAD_DIM * sizeof(float),
             &ws->bytes)) {
@@ -72,8 +71,8 @@ void lh_workspace_destroy(lh_workspace *ws)
         return;
     }
     void *device[] = {ws->d_params, ws->d_q, ws->d_attn, ws->d_gated, ws->d_up, ws->d_xn,
-        ws->d_qraw, ws->d_kraw, ws->d_vraw, ws->d_S, ws->d_BM, ws->d_PT, ws->d_PA, ws->d_split,
-        ws->d_gemm};
+        ws->d_qraw, ws->d_kraw, ws->d_vraw, ws->d_PM, ws->d_PT, ws->d_PA,
+        ws->d_split, ws->d_gemm};
     for (size_t i = 0; i < sizeof device / sizeof device[0]; i++) {
         if (device[i]) {
             (void)hipFree(device[i]);
@@ -163,8 +162,8 @@ static int layer_unfused(const lh_layer_weights *w, float *x, float *keys, float
             LH_KV, LH_HIDDEN, n, s), "v") ||
         launched(lh_launch_rope_append(ws->d_qraw, ws->d_kraw, ws->d_vraw, params, n, ws->d_q,
             keys, values, C, s), "rope/append") ||
-        launched(lh_launch_attention(ws->d_q, keys, values, params, n,
-            (uint32_t)(ws->length + n), C, ws->d_S, ws->d_BM, ws->d_PT, ws->d_PA, ws->d_attn, s),
+        launched(lh_launch_attention(ws->d_q, keys, values, ws->d_params, (uint32_t)ws->length, n,
+            C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_attn, s),
             "attention") ||
         launched(lh_launch_matvec(kind, 0, wo, w->scale[3], ws->d_attn, x, x, LH_HIDDEN,
             LH_QUERY, n, s), "o") ||
@@ -189,8 +188,8 @@ static int layer_fused(const lh_layer_weights *w, float *x, float *keys, float *
     const lh_step_params *params = ws->d_params;
     if (launched(lh_launch_qkv_rope(lookup, w->qkv, w->scale[0], w->scale[1], w->scale[2],
             w->input_norm, x, params, n, ws->d_q, keys, values, C, s), "qkv") ||
-        launched(lh_launch_attention(ws->d_q, keys, values, params, n,
-            (uint32_t)(ws->length + n), C, ws->d_S, ws->d_BM, ws->d_PT, ws->d_PA, ws->d_attn, s),
+        launched(lh_launch_attention(ws->d_q, keys, values, ws->d_params, (uint32_t)ws->length, n,
+            C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_attn, s),
             "attention") ||
         launched(lh_launch_matvec(0, lookup, w->o, w->scale[3], ws->d_attn, x, x, LH_HIDDEN,
             LH_QUERY, n, s), "o") ||
@@ -217,8 +216,8 @@ int lh_layer_operator(int op, const lh_layer_weights *w, float *d_x, float *d_ke
         return launched(lh_launch_qkv_rope(0, w->qkv, w->scale[0], w->scale[1], w->scale[2],
             w->input_norm, d_x, ws->d_params, n, ws->d_q, d_keys, d_values, C, s), "qkv");
     case LH_OP_ATTENTION:
-        return launched(lh_launch_attention(ws->d_q, d_keys, d_values, ws->d_params, n,
-            (uint32_t)(ws->length + n), C, ws->d_S, ws->d_BM, ws->d_PT, ws->d_PA, ws->d_attn, s),
+        return launched(lh_launch_attention(ws->d_q, d_keys, d_values, ws->d_params, (uint32_t)ws->length, n,
+            C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_attn, s),
             "attention");
     case LH_OP_O_RESIDUAL:
         return launched(lh_launch_matvec(0, 0, w->o, w->scale[3], ws->d_attn, d_x, d_x, LH_HIDDEN,
@@ -271,9 +270,9 @@ int lh_attention(const float *d_q, const float *d_keys, const float *d_values, l
         lh_set_error("attention: missing argument or tokens not set");
         return -1;
     }
-    return launched(lh_launch_attention(d_q, d_keys, d_values, ws->d_params, (uint32_t)ws->count,
-        (uint32_t)(ws->length + ws->count), (uint32_t)ws->capacity, ws->d_S, ws->d_BM, ws->d_PT,
-        ws->d_PA, d_out, (hipStream_t)stream), "attention");
+    return launched(lh_launch_attention(d_q, d_keys, d_values, ws->d_params,
+        (uint32_t)ws->length, (uint32_t)ws->count, (uint32_t)ws->capacity, ws->d_PM, ws->d_PT, ws->d_PA,
+        d_out, (hipStream_t)stream), "attention");
 }
 
 int lh_head_forward(const uint16_t *d_embedding, const float *d_gamma, const float *d_xrow,

@@ -25,9 +25,14 @@ int lh_launch_head(const uint16_t *E, const float *gamma, const float *xrow, flo
     hipStream_t s);
 int lh_launch_rmsnorm(const float *gamma, const float *x, float *out, uint32_t width,
     uint32_t tokens, hipStream_t s);
+/* Query token t attends positions [0, params->length + t]; length (equal to
+ * params->length) sizes the block grid only. */
 int lh_launch_attention(const float *q, const float *kcache_layer, const float *vcache_layer,
-    const lh_step_params *params, uint32_t count, uint32_t max_positions, uint32_t capacity,
-    float *S, float *BM, float *PT, float *PA, float *out, hipStream_t s);
+    const lh_step_params *params, uint32_t length, uint32_t count, uint32_t capacity, float *PM,
+    float *PT, float *PA, float *out, hipStream_t s);
+/* Block-grid width of the attention kernel, and its function (graph updates). */
+uint32_t lh_attention_blocks(uint32_t length, uint32_t count);
+const void *lh_attention_blocks_kernel(void);
 int lh_launch_embed(const uint16_t *E, const lh_step_params *params, uint32_t count, float *x,
     hipStream_t s);
 int lh_launch_element(int mode, const float *a, const float *b, float *out, size_t n,

@@ -19,9 +19,8 @@ struct lh_workspace {
     float *d_gated, *d_up;         /* [B][9216] */
     float *d_xn;                   /* [B][3072] */
     float *d_qraw, *d_kraw, *d_vraw;
-    float *d_S;                    /* [B][32][C] scores */
-    float *d_BM, *d_PT;            /* [B][32][C/64] */
-    float *d_PA;                   /* [B][32][C/64][128] */
+    float *d_PM, *d_PT;            /* [B][32][C/64] block maxima and sums */
+    float *d_PA;                   /* [B][32][C/64][128] block P.V partials */
     /* MFMA path: BF16 hi/mid/lo splits of the GEMM inputs, [3][B][K]. */
     uint16_t *d_split;
     float *d_gemm;                 /* [B][18432] GEMM outputs */

@@ -11,11 +11,13 @@
  *              (head) or the stored FP32 decode (resident strategy).
  *   RMSNorm  : ss by the row-dot schedule with w = x; r = 1/sqrt(ss/n + 1e-5);
  *              out = gamma * (x * r).
- *   attention: per (token, head) s_p = fl(chain_d fma(q_d, k_pd) * 1/sqrt(128));
- *              M = max s_p; e_p = expf_cw(s_p - M); per 64-position block the
- *              e_p reduce by the 64-lane tree and A_b[d] chains fma(e_p, v_pd)
- *              over the block's valid positions; blocks chain into 256-position
- *              tiles, tiles chain in order; out = A / T.
+ *   attention: per (token, head) c_i = chain over d in [32i, 32i+32) of
+ *              fma(q_d, k_pd); s_p = fl(((c_0 + c_1) + (c_2 + c_3)) * 2^-3.5);
+ *              per 64-position block b: m_b = max s_p, e_p = expf_cw(s_p - m_b),
+ *              T_b = 64-lane tree of e, A_b[d] chains fma(e_p, v_pd) over the
+ *              block's valid positions; M = max m_b, f_b = expf_cw(m_b - M);
+ *              groups of 8 blocks chain fma(f_b, A_b[d]) and fma(f_b, T_b)
+ *              from 0; group results add left to right; out = A / T.
  */
 #ifndef LH_SCHEDULE_H
 #define LH_SCHEDULE_H
@@ -36,7 +38,6 @@
 #define LH_CHUNK 1024      /* columns per canonical chunk */
 #define LH_LANE_COLS 16    /* columns per lane per chunk */
 #define LH_ATTN_BLOCK 64   /* positions per attention block */
-#define LH_ATTN_TILE 4     /* blocks per tile in the combine */
 #define LH_MAX_BLOCK 256   /* largest executed block (B) */
 
 #define LH_SCORE_SCALE 0.08838834764831845f

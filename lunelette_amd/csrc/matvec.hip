@@ -127,110 +127,72 @@ __device__ __forceinline__ void fill_lut(float* lut)
     }
 }
 
-// Canonical RMSNorm of the lane's NCH x 16 values held in xs (row width
-// NCH*1024): ss by the row-dot schedule with w = x, r = 1/sqrt(ss/n + 1e-5),
-// xs = gamma * (xs * r). Wave-local; every lane ends with the same r.
-template <int NCH>
-__device__ __forceinline__ void rmsnorm_wave(float (&xs)[NCH][16], const float* gamma)
+// Workgroup-shared input row in LDS, laid out [chunk][quad][lane] as 16-byte
+// words: lane l's 16 values of chunk c (columns c*1024 + 16l .. +15) are the
+// words (4c + q)*64 + l, q = 0..3, so a wave reads a chunk with four
+// conflict-free 16-byte loads. Staging is split around the weight loads:
+// stage_load issues the row (and gamma) loads first, since vector loads retire
+// in issue order; stage_commit writes LDS and, with gamma, has wave 0 apply the
+// canonical RMSNorm in place: ss by the row-dot schedule with w = x,
+// r = 1/sqrt(ss/n + 1e-5), x = gamma * (x * r).
+__device__ __forceinline__ uint32_t staged_word(int i, uint32_t tid)
 {
-    const int lane = threadIdx.x & 63;
-    float acc = 0.0f;
-#pragma unroll
-    for (int c = 0; c < NCH; c++) {
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-            acc = __builtin_fmaf(xs[c][j], xs[c][j], acc);
-        }
-    }
-    const float ss = wave_lane0(wave_tree64(acc));
-    const float r = 1.0f / __builtin_sqrtf(ss / (float)(NCH * LH_CHUNK) + 1e-5f);
-#pragma unroll
-    for (int c = 0; c < NCH; c++) {
-        float g[16];
-        load_x16(gamma + c * LH_CHUNK + lane * LH_LANE_COLS, g);
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-            xs[c][j] = g[j] * (xs[c][j] * r);
-        }
-    }
+    // float4 index tid + 256*i of the row is chunk i, lane tid/4, quad tid%4
+    return (4 * i + (tid & 3)) * 64 + (tid >> 2);
 }
 
-template <int NCH>
-__device__ __forceinline__ void load_row_slices(const float* row, float (&xs)[NCH][16])
+template <int NCH, bool NORM>
+__device__ __forceinline__ void stage_load(const float* row, const float* gamma, float4 (&xv)[NCH],
+    float4 (&gv)[NCH])
 {
-    const int lane = threadIdx.x & 63;
+    const uint32_t tid = threadIdx.x;
 #pragma unroll
-    for (int c = 0; c < NCH; c++) {
-        load_x16(row + c * LH_CHUNK + lane * LH_LANE_COLS, xs[c]);
+    for (int i = 0; i < NCH; i++) {
+        xv[i] = reinterpret_cast<const float4*>(row)[tid + 256 * i];
     }
-}
-
-// Workgroup-shared input slices, in two phases around the weight loads.
-// Phase 1 (wave 0): load the lane slices of the input row and of gamma. Vector
-// loads retire in issue order, so these must precede the weight loads or the
-// normalization would wait for the weights too.
-template <int NCH>
-__device__ __forceinline__ void wg_input_load(const float* row, const float* gamma,
-    float (&xs)[NCH][16], float (&gs)[NCH][16])
-{
-    if ((threadIdx.x >> 6) == 0) {
-        load_row_slices<NCH>(row, xs);
-        if (gamma) {
-            load_row_slices<NCH>(gamma, gs);
+    if constexpr (NORM) {
+#pragma unroll
+        for (int i = 0; i < NCH; i++) {
+            gv[i] = reinterpret_cast<const float4*>(gamma)[tid + 256 * i];
         }
     }
 }
 
-// Phase 2: wave 0 RMS-normalizes (when gamma is given) and publishes through
-// LDS laid out [chunk][quad][lane] (16-byte words, conflict-free); every wave
-// reads its copy back.
-template <int NCH>
-__device__ __forceinline__ void wg_input_publish(bool norm, float (&xs)[NCH][16],
-    const float (&gs)[NCH][16], float4* lds)
+template <int NCH, bool NORM>
+__device__ __forceinline__ void stage_commit(const float4 (&xv)[NCH], const float4 (&gv)[NCH],
+    float4* xl, float4* gl)
 {
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    if (wave == 0) {
-        if (norm) {
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+#pragma unroll
+    for (int i = 0; i < NCH; i++) {
+        xl[staged_word(i, tid)] = xv[i];
+        if constexpr (NORM) {
+            gl[staged_word(i, tid)] = gv[i];
+        }
+    }
+    __syncthreads();
+    if constexpr (NORM) {
+        if ((tid >> 6) == 0) {
             float acc = 0.0f;
 #pragma unroll
-            for (int c = 0; c < NCH; c++) {
-#pragma unroll
-                for (int j = 0; j < 16; j++) {
-                    acc = __builtin_fmaf(xs[c][j], xs[c][j], acc);
-                }
+            for (int w = 0; w < NCH * 4; w++) {
+                const float4 v = xl[w * 64 + lane];
+                acc = __builtin_fmaf(v.x, v.x, acc);
+                acc = __builtin_fmaf(v.y, v.y, acc);
+                acc = __builtin_fmaf(v.z, v.z, acc);
+                acc = __builtin_fmaf(v.w, v.w, acc);
             }
             const float ss = wave_lane0(wave_tree64(acc));
             const float r = 1.0f / __builtin_sqrtf(ss / (float)(NCH * LH_CHUNK) + 1e-5f);
 #pragma unroll
-            for (int c = 0; c < NCH; c++) {
-#pragma unroll
-                for (int j = 0; j < 16; j++) {
-                    xs[c][j] = gs[c][j] * (xs[c][j] * r);
-                }
+            for (int w = 0; w < NCH * 4; w++) {
+                const float4 v = xl[w * 64 + lane];
+                const float4 g = gl[w * 64 + lane];
+                xl[w * 64 + lane] = make_float4(g.x * (v.x * r), g.y * (v.y * r),
+                    g.z * (v.z * r), g.w * (v.w * r));
             }
         }
-#pragma unroll
-        for (int c = 0; c < NCH; c++) {
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                lds[(c * 4 + q) * 64 + lane] =
-                    make_float4(xs[c][4 * q], xs[c][4 * q + 1], xs[c][4 * q + 2], xs[c][4 * q + 3]);
-            }
-        }
-    }
-    __syncthreads();
-    if (wave != 0) {
-#pragma unroll
-        for (int c = 0; c < NCH; c++) {
-#pragma unroll
-            for (int q = 0; q < 4; q++) {
-                const float4 v = lds[(c * 4 + q) * 64 + lane];
-                xs[c][4 * q] = v.x;
-                xs[c][4 * q + 1] = v.y;
-                xs[c][4 * q + 2] = v.z;
-                xs[c][4 * q + 3] = v.w;
-            }
-        }
+        __syncthreads();
     }
 }
 
@@ -252,14 +214,15 @@ __device__ __forceinline__ void issue_rows(const void* W, const uint32_t (&rows)
     }
 }
 
-// R canonical dots (unscaled) of the issued rows against the lane's x
-// slices; lane 0 holds the wave totals. The R chains are interleaved element
-// by element (each row's own order is unchanged) for instruction-level
+// R canonical dots (unscaled) of the issued rows against the staged input
+// row; lane 0 holds the wave totals. The R chains are interleaved element by
+// element (each row's own order is unchanged) for instruction-level
 // parallelism.
 template <int KIND, bool LUT, int NCH, int R>
-__device__ __forceinline__ void dot_rows(const WVec<KIND> (&wv)[R][NCH],
-    const float (&xs)[NCH][16], const float* lut, float (&out)[R])
+__device__ __forceinline__ void dot_rows(const WVec<KIND> (&wv)[R][NCH], const float4* xl,
+    const float* lut, float (&out)[R])
 {
+    const uint32_t lane = threadIdx.x & 63;
     float acc[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -267,9 +230,18 @@ __device__ __forceinline__ void dot_rows(const WVec<KIND> (&wv)[R][NCH],
     }
 #pragma unroll
     for (int c = 0; c < NCH; c++) {
+        float xs[16];
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+            const float4 v = xl[(c * 4 + q) * 64 + lane];
+            xs[4 * q] = v.x;
+            xs[4 * q + 1] = v.y;
+            xs[4 * q + 2] = v.z;
+            xs[4 * q + 3] = v.w;
+        }
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            acc[r] = chain16<KIND, LUT>(wv[r][c], xs[c], lut, acc[r]);
+            acc[r] = chain16<KIND, LUT>(wv[r][c], xs, lut, acc[r]);
         }
     }
 #pragma unroll
@@ -287,26 +259,25 @@ k_rows(const void* __restrict__ W, float scale, const float* __restrict__ x, flo
     const float* residual, uint32_t rows)
 {
     __shared__ float lut_s[LUT ? 256 : 1];
+    __shared__ float4 xin_s[NCH * 4 * 64];
     if constexpr (LUT) {
         fill_lut(lut_s);
-        __syncthreads();
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t t = blockIdx.y;
     const uint32_t row0 = (blockIdx.x * 4 + wave) * R;
+    float4 xv[NCH], gv[NCH];
+    stage_load<NCH, false>(x + (size_t)t * NCH * LH_CHUNK, nullptr, xv, gv);
     uint32_t rr[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
         rr[r] = row0 + r;
     }
-    __shared__ float4 xin_s[NCH * 4 * 64];
-    float xs[NCH][16], gs[NCH][16];
-    wg_input_load<NCH>(x + (size_t)t * NCH * LH_CHUNK, nullptr, xs, gs);
     WVec<KIND> wv[R][NCH];
     issue_rows<KIND, NCH, R>(W, rr, wv);
-    wg_input_publish<NCH>(false, xs, gs, xin_s);
+    stage_commit<NCH, false>(xv, gv, xin_s, nullptr);
     float dots[R];
-    dot_rows<KIND, LUT, NCH, R>(wv, xs, lut_s, dots);
+    dot_rows<KIND, LUT, NCH, R>(wv, xin_s, lut_s, dots);
     if (lane == 0) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
@@ -363,9 +334,10 @@ k_rows_generic(const void* __restrict__ W, float scale, const float* __restrict_
 
 // ---------------------------------------------------------------------------
 // RMSNorm -> q|k|v -> RoPE (+ query factor on Q) -> Q scratch and KV append
-// (src/metal_encode.m:129-153). Wave g owns RoPE pairs i, i+1 (i = 2*(g%32))
-// of head g/32 (48 heads: 32 q, 8 k, 8 v): rows head*128 + {i, i+1} and + 64.
-// grid (48*32/4, count), block 256.
+// (src/metal_encode.m:129-153). The 48 heads (32 q, 8 k, 8 v) hold 64 RoPE
+// pairs each, rows head*128 + i and + 64; wave g (of 1024) owns the pairs
+// P = 3g, 3g+1, 3g+2 (head P/64, i = P%64), so every SIMD gets six rows.
+// grid (1024/4, count), block 256.
 template <bool LUT>
 __global__ void __launch_bounds__(256)
 k_qkv_rope(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restrict__ gamma,
@@ -381,52 +353,58 @@ k_qkv_rope(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restr
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t t = blockIdx.y;
     const uint32_t g = blockIdx.x * 4 + wave;
-    const uint32_t head = g >> 5, i0 = 2 * (g & 31);
-    const uint32_t base = head * 128 + i0;
-    const uint32_t rr[4] = {base, base + 1, base + 64, base + 65};
-    __shared__ float4 xin_s[3 * 4 * 64];
-    float xs[3][16], gs[3][16];
-    wg_input_load<3>(xin + (size_t)t * LH_HIDDEN, gamma, xs, gs);
-    WVec<K_FP8> wv[4][3];
-    issue_rows<K_FP8, 3, 4>(Wqkv, rr, wv);
-    wg_input_publish<3>(true, xs, gs, xin_s);
-    float dots[4];
-    dot_rows<K_FP8, LUT, 3, 4>(wv, xs, lut_s, dots);
-    const float scale = head < 32 ? scales.x : (head < 40 ? scales.y : scales.z);
+    uint32_t heads[3], is[3], rr[6];
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+        const uint32_t pair = 3 * g + j;
+        heads[j] = pair >> 6;
+        is[j] = pair & 63;
+        rr[j] = heads[j] * 128 + is[j];
+        rr[3 + j] = rr[j] + 64;
+    }
+    __shared__ float4 xin_s[3 * 4 * 64], gam_s[3 * 4 * 64];
+    float4 xv[3], gv[3];
+    stage_load<3, true>(xin + (size_t)t * LH_HIDDEN, gamma, xv, gv);
+    WVec<K_FP8> wv[6][3];
+    issue_rows<K_FP8, 3, 6>(Wqkv, rr, wv);
+    stage_commit<3, true>(xv, gv, xin_s, gam_s);
+    float dots[6];
+    dot_rows<K_FP8, LUT, 3, 6>(wv, xin_s, lut_s, dots);
     const lh_token_params* tp = &params->tokens[t];
     const uint32_t position = params->length + t;
     if (lane == 0) {
 #pragma unroll
-        for (int p = 0; p < 2; p++) {
-        const uint32_t i = i0 + p;
-        const float lo = dots[p] * scale;
-        const float hi = dots[2 + p] * scale;
-        if (head < 40) {
-            // column i < 64 rotates with -x[i+64]; column i+64 with x[i].
-            float out_lo = lo * tp->cosine[i] + (-hi) * tp->sine[i];
-            float out_hi = hi * tp->cosine[i + 64] + lo * tp->sine[i + 64];
-            if (head < 32) {
-                out_lo = out_lo * tp->qfactor;
-                out_hi = out_hi * tp->qfactor;
-                float* qh = qout + (size_t)t * LH_QUERY + head * 128;
-                qh[i] = out_lo;
-                qh[i + 64] = out_hi;
+        for (int j = 0; j < 3; j++) {
+            const uint32_t head = heads[j], i = is[j];
+            const float scale = head < 32 ? scales.x : (head < 40 ? scales.y : scales.z);
+            const float lo = dots[j] * scale;
+            const float hi = dots[3 + j] * scale;
+            if (head < 40) {
+                // column i < 64 rotates with -x[i+64]; column i+64 with x[i].
+                float out_lo = lo * tp->cosine[i] + (-hi) * tp->sine[i];
+                float out_hi = hi * tp->cosine[i + 64] + lo * tp->sine[i + 64];
+                if (head < 32) {
+                    out_lo = out_lo * tp->qfactor;
+                    out_hi = out_hi * tp->qfactor;
+                    float* qh = qout + (size_t)t * LH_QUERY + head * 128;
+                    qh[i] = out_lo;
+                    qh[i + 64] = out_hi;
+                } else {
+                    float* kr = kcache + lh_kv_index(capacity, 0, head - 32, position);
+                    kr[i] = out_lo;
+                    kr[i + 64] = out_hi;
+                }
             } else {
-                float* kr = kcache + lh_kv_index(capacity, 0, head - 32, position);
-                kr[i] = out_lo;
-                kr[i + 64] = out_hi;
+                float* vr = vcache + lh_kv_index(capacity, 0, head - 40, position);
+                vr[i] = lo;
+                vr[i + 64] = hi;
             }
-        } else {
-            float* vr = vcache + lh_kv_index(capacity, 0, head - 40, position);
-            vr[i] = lo;
-            vr[i + 64] = hi;
-        }
         }
     }
 }
 
 // RMSNorm -> gate and up rows -> SiLU(gate)*up (src/metal_encode.m:162-171).
-// Wave g owns inner rows 2g, 2g+1 (gate and up). grid (9216/8, count).
+// Wave g owns inner rows 3g .. 3g+2 (gate and up). grid (9216/12, count).
 template <bool LUT>
 __global__ void __launch_bounds__(256)
 k_gateup_silu(const uint8_t* __restrict__ Wgate, const uint8_t* __restrict__ Wup, float2 scales,
@@ -439,21 +417,21 @@ k_gateup_silu(const uint8_t* __restrict__ Wgate, const uint8_t* __restrict__ Wup
     }
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t t = blockIdx.y;
-    const uint32_t row0 = (blockIdx.x * 4 + wave) * 2;
-    const uint32_t rr[2] = {row0, row0 + 1};
-    __shared__ float4 xin_s[3 * 4 * 64];
-    float xs[3][16], gs[3][16];
-    wg_input_load<3>(xin + (size_t)t * LH_HIDDEN, gamma, xs, gs);
-    WVec<K_FP8> wg[2][3], wu[2][3];
-    issue_rows<K_FP8, 3, 2>(Wgate, rr, wg);
-    issue_rows<K_FP8, 3, 2>(Wup, rr, wu);
-    wg_input_publish<3>(true, xs, gs, xin_s);
-    float g[2], u[2];
-    dot_rows<K_FP8, LUT, 3, 2>(wg, xs, lut_s, g);
-    dot_rows<K_FP8, LUT, 3, 2>(wu, xs, lut_s, u);
+    const uint32_t row0 = (blockIdx.x * 4 + wave) * 3;
+    const uint32_t rr[3] = {row0, row0 + 1, row0 + 2};
+    __shared__ float4 xin_s[3 * 4 * 64], gam_s[3 * 4 * 64];
+    float4 xv[3], gv[3];
+    stage_load<3, true>(xin + (size_t)t * LH_HIDDEN, gamma, xv, gv);
+    WVec<K_FP8> wg[3][3], wu[3][3];
+    issue_rows<K_FP8, 3, 3>(Wgate, rr, wg);
+    issue_rows<K_FP8, 3, 3>(Wup, rr, wu);
+    stage_commit<3, true>(xv, gv, xin_s, gam_s);
+    float g[3], u[3];
+    dot_rows<K_FP8, LUT, 3, 3>(wg, xin_s, lut_s, g);
+    dot_rows<K_FP8, LUT, 3, 3>(wu, xin_s, lut_s, u);
     if (lane == 0) {
 #pragma unroll
-        for (int r = 0; r < 2; r++) {
+        for (int r = 0; r < 3; r++) {
             const float gv = g[r] * scales.x;
             const float uv = u[r] * scales.y;
             gated[(size_t)t * LH_INNER + row0 + r] = silu(gv) * uv;
@@ -470,14 +448,14 @@ k_head(const uint16_t* __restrict__ E, const float* __restrict__ gamma,
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t row0 = (blockIdx.x * 4 + wave) * 4;
     const uint32_t rr[4] = {row0, row0 + 1, row0 + 2, row0 + 3};
-    __shared__ float4 xin_s[3 * 4 * 64];
-    float xs[3][16], gs[3][16];
-    wg_input_load<3>(xrow, gamma, xs, gs);
+    __shared__ float4 xin_s[3 * 4 * 64], gam_s[3 * 4 * 64];
+    float4 xv[3], gv[3];
+    stage_load<3, true>(xrow, gamma, xv, gv);
     WVec<K_BF16> wv[4][3];
     issue_rows<K_BF16, 3, 4>(E, rr, wv);
-    wg_input_publish<3>(true, xs, gs, xin_s);
+    stage_commit<3, true>(xv, gv, xin_s, gam_s);
     float dots[4];
-    dot_rows<K_BF16, false, 3, 4>(wv, xs, nullptr, dots);
+    dot_rows<K_BF16, false, 3, 4>(wv, xin_s, nullptr, dots);
     if (lane == 0) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
@@ -524,20 +502,37 @@ static int launch_rows(const void* W, float scale, const float* x, float* y, con
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-// Model shapes (3072, 4096 or 9216 columns, rows a multiple of 4R) use the
-// unrolled kernel; returns 1 when the shape is not one of them.
+
+// Model shapes (3072, 4096 or 9216 columns) use the unrolled kernel. FP8 and
+// BF16 weights take three rows per wave where the row count allows it (the
+// model's 3072-row o and down projections then give each SIMD of the 256 CUs
+// the same work); resident FP32 rows take fewer to fit the register file.
+// Returns 1 when the shape is not a model shape.
 template <int KIND, bool LUT>
 static int launch_model_rows(const void* W, float scale, const float* x, float* y,
     const float* residual, uint32_t rows, uint32_t cols, uint32_t tokens, hipStream_t s)
 {
-    if (cols == 3072 && rows % 16 == 0) {
-        return launch_rows<KIND, LUT, 3, 4>(W, scale, x, y, residual, rows, tokens, s);
+    if constexpr (KIND != K_F32) {
+        if (rows % 12 == 0) {
+            if (cols == 3072) {
+                return launch_rows<KIND, LUT, 3, 3>(W, scale, x, y, residual, rows, tokens, s);
+            }
+            if (cols == 4096) {
+                return launch_rows<KIND, LUT, 4, 3>(W, scale, x, y, residual, rows, tokens, s);
+            }
+            if (cols == 9216) {
+                return launch_rows<KIND, LUT, 9, 3>(W, scale, x, y, residual, rows, tokens, s);
+            }
+        }
+    }
+    if (cols == 3072 && rows % 8 == 0) {
+        return launch_rows<KIND, LUT, 3, 2>(W, scale, x, y, residual, rows, tokens, s);
     }
     if (cols == 4096 && rows % 8 == 0) {
         return launch_rows<KIND, LUT, 4, 2>(W, scale, x, y, residual, rows, tokens, s);
     }
-    if (cols == 9216 && rows % 8 == 0) {
-        return launch_rows<KIND, LUT, 9, 2>(W, scale, x, y, residual, rows, tokens, s);
+    if (cols == 9216 && rows % 4 == 0) {
+        return launch_rows<KIND, LUT, 9, 1>(W, scale, x, y, residual, rows, tokens, s);
     }
     return 1;
 }
@@ -593,7 +588,7 @@ extern "C" int lh_launch_qkv_rope(int lookup, const uint8_t* Wqkv, float sq, flo
     const float* gamma, const float* x, const lh_step_params* params, uint32_t count,
     float* q, float* kcache_layer, float* vcache_layer, uint32_t capacity, hipStream_t s)
 {
-    dim3 grid(48 * 32 / 4, count);
+    dim3 grid(48 * 64 / 3 / 4, count);
     float3 scales = make_float3(sq, sk, sv);
     if (lookup) {
         hipLaunchKernelGGL(k_qkv_rope<true>, grid, dim3(256), 0, s, Wqkv, scales, gamma, x, params,
@@ -609,7 +604,7 @@ extern "C" int lh_launch_gateup_silu(int lookup, const uint8_t* Wgate, const uin
     float sg, float su, const float* gamma, const float* x, uint32_t count, float* gated,
     hipStream_t s)
 {
-    dim3 grid(LH_INNER / 8, count);
+    dim3 grid(LH_INNER / 12, count);
     float2 scales = make_float2(sg, su);
     if (lookup) {
         hipLaunchKernelGGL(k_gateup_silu<true>, grid, dim3(256), 0, s, Wgate, Wup, scales, gamma, x, gated);

@@ -413,8 +413,8 @@ extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, floa
         make_float3(w->scale[0], w->scale[1], w->scale[2]), ws->d_split, n, B, ws->d_params,
         ws->d_q, d_keys, d_values, C);
     if (launched_ok("gemm qkv") ||
-        lh_launch_attention(ws->d_q, d_keys, d_values, ws->d_params, n, (uint32_t)(ws->length + n),
-            C, ws->d_S, ws->d_BM, ws->d_PT, ws->d_PA, ws->d_attn, s) ||
+        lh_launch_attention(ws->d_q, d_keys, d_values, ws->d_params, (uint32_t)ws->length, n,
+            C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_attn, s) ||
         split_rows(NULL, ws->d_attn, ws->d_split, LH_QUERY, n, B, s) ||
         rows_residual(w->o, w->scale[3], LH_HIDDEN, LH_QUERY, ws->d_split, n, B, ws->d_gemm, d_x,
             s) ||

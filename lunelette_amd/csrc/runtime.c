@@ -31,6 +31,19 @@ struct lunelette_metal_checkpoint {
     float logits[LH_VOCAB];
 };
 
+/* One-token steps replay a HIP graph per layer path: embedding, every layer
+ * and the head captured once. Replays read ids, positions, rotations and the
+ * context length from the device step record; only the attention block grid
+ * changes, when the context crosses a 64-position boundary, and is updated in
+ * place on the instantiated graph. */
+typedef struct {
+    hipGraph_t graph;
+    hipGraphExec_t exec;
+    hipGraphNode_t attention[LH_LAYERS];
+    uint32_t nodes;           /* attention block nodes found in the capture */
+    uint32_t blocks;          /* grid width the instantiated graph holds */
+} decode_graph;
+
 typedef struct lh_runtime {
     lunelette_metal_limits limits;
     lunelette_metal_prefill_mode prefill_mode;
@@ -55,6 +68,8 @@ typedef struct lh_runtime {
     uint64_t identity, checkpoint_epoch;
     lunelette_metal_checkpoint *active_checkpoint;
     int inject;               /* test seam, see lunelette_metal_test_inject */
+    bool graphs;              /* replay one-token steps as HIP graphs */
+    decode_graph decode[5];   /* indexed by LH_PATH_* */
 } lh_runtime;
 
 struct lunelette_metal {
@@ -125,6 +140,14 @@ static void destroy_runtime(lh_runtime *rt)
     }
     if (rt->h_logits) {
         (void)hipHostFree(rt->h_logits);
+    }
+    for (size_t i = 0; i < sizeof rt->decode / sizeof rt->decode[0]; i++) {
+        if (rt->decode[i].exec) {
+            (void)hipGraphExecDestroy(rt->decode[i].exec);
+        }
+        if (rt->decode[i].graph) {
+            (void)hipGraphDestroy(rt->decode[i].graph);
+        }
     }
     lh_workspace_destroy(rt->ws);
     if (rt->started) {
@@ -331,6 +354,9 @@ lunelette_metal *lunelette_metal_create_synthetic(const lunelette_synthetic_conf
     rt->prefill_mode = selected.prefill;
     rt->strategy = selected.strategy;
     rt->layers = config->layers;
+    /* LUNELETTE_HIP_GRAPHS=0 launches one-token steps kernel by kernel. */
+    const char *graphs = getenv("LUNELETTE_HIP_GRAPHS");
+    rt->graphs = !(graphs && strcmp(graphs, "0") == 0);
     const bool resident = selected.strategy == LUNELETTE_METAL_RESIDENT_FP32;
     const size_t C = resolved.context, B = resolved.block;
     const uint64_t fp8_bytes = layer_fp8_bytes() * rt->layers;
@@ -575,6 +601,108 @@ static int select_path(const lh_runtime *rt, size_t count)
 }
 
 /* src/metal_runtime.m:349-432. */
+/* Device work of one step: embedding gather, every layer, final norm + head. */
+static int launch_step(lh_runtime *rt, size_t count, int path, hipStream_t s)
+{
+    const size_t per_layer = (size_t)LH_KV_HEADS * rt->limits.context * LH_HEAD_DIM;
+    if (lh_embed_forward(rt->d_embedding, rt->d_x, rt->ws, s)) {
+        return -1;
+    }
+    for (uint32_t l = 0; l < rt->layers; l++) {
+        if (lh_layer_forward(&rt->layer[l], rt->d_x, rt->d_keys + l * per_layer,
+                rt->d_values + l * per_layer, rt->ws, path, s)) {
+            return -1;
+        }
+    }
+    return lh_head_forward(rt->d_embedding, rt->d_norms + 2ull * rt->layers * LH_HIDDEN,
+        rt->d_x + (count - 1) * LH_HIDDEN, rt->d_logits, s);
+}
+
+static int graph_fail(hipError_t status, const char *what)
+{
+    lh_set_error("decode graph %s: %s", what, hipGetErrorString(status));
+    return -1;
+}
+
+static int capture_step(lh_runtime *rt, decode_graph *g, int path, uint32_t blocks, hipStream_t s)
+{
+    hipError_t status = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
+    if (status != hipSuccess) {
+        return graph_fail(status, "capture");
+    }
+    const int failed = launch_step(rt, 1, path, s);
+    hipGraph_t graph = NULL;
+    status = hipStreamEndCapture(s, &graph);
+    if (failed || status != hipSuccess || !graph) {
+        if (graph) {
+            (void)hipGraphDestroy(graph);
+        }
+        return failed ? -1 : graph_fail(status, "capture end");
+    }
+    size_t count = 0;
+    hipGraphNode_t *nodes = NULL;
+    status = hipGraphGetNodes(graph, NULL, &count);
+    if (status == hipSuccess && count) {
+        nodes = malloc(count * sizeof *nodes);
+        status = nodes ? hipGraphGetNodes(graph, nodes, &count) : hipErrorOutOfMemory;
+    }
+    const void *kernel = lh_attention_blocks_kernel();
+    g->nodes = 0;
+    for (size_t i = 0; status == hipSuccess && i < count; i++) {
+        hipGraphNodeType type;
+        status = hipGraphNodeGetType(nodes[i], &type);
+        if (status != hipSuccess || type != hipGraphNodeTypeKernel) {
+            continue;
+        }
+        hipKernelNodeParams params;
+        status = hipGraphKernelNodeGetParams(nodes[i], &params);
+        if (status == hipSuccess && params.func == kernel && g->nodes < LH_LAYERS) {
+            g->attention[g->nodes++] = nodes[i];
+        }
+    }
+    free(nodes);
+    if (status == hipSuccess && g->nodes != rt->layers) {
+        status = hipErrorInvalidValue;
+    }
+    if (status == hipSuccess) {
+        status = hipGraphInstantiate(&g->exec, graph, NULL, NULL, 0);
+    }
+    if (status != hipSuccess) {
+        g->exec = NULL;
+        (void)hipGraphDestroy(graph);
+        return graph_fail(status, "instantiate");
+    }
+    g->graph = graph;
+    g->blocks = blocks;
+    return 0;
+}
+
+static int graph_step(lh_runtime *rt, int path, hipStream_t s)
+{
+    decode_graph *g = &rt->decode[path];
+    const uint32_t blocks = lh_attention_blocks((uint32_t)rt->length, 1);
+    if (!g->exec) {
+        if (capture_step(rt, g, path, blocks, s)) {
+            return -1;
+        }
+    } else if (g->blocks != blocks) {
+        for (uint32_t i = 0; i < g->nodes; i++) {
+            hipKernelNodeParams params;
+            hipError_t status = hipGraphKernelNodeGetParams(g->attention[i], &params);
+            if (status == hipSuccess) {
+                params.gridDim.x = blocks;
+                status = hipGraphExecKernelNodeSetParams(g->exec, g->attention[i], &params);
+            }
+            if (status != hipSuccess) {
+                return graph_fail(status, "update");
+            }
+        }
+        g->blocks = blocks;
+    }
+    hipError_t status = hipGraphLaunch(g->exec, s);
+    return status == hipSuccess ? 0 : graph_fail(status, "launch");
+}
+
 static int execute(lunelette_metal *context, const int64_t *ids, size_t count, bool prefill,
     const float **logits, char *error, size_t capacity)
 {
@@ -617,20 +745,11 @@ static int execute(lunelette_metal *context, const int64_t *ids, size_t count, b
         return -1;
     }
     const int path = select_path(rt, count);
-    const size_t per_layer = (size_t)LH_KV_HEADS * rt->limits.context * LH_HEAD_DIM;
     int failed = hipEventRecord(rt->started, s) != hipSuccess ||
-        lh_embed_forward(rt->d_embedding, rt->d_x, rt->ws, s);
-    for (uint32_t l = 0; l < rt->layers && !failed; l++) {
-        failed = lh_layer_forward(&rt->layer[l], rt->d_x, rt->d_keys + l * per_layer,
-            rt->d_values + l * per_layer, rt->ws, path, s);
-    }
-    if (!failed) {
-        failed = lh_head_forward(rt->d_embedding, rt->d_norms + 2ull * rt->layers * LH_HIDDEN,
-            rt->d_x + (count - 1) * LH_HIDDEN, rt->d_logits, s) ||
-            hipEventRecord(rt->finished, s) != hipSuccess ||
-            hipMemcpyAsync(rt->h_logits, rt->d_logits, LH_VOCAB * sizeof(float),
-                hipMemcpyDeviceToHost, s) != hipSuccess;
-    }
+        (count == 1 && rt->graphs ? graph_step(rt, path, s) : launch_step(rt, count, path, s)) ||
+        hipEventRecord(rt->finished, s) != hipSuccess ||
+        hipMemcpyAsync(rt->h_logits, rt->d_logits, LH_VOCAB * sizeof(float),
+            hipMemcpyDeviceToHost, s) != hipSuccess;
     hipError_t status = hipStreamSynchronize(s);
     if (failed || status != hipSuccess) {
         snprintf(error, capacity, "execution failed; reset required: %s",

@@ -247,73 +247,88 @@ static void attend_ref(const float *q, const float *keys, const float *values,
     }
 }
 
-/* Device-mirror attention for one (token, head):
- *   s_p = fl(chain_d fma(q_d, k_pd) * 1/sqrt(128)); M = max_p s_p;
- *   e_p = orc_expf(s_p - M);
- *   per 64-position block b: T_b = tree64(e, zero-padded), A_b[d] = chain over
- *   the block's valid p of fma(e_p, v_pd, acc);
- *   per 256-position tile: chain of its non-empty blocks in order;
- *   over tiles: chain in order; out[d] = A[d] / T. */
+/* Device-mirror attention for one (token, head), 64-position blocks b:
+ *   c_i = chain over d in [32i, 32i+32) of fma(q_d, k_pd) from 0 (i = 0..3);
+ *   s_p = fl(((c_0 + c_1) + (c_2 + c_3)) * 1/sqrt(128));
+ *   m_b = max of the block's s_p; e_p = orc_expf(s_p - m_b);
+ *   T_b = tree64(e, zero-padded); A_b[d] = chain over the block's valid p of
+ *   fma(e_p, v_pd, acc) from 0;
+ *   M = max_b m_b; f_b = orc_expf(m_b - M);
+ *   groups of 8 consecutive blocks: S_g[d] = chain fma(f_b, A_b[d]) and
+ *   U_g = chain fma(f_b, T_b), both from 0 in block order;
+ *   A = S_0 + S_1 + ..., T = U_0 + U_1 + ... left to right; out[d] = A[d] / T. */
 static void attend_mirror(const float *q, const float *keys, const float *values,
     size_t head_stride, size_t pos_stride, size_t kvh, size_t n, float *scores, float *out)
 {
     const float *k0 = keys + kvh * head_stride;
     const float *v0 = values + kvh * head_stride;
+    for (size_t p = 0; p < n; p++) {
+        float c[4];
+        for (int i = 0; i < 4; i++) {
+            float acc = 0.0f;
+            for (int d = 32 * i; d < 32 * i + 32; d++) {
+                acc = fmaf(q[d], k0[p * pos_stride + d], acc);
+            }
+            c[i] = acc;
+        }
+        scores[p] = ((c[0] + c[1]) + (c[2] + c[3])) * ORC_SCORE_SCALE;
+    }
+    const size_t nb = (n + 63) / 64;
+    float *bmax = malloc(nb * sizeof(float));
+    float *btotal = malloc(nb * sizeof(float));
+    float *bacc = malloc(nb * 128 * sizeof(float));
     float maximum = -INFINITY;
-    for (size_t p = 0; p < n; p++) {
-        float acc = 0.0f;
+    for (size_t b = 0; b < nb; b++) {
+        float block_max = -INFINITY;
+        for (size_t p = b * 64; p < n && p < b * 64 + 64; p++) {
+            block_max = fmaxf(block_max, scores[p]);
+        }
+        float lanes[64];
+        float *acc = bacc + b * 128;
         for (int d = 0; d < 128; d++) {
-            acc = fmaf(q[d], k0[p * pos_stride + d], acc);
+            acc[d] = 0.0f;
         }
-        float s = acc * ORC_SCORE_SCALE;
-        scores[p] = s;
-        maximum = fmaxf(maximum, s);
-    }
-    for (size_t p = 0; p < n; p++) {
-        scores[p] = orc_expf(scores[p] - maximum);
-    }
-    float total = 0.0f, acc[128];
-    for (size_t tile = 0; tile * 256 < n; tile++) {
-        float tile_total = 0.0f, tile_acc[128];
-        for (size_t block = tile * 4; block < tile * 4 + 4 && block * 64 < n; block++) {
-            float lanes[64];
-            float block_acc[128];
-            for (int d = 0; d < 128; d++) {
-                block_acc[d] = 0.0f;
-            }
-            for (int l = 0; l < 64; l++) {
-                size_t p = block * 64 + (size_t)l;
-                lanes[l] = p < n ? scores[p] : 0.0f;
-                if (p < n) {
-                    for (int d = 0; d < 128; d++) {
-                        block_acc[d] = fmaf(scores[p], v0[p * pos_stride + d], block_acc[d]);
-                    }
-                }
-            }
-            float block_total = tree64(lanes);
-            if (block == tile * 4) {
-                tile_total = block_total;
-                memcpy(tile_acc, block_acc, sizeof tile_acc);
-            } else {
-                tile_total = tile_total + block_total;
+        for (int l = 0; l < 64; l++) {
+            size_t p = b * 64 + (size_t)l;
+            lanes[l] = 0.0f;
+            if (p < n) {
+                float e = orc_expf(scores[p] - block_max);
+                lanes[l] = e;
                 for (int d = 0; d < 128; d++) {
-                    tile_acc[d] = tile_acc[d] + block_acc[d];
+                    acc[d] = fmaf(e, v0[p * pos_stride + d], acc[d]);
                 }
             }
         }
-        if (tile == 0) {
-            total = tile_total;
-            memcpy(acc, tile_acc, sizeof acc);
-        } else {
-            total = total + tile_total;
+        bmax[b] = block_max;
+        btotal[b] = tree64(lanes);
+        maximum = fmaxf(maximum, block_max);
+    }
+    float total = 0.0f, sum[128] = {0};
+    for (size_t g = 0; g * 8 < nb; g++) {
+        float group_total = 0.0f, group[128] = {0};
+        for (size_t b = g * 8; b < g * 8 + 8 && b < nb; b++) {
+            float f = orc_expf(bmax[b] - maximum);
+            group_total = fmaf(f, btotal[b], group_total);
             for (int d = 0; d < 128; d++) {
-                acc[d] = acc[d] + tile_acc[d];
+                group[d] = fmaf(f, bacc[b * 128 + d], group[d]);
+            }
+        }
+        if (g == 0) {
+            total = group_total;
+            memcpy(sum, group, sizeof sum);
+        } else {
+            total = total + group_total;
+            for (int d = 0; d < 128; d++) {
+                sum[d] = sum[d] + group[d];
             }
         }
     }
     for (int d = 0; d < 128; d++) {
-        out[d] = acc[d] / total;
+        out[d] = sum[d] / total;
     }
+    free(bmax);
+    free(btotal);
+    free(bacc);
 }
 
 void orc_attention(int schedule, const float *q, const float *keys, const float *values,

@@ -126,6 +126,37 @@ def attention_on_device(gpu, q, kpm, vpm, length, count, capacity):
         gpu.lh_workspace_destroy(ws)
 
 
+def test_attention_repeated_launches_one_workspace(gpu):
+    """The per-(token, kv head) arrival counters return to zero after every
+    launch: successive calls with different lengths and counts in one
+    workspace stay bitwise equal to the mirror."""
+    rng = np.random.default_rng(21)
+    capacity, block = 4352, 8
+    total = 3000
+    kpm = rng.normal(size=(total, 1024)).astype(np.float32)
+    vpm = rng.normal(size=(total, 1024)).astype(np.float32)
+    keys = lh.DeviceBuffer.from_array(gpu_util.kv_to_device_layout(kpm, capacity))
+    values = lh.DeviceBuffer.from_array(gpu_util.kv_to_device_layout(vpm, capacity))
+    ws = gpu.lh_workspace_create(capacity, block)
+    assert ws, lh.last_error()
+    try:
+        for length, count in ((2991, 8), (100, 1), (2999, 1), (64, 5), (2047, 2)):
+            q = (rng.normal(size=count * 4096) * 2).astype(np.float32)
+            ids = np.zeros(count, np.int64)
+            lh.check(gpu.lh_workspace_set_tokens(ws, ids.ctypes.data_as(lh.c_int64_p), length,
+                                                 count, None))
+            d_q = lh.DeviceBuffer.from_array(q)
+            out = lh.DeviceBuffer(count * 4096 * 4)
+            lh.check(gpu.lh_attention(d_q.ptr, keys.ptr, values.ptr, ws, out.ptr, None))
+            got = out.download(np.float32)
+            mirror = oracle_lib.attention(MIRROR, q, kpm[:length + count].reshape(-1),
+                                          vpm[:length + count].reshape(-1), 128, 1024,
+                                          length, count)
+            assert np.array_equal(bits(got), bits(mirror)), (length, count)
+    finally:
+        gpu.lh_workspace_destroy(ws)
+
+
 def test_long_causal_sentinel_through_kernels(gpu):
     """tests/test_metal.m:956-999: zero q and K, V rows of 1 except a 4352
     sentinel in the last row; query row 0 must mask it (1.0), row 1 must
@@ -146,8 +177,11 @@ def test_long_causal_sentinel_through_kernels(gpu):
 
 def test_attention_random_bitwise_and_tolerance(gpu):
     rng = np.random.default_rng(12)
+    # Block counts 1, 4, 68 (three combine windows), 32 and 33 (window edge),
+    # 17-token causal chunks, and the 16K-prefix decode shape.
     for length, count, capacity in ((0, 1, 256), (200, 3, 256), (4351, 1, 4352),
-                                    (1000, 17, 4352)):
+                                    (1000, 17, 4352), (2047, 1, 2048), (2047, 3, 4352),
+                                    (16383, 1, 17920)):
         total = length + count
         q = (rng.normal(size=count * 4096) * 3).astype(np.float32)
         kpm = rng.normal(size=(total, 1024)).astype(np.float32)
