@@ -42,6 +42,21 @@ ACT_BYTES = {"qkv_rope": (3072 + 3072 + 4096 + 2048) * 4,
              "down_residual": (9216 + 2 * 3072) * 4}
 
 
+def pmc_traffic():
+    """HBM bytes per k_gateup_silu launch from the committed PMC summary
+    (FETCH_SIZE and WRITE_SIZE runs, calibrated against a kernel of known
+    traffic); None when the summary is absent."""
+    path = os.path.join(ROOT, "profiles", "gateup_silu_decode_pmc_traffic.md")
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return int(line.split(":", 1)[1])
+    except (OSError, ValueError):
+        pass
+    return None
+
+
 def log(*a):
     print(*a, file=sys.stderr, flush=True)
 
@@ -98,6 +113,14 @@ def time_operators(lh, syn, seed, repeats):
         w.post_norm = norms.ptr + 3072 * 4
         layers.append(w)
     stream = lib.lh_stream_create()
+    # Calibration launch of known traffic for the HBM counters: an elementwise
+    # add over 16 Mi floats reads 128 MiB and writes 64 MiB (k_element).
+    cal_n = 16 << 20
+    cal = lh.DeviceBuffer(3 * cal_n * 4)
+    lh.check(lib.lh_memset_device(cal.ptr, 0, 3 * cal_n * 4))
+    for _ in range(2):
+        lh.check(lib.lh_element(0, cal.ptr, cal.ptr + cal_n * 4, cal.ptr + 2 * cal_n * 4, cal_n,
+                                stream))
     ws = lib.lh_workspace_create(capacity, 1)
     ids = np.array([7], np.int64)
     lh.check(lib.lh_workspace_set_tokens(ws, ids.ctypes.data_as(lh.c_int64_p), length, 1, stream))
@@ -252,7 +275,7 @@ def main():
         out["roofline"] = {"bound": "hbm", "kernel": "k_gateup_silu (RMSNorm + gate/up FP8 "
                            "row dots + SiLU*up)", "achieved": round(achieved, 1),
                            "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                           "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": None,
+                           "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": pmc_traffic(),
                            "bytes_per_launch": dom_bytes, "avg_us": round(ops[dom], 3)}
         log("operators (us): %s" % out["operators_us_at_pos4351"])
     if not args.no_cpu_baseline:

@@ -31,8 +31,8 @@ struct lunelette_metal_checkpoint {
     float logits[LH_VOCAB];
 };
 
-/* One-token steps replay a HIP graph per layer path: embedding, every layer
- * and the head captured once. Replays read ids, positions, rotations and the
+/* With graphs enabled, one-token steps replay a HIP graph per layer path:
+ * embedding, every layer and the head captured once. Replays read ids, positions, rotations and the
  * context length from the device step record; only the attention block grid
  * changes, when the context crosses a 64-position boundary, and is updated in
  * place on the instantiated graph. */
@@ -53,7 +53,7 @@ typedef struct lh_runtime {
     hipStream_t stream;
     hipEvent_t started, finished;
     float last_ms;
-    void *d_weights;          /* FP8 codes (compact) or FP32 fl(dec*s) (resident) */
+    void *d_weights;          /* FP8 codes (compact) or their exact FP32 decode (resident) */
     uint16_t *d_embedding;    /* BF16 [131072][3072], also the tied head */
     float *d_norms;           /* FP32 [2*layers+1][3072] */
     lh_layer_weights layer[LH_LAYERS];
@@ -354,9 +354,11 @@ lunelette_metal *lunelette_metal_create_synthetic(const lunelette_synthetic_conf
     rt->prefill_mode = selected.prefill;
     rt->strategy = selected.strategy;
     rt->layers = config->layers;
-    /* LUNELETTE_HIP_GRAPHS=0 launches one-token steps kernel by kernel. */
+    /* LUNELETTE_HIP_GRAPHS=1 replays one-token steps as a HIP graph (opt-in:
+     * on MI355X it measures level with kernel-by-kernel launches, and
+     * rocprofv3 kernel tracing of graph replays has crashed the host process). */
     const char *graphs = getenv("LUNELETTE_HIP_GRAPHS");
-    rt->graphs = !(graphs && strcmp(graphs, "0") == 0);
+    rt->graphs = graphs && strcmp(graphs, "1") == 0;
     const bool resident = selected.strategy == LUNELETTE_METAL_RESIDENT_FP32;
     const size_t C = resolved.context, B = resolved.block;
     const uint64_t fp8_bytes = layer_fp8_bytes() * rt->layers;

@@ -256,25 +256,25 @@ def test_memory_and_limits(rt):
     assert mem["total_bytes"] == mem["weight_bytes"] + mem["scratch_bytes"] + mem["kv_bytes"]
 
 
-def test_graph_replay_equals_kernel_launches_across_blocks(gpu, rt, monkeypatch):
-    """One-token steps replay a captured HIP graph whose attention grid is
-    updated at every 64-position boundary; the same steps launched kernel by
-    kernel (LUNELETTE_HIP_GRAPHS=0) give bitwise equal logits and tokens."""
+def test_graph_replay_equals_kernel_launches_across_blocks(gpu, monkeypatch):
+    """One-token steps replayed from a captured HIP graph (LUNELETTE_HIP_GRAPHS=1)
+    whose attention grid is updated at every 64-position boundary give bitwise
+    the logits and tokens of the same steps launched kernel by kernel."""
+    monkeypatch.setenv("LUNELETTE_HIP_GRAPHS", "1")
+    graphed = Runtime(seed=SEED, layers=LAYERS, context=256, block=256, prefill=lh.PREFILL_CUSTOM)
     monkeypatch.setenv("LUNELETTE_HIP_GRAPHS", "0")
     plain = Runtime(seed=SEED, layers=LAYERS, context=256, block=256, prefill=lh.PREFILL_CUSTOM)
-    monkeypatch.delenv("LUNELETTE_HIP_GRAPHS")
     try:
         ids = syn.tokens(SEED, 9, 60)
-        rt.reset()
-        plain.reset()
-        assert np.array_equal(bits(rt.prefill(ids)), bits(plain.prefill(ids)))
-        token = rt.greedy()
+        assert np.array_equal(bits(graphed.prefill(ids)), bits(plain.prefill(ids)))
+        token = graphed.greedy()
         assert token == plain.greedy()
         for _ in range(72):   # positions 60..131: block counts 1, 2, 3
-            a = rt.decode(token)
+            a = graphed.decode(token)
             b = plain.decode(token)
             assert np.array_equal(bits(a), bits(b))
-            token = rt.greedy()
+            token = graphed.greedy()
             assert token == plain.greedy()
     finally:
         plain.close()
+        graphed.close()
