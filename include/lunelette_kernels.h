@@ -121,6 +121,12 @@ int lh_layer_operator(int op, const lh_layer_weights *w, float *d_x, float *d_ke
  * [0, length+t] of d_keys/d_values ([8][capacity][128]) into d_out. */
 int lh_attention(const float *d_q, const float *d_keys, const float *d_values, lh_workspace *ws,
     float *d_out, void *stream);
+/* The same attention on the matrix cores (the PREFILL_MPS path's operator;
+ * replaces the scores + attend dispatches of src/metal_encode.m:154-159 when
+ * prefill runs on MPS): FP32 MFMA with an online softmax, tolerance-equal to
+ * lh_attention. */
+int lh_attention_mfma(const float *d_q, const float *d_keys, const float *d_values,
+    lh_workspace *ws, float *d_out, void *stream);
 /* MFMA block projection (PREFILL_MPS; replaces convert_fp8 + MPS GEMM,
  * src/metal_encode.m:94-110): y[t][r] = scale * sum_c dec(W[r][c]) x[t][c],
  * FP8 decoded exactly to BF16 tiles, x split exactly into three BF16 parts,

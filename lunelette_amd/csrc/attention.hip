@@ -266,3 +266,206 @@ extern "C" int lh_launch_embed(const uint16_t* E, const lh_step_params* params, 
     hipLaunchKernelGGL(k_embed, dim3(count), dim3(256), 0, s, E, params, x);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
+
+// ---------------------------------------------------------------------------
+// Multi-token attention on the matrix cores (the PREFILL_MPS path; the
+// precise path keeps the block/combine kernels above). FP32 MFMA
+// (v_mfma_f32_16x16x4_f32): products exact, FP32 accumulation in the
+// hardware's order, so the result is tolerance-checked, not bit-mirrored.
+//
+// Workgroup (16-token tile, kv head); wave w is query head 4*kvh + w over the
+// tile's tokens, so the four GQA heads share every K/V tile staged in LDS.
+// Per 64-position block:
+//   S[16 x 64] = Q[16 x 128] K^T: lane group g = lane/16 feeds dims
+//     32g .. 32g+31 (one per MFMA step) of both operands; Q stays in registers.
+//   online softmax per token row (exp as in the decode kernels), causal mask
+//   p <= length + t;
+//   O[16 x 128] += P[16 x 64] V through a per-wave P tile in LDS: lane group g
+//     feeds positions 16g .. 16g+15.
+// out = O / l. grid (ceil(count/16), 8), block 256.
+namespace lh {
+
+constexpr uint32_t FA_TQ = 16;                      // tokens per workgroup
+constexpr uint32_t FA_KS = LH_HEAD_DIM + 4;         // K tile row stride (floats)
+constexpr uint32_t FA_VS = LH_HEAD_DIM + 1;         // V tile row stride
+constexpr uint32_t FA_PS = LH_ATTN_BLOCK + 4;       // P tile row stride
+
+typedef float fa_floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float quad16_max(float v)
+{
+    v = fmaxf(v, __shfl_xor(v, 1, 64));
+    v = fmaxf(v, __shfl_xor(v, 2, 64));
+    v = fmaxf(v, __shfl_xor(v, 4, 64));
+    return fmaxf(v, __shfl_xor(v, 8, 64));
+}
+
+__device__ __forceinline__ float quad16_sum(float v)
+{
+    v = v + __shfl_xor(v, 1, 64);
+    v = v + __shfl_xor(v, 2, 64);
+    v = v + __shfl_xor(v, 4, 64);
+    return v + __shfl_xor(v, 8, 64);
+}
+
+__global__ void __launch_bounds__(256)
+k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
+    const float* __restrict__ vcache, uint32_t length, uint32_t count, uint32_t capacity,
+    float* __restrict__ out)
+{
+    __shared__ __attribute__((aligned(16))) float Ks[LH_ATTN_BLOCK * FA_KS];
+    __shared__ float Vs[LH_ATTN_BLOCK * FA_VS];
+    __shared__ __attribute__((aligned(16))) float Ps[4][FA_TQ * FA_PS];
+    const uint32_t t0 = blockIdx.x * FA_TQ, kvh = blockIdx.y;
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t g = lane >> 4, l16 = lane & 15;
+    const uint32_t head = kvh * 4 + wave;
+    const uint32_t last = (t0 + FA_TQ < count ? t0 + FA_TQ : count) - 1;   // last real token
+    // Q operand: lane (token l16, group g) holds dims 32g .. 32g+31.
+    const uint32_t tq = t0 + l16 <= last ? t0 + l16 : last;
+    fa_floatx4 qv[8];
+    {
+        const fa_floatx4* src = reinterpret_cast<const fa_floatx4*>(
+            q + (size_t)tq * LH_QUERY + head * LH_HEAD_DIM + 32 * g);
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            qv[i] = src[i];
+        }
+    }
+    // Accumulator rows held by this lane: tokens t0 + 4g + r (clamped to the
+    // last real token for the mask; their outputs are not stored).
+    uint32_t limit[4];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const uint32_t t = t0 + 4 * g + r;
+        limit[r] = length + (t <= last ? t : last);   // last visible position
+    }
+    float m[4], l[4];
+    fa_floatx4 o[8];
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        m[r] = -__builtin_inff();
+        l[r] = 0.0f;
+    }
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        o[i] = fa_floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    const uint32_t nb = (length + last + 1 + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
+    const size_t head_base = lh_kv_index(capacity, 0, kvh, 0);
+    float* pw = Ps[wave];
+    for (uint32_t b = 0; b < nb; b++) {
+        // Stage K (float4 rows, stride 132) and V (stride 129) of the block;
+        // every row is inside the capacity (the block count never exceeds it).
+        const fa_floatx4* kb = reinterpret_cast<const fa_floatx4*>(
+            kcache + head_base + (size_t)b * LH_ATTN_BLOCK * LH_HEAD_DIM);
+        const fa_floatx4* vb = reinterpret_cast<const fa_floatx4*>(
+            vcache + head_base + (size_t)b * LH_ATTN_BLOCK * LH_HEAD_DIM);
+        fa_floatx4 kr[8], vr[8];
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            kr[i] = kb[tid + 256 * i];
+            vr[i] = vb[tid + 256 * i];
+        }
+        __syncthreads();   // the previous block's tiles are consumed
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t idx = tid + 256 * i, row = idx >> 5, c4 = idx & 31;
+            *reinterpret_cast<fa_floatx4*>(&Ks[row * FA_KS + 4 * c4]) = kr[i];
+            float* vd = &Vs[row * FA_VS + 4 * c4];
+            vd[0] = vr[i].x;
+            vd[1] = vr[i].y;
+            vd[2] = vr[i].z;
+            vd[3] = vr[i].w;
+        }
+        __syncthreads();
+        // S tiles j = 0..3: positions 16j + l16 of the block.
+        fa_floatx4 s[4];
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            s[j] = fa_floatx4{0.f, 0.f, 0.f, 0.f};
+            const fa_floatx4* kp = reinterpret_cast<const fa_floatx4*>(&Ks[(16 * j + l16) * FA_KS + 32 * g]);
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const fa_floatx4 kk = kp[i];
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[i].x, kk.x, s[j], 0, 0, 0);
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[i].y, kk.y, s[j], 0, 0, 0);
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[i].z, kk.z, s[j], 0, 0, 0);
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[i].w, kk.w, s[j], 0, 0, 0);
+            }
+        }
+        // Scale, causal mask, online softmax; P to this wave's LDS tile.
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float mx = -__builtin_inff();
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t p = b * LH_ATTN_BLOCK + 16 * j + l16;
+                const float v = p <= limit[r] ? s[j][r] * LH_SCORE_SCALE : -__builtin_inff();
+                s[j][r] = v;
+                mx = fmaxf(mx, v);
+            }
+            mx = quad16_max(mx);
+            const float m_new = fmaxf(m[r], mx);
+            const float alpha = expf_cw(m[r] - m_new);
+            float sum = 0.0f;
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const float e = expf_cw(s[j][r] - m_new);
+                sum = sum + e;
+                pw[(4 * g + r) * FA_PS + 16 * j + l16] = e;
+            }
+            l[r] = l[r] * alpha + quad16_sum(sum);
+            m[r] = m_new;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                o[i][r] = o[i][r] * alpha;
+            }
+        }
+        // O += P V. A operand: lane (token l16, group g) holds P[l16][16g .. 16g+15].
+        fa_floatx4 pv[4];
+        {
+            const fa_floatx4* pp = reinterpret_cast<const fa_floatx4*>(&pw[l16 * FA_PS + 16 * g]);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                pv[i] = pp[i];
+            }
+        }
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+#pragma unroll
+            for (int k = 0; k < 4; k++) {
+                const float* vrow = &Vs[(16 * g + 4 * k) * FA_VS + 16 * i + l16];
+                o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[k].x, vrow[0], o[i], 0, 0, 0);
+                o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[k].y, vrow[FA_VS], o[i], 0, 0, 0);
+                o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[k].z, vrow[2 * FA_VS], o[i], 0, 0, 0);
+                o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[k].w, vrow[3 * FA_VS], o[i], 0, 0, 0);
+            }
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+        const uint32_t t = t0 + 4 * g + r;
+        if (t <= last) {
+            float* dst = out + (size_t)t * LH_QUERY + head * LH_HEAD_DIM + l16;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                dst[16 * i] = o[i][r] / l[r];
+            }
+        }
+    }
+}
+
+}  // namespace lh
+
+extern "C" int lh_launch_attention_mfma(const float* q, const float* kcache_layer,
+    const float* vcache_layer, uint32_t length, uint32_t count, uint32_t capacity, float* out,
+    hipStream_t s)
+{
+    if (!count || capacity % LH_ATTN_BLOCK || length + count > capacity) {
+        return -1;
+    }
+    hipLaunchKernelGGL(lh::k_attn_mfma, dim3((count + lh::FA_TQ - 1) / lh::FA_TQ, LH_KV_HEADS),
+        dim3(256), 0, s, q, kcache_layer, vcache_layer, length, count, capacity, out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}

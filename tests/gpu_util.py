@@ -57,3 +57,25 @@ def kv_to_device_layout(kpm, capacity):
 def kv_from_device_layout(khm, position, count):
     return np.ascontiguousarray(khm[:, position:position + count].transpose(1, 0, 2)).reshape(
         count, 1024)
+
+
+def attention_on_device(gpu, entry, q, kpm, vpm, length, count, capacity):
+    """Run an attention entry point (lh_attention or lh_attention_mfma) on
+    position-major q/K/V; returns [count][4096] and checks the output guard."""
+    ws = gpu.lh_workspace_create(capacity, count)
+    assert ws, lh.last_error()
+    try:
+        ids = np.zeros(count, np.int64)
+        lh.check(gpu.lh_workspace_set_tokens(ws, ids.ctypes.data_as(lh.c_int64_p), length, count,
+                                             None))
+        d_q = lh.DeviceBuffer.from_array(q)
+        keys = lh.DeviceBuffer.from_array(kv_to_device_layout(kpm, capacity))
+        values = lh.DeviceBuffer.from_array(kv_to_device_layout(vpm, capacity))
+        out = lh.DeviceBuffer(count * 4096 * 4 + 16)
+        lh.check(gpu.lh_memset_device(out.ptr, 0x5a, out.nbytes))
+        lh.check(entry(d_q.ptr, keys.ptr, values.ptr, ws, out.ptr, None))
+        raw = out.download(np.uint8)
+        assert np.all(raw[count * 4096 * 4:] == 0x5a), "wrote past the output"
+        return raw[:count * 4096 * 4].view(np.float32)
+    finally:
+        gpu.lh_workspace_destroy(ws)

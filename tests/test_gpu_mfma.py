@@ -9,7 +9,11 @@ The reference's own MPS path is pinned only by tolerance (tests/test_metal.m:
   <= 1e-5), appended K/V rows within 1e-5 of the row max-abs;
 - runtime prefill of a 2-layer model in MPS mode: logits within 1e-3 of the
   logit range of the precise oracle and the same greedy token, continuing
-  into decode.
+  into decode;
+- matrix-core attention (FP32 MFMA, online softmax) vs the oracle's
+  reference-literal and mirror schedules: |err| <= 2e-4 for unit-scale
+  values over 1..69 blocks, ragged token tiles and the causal sentinel of
+  tests/test_metal.m:956-999.
 """
 import numpy as np
 import pytest
@@ -122,3 +126,40 @@ def test_runtime_mps_prefill_then_decode(gpu):
             assert rt.greedy() == int(np.argmax(want))
             token = rt.greedy()
             length += 1
+
+
+@pytest.mark.parametrize("length,count,capacity", [(0, 5, 256), (60, 3, 256), (0, 256, 256),
+                                                   (256, 256, 4352), (1000, 17, 4352),
+                                                   (4096, 256, 4352)])
+def test_attention_mfma_vs_oracle(gpu, length, count, capacity):
+    rng = np.random.default_rng(length + 7 * count)
+    total = length + count
+    q = (rng.normal(size=count * 4096) * 3).astype(np.float32)
+    kpm = rng.normal(size=(total, 1024)).astype(np.float32)
+    vpm = rng.normal(size=(total, 1024)).astype(np.float32)
+    got = gpu_util.attention_on_device(gpu, gpu.lh_attention_mfma, q, kpm, vpm, length, count,
+                                       capacity)
+    mirror = oracle_lib.attention(MIRROR, q, kpm.reshape(-1), vpm.reshape(-1), 128, 1024,
+                                  length, count)
+    assert np.all(np.isfinite(got))
+    assert np.max(np.abs(got - mirror)) < 2e-4, (length, count)
+    if total <= 1024:
+        ref = oracle_lib.attention(REF, q, kpm.reshape(-1), vpm.reshape(-1), 128, 1024,
+                                   length, count)
+        assert np.max(np.abs(got - ref)) < 2e-4, (length, count)
+
+
+def test_attention_mfma_causal_sentinel(gpu):
+    """tests/test_metal.m:956-999 through the matrix-core kernel: zero q and K,
+    V rows of 1 except 4352 in the last row; row 0 masks it (1.0), row 1
+    includes it (8703/4352)."""
+    capacity, count = 4352, 2
+    length = capacity - count
+    q = np.zeros(count * 4096, np.float32)
+    kpm = np.zeros((capacity, 1024), np.float32)
+    vpm = np.ones((capacity, 1024), np.float32)
+    vpm[capacity - 1] = 4352.0
+    got = gpu_util.attention_on_device(gpu, gpu.lh_attention_mfma, q, kpm, vpm, length, count,
+                                       capacity)
+    assert np.max(np.abs(got[:4096] - 1.0)) < 2e-4
+    assert np.max(np.abs(got[4096:] - 8703.0 / 4352)) < 2e-4
