@@ -71,6 +71,8 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-operators", action="store_true")
     p.add_argument("--op-repeats", type=int, default=4)
+    p.add_argument("--long", action="store_true",
+                   help="also run the long-context prefix-reuse workload (about a minute)")
     return p.parse_args()
 
 
@@ -150,6 +152,59 @@ def time_operators(lh, syn, seed, repeats):
     lib.lh_workspace_destroy(ws)
     lib.lh_stream_destroy(stream)
     return result
+
+
+def long_context(lh, syn, Runtime, seed, prefill_mode):
+    """Prefix-reuse workload at the 17920 profile: a 16384-token seeded prompt
+    prefilled in 256-token chunks (checkpoint after 15872 tokens), then 8
+    turns that restore the 15872-token prefix, append 64 new random tokens
+    and greedily decode 128 tokens (KV length 15937..16064)."""
+    rt = Runtime(seed=seed, layers=26, context=17920, block=256, prefill=prefill_mode,
+                 strategy=lh.COMPACT_FP8_ARITHMETIC)
+    try:
+        prompt = syn.tokens(seed, 2, 16384)
+        keep, chunk = 15872, 256
+        lh.check(lh.lib().lh_device_synchronize())
+        t = time.perf_counter()
+        device = 0.0
+        checkpoint = None
+        for begin in range(0, len(prompt), chunk):
+            ids = prompt[begin:begin + chunk]
+            if begin == 0:
+                rt.prefill(ids, copy=False)
+            else:
+                rt.append(ids, copy=False)
+            device += rt.last_device_ms()
+            if begin + chunk == keep:
+                checkpoint = rt.checkpoint()
+        lh.check(lh.lib().lh_device_synchronize())
+        prefill_s = time.perf_counter() - t
+        turns, append_s, decode_s, decode_device = 8, 0.0, 0.0, 0.0
+        decoded = 0
+        for turn in range(turns):
+            rt.restore(checkpoint, copy=False)
+            t = time.perf_counter()
+            rt.append(syn.tokens(seed, 100 + turn, 64), copy=False)
+            append_s += time.perf_counter() - t
+            token = rt.greedy()
+            t = time.perf_counter()
+            for _ in range(128):
+                rt.decode(token, copy=False)
+                decode_device += rt.last_device_ms()
+                token = rt.greedy()
+                decoded += 1
+            decode_s += time.perf_counter() - t
+        rt.destroy_checkpoint(checkpoint)
+        return {"workload": "16384-token prompt in 256-token chunks at context 17920; 8 turns "
+                            "restore a 15872-token prefix, append 64 tokens, decode 128",
+                "prefill_tok_s": round(len(prompt) / prefill_s, 1),
+                "prefill_device_ms": round(device, 2),
+                "turn_append_ms": round(append_s * 1e3 / turns, 3),
+                "decode_tok_s": round(decoded / decode_s, 2),
+                "decode_device_ms_per_step": round(decode_device / decoded, 4),
+                "kv_length": [keep + 65, keep + 64 + 128]}
+    finally:
+        rt.close()
 
 
 def cpu_baseline(syn, seed, budget_s=20.0):
@@ -278,6 +333,9 @@ def main():
                            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": pmc_traffic(),
                            "bytes_per_launch": dom_bytes, "avg_us": round(ops[dom], 3)}
         log("operators (us): %s" % out["operators_us_at_pos4351"])
+    if args.long:
+        out["long_context"] = long_context(lh, syn, Runtime, args.seed, prefill_mode)
+        log("long context: %s" % out["long_context"])
     if not args.no_cpu_baseline:
         out["cpu_baseline"] = cpu_baseline(syn, args.seed)
     print(json.dumps(out), flush=True)

@@ -123,11 +123,13 @@ k_attn_blocks(const float* __restrict__ q, const float* __restrict__ kcache,
 }
 
 // grid (32 heads, count), 256 threads: thread (c = tid & 31, s = tid >> 5)
-// owns dims 4c..4c+3 of groups s and s + 8 of each 128-block round.
+// owns dims 4c..4c+3 of groups s and s + 8 of each 128-block round. The
+// partials are the token's 64-position blocks (parts = 0) or `parts` KV
+// splits of the matrix-core kernel (same (max, sum, P.V) form).
 __global__ void __launch_bounds__(256)
 k_attn_combine(const float* __restrict__ PM, const float* __restrict__ PT,
     const float* __restrict__ PA, const lh_step_params* __restrict__ params, uint32_t capacity,
-    float* __restrict__ out)
+    uint32_t parts, float* __restrict__ out)
 {
     __shared__ float wmax[4];
     __shared__ float fs[ROUND], ts[ROUND];
@@ -135,7 +137,7 @@ k_attn_combine(const float* __restrict__ PM, const float* __restrict__ PT,
     __shared__ float ug[ROUND / GROUP];
     const uint32_t h = blockIdx.x, t = blockIdx.y;
     const uint32_t n = params->length + t + 1;
-    const uint32_t nb = (n + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
+    const uint32_t nb = parts ? parts : (n + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
     const uint32_t nbc = capacity / LH_ATTN_BLOCK;
     const size_t th = (size_t)t * LH_HEADS + h;
     const float* pm = PM + th * nbc;
@@ -246,7 +248,7 @@ extern "C" int lh_launch_attention(const float* q, const float* kcache_layer,
     hipLaunchKernelGGL(k_attn_blocks, dim3(lh_attention_blocks(length, count), LH_KV_HEADS, count),
         dim3(256), 0, s, q, kcache_layer, vcache_layer, params, capacity, PM, PT, PA);
     hipLaunchKernelGGL(k_attn_combine, dim3(LH_HEADS, count), dim3(256), 0, s, PM, PT, PA, params,
-        capacity, out);
+        capacity, 0u, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -282,7 +284,10 @@ extern "C" int lh_launch_embed(const uint16_t* E, const lh_step_params* params, 
 //   p <= length + t;
 //   O[16 x 128] += P[16 x 64] V through a per-wave P tile in LDS: lane group g
 //     feeds positions 16g .. 16g+15.
-// out = O / l. grid (ceil(count/16), 8), block 256.
+// out = O / l. grid (ceil(count/16), 8, splits), block 256. With splits > 1
+// split z takes a contiguous range of the tile's blocks and writes its
+// unnormalized (max, sum, O) rows as part z of PM/PT/PA (partial stride
+// capacity/64 per (token, head)), merged by k_attn_combine.
 namespace lh {
 
 constexpr uint32_t FA_TQ = 16;                      // tokens per workgroup
@@ -311,7 +316,7 @@ __device__ __forceinline__ float quad16_sum(float v)
 __global__ void __launch_bounds__(256)
 k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
     const float* __restrict__ vcache, uint32_t length, uint32_t count, uint32_t capacity,
-    float* __restrict__ out)
+    float* __restrict__ PM, float* __restrict__ PT, float* __restrict__ PA, float* __restrict__ out)
 {
     __shared__ __attribute__((aligned(16))) float Ks[LH_ATTN_BLOCK * FA_KS];
     __shared__ float Vs[LH_ATTN_BLOCK * FA_VS];
@@ -352,9 +357,13 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
         o[i] = fa_floatx4{0.f, 0.f, 0.f, 0.f};
     }
     const uint32_t nb = (length + last + 1 + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
+    const uint32_t splits = gridDim.z, z = blockIdx.z;
+    const uint32_t per = (nb + splits - 1) / splits;
+    const uint32_t b_begin = z * per < nb ? z * per : nb;
+    const uint32_t b_end = b_begin + per < nb ? b_begin + per : nb;
     const size_t head_base = lh_kv_index(capacity, 0, kvh, 0);
     float* pw = Ps[wave];
-    for (uint32_t b = 0; b < nb; b++) {
+    for (uint32_t b = b_begin; b < b_end; b++) {
         // Stage K (float4 rows, stride 132) and V (stride 129) of the block;
         // every row is inside the capacity (the block count never exceeds it).
         const fa_floatx4* kb = reinterpret_cast<const fa_floatx4*>(
@@ -406,12 +415,15 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
                 mx = fmaxf(mx, v);
             }
             mx = quad16_max(mx);
+            // A split can start past a row's last visible position: keep
+            // the row empty (no exp of -inf - -inf).
             const float m_new = fmaxf(m[r], mx);
-            const float alpha = expf_cw(m[r] - m_new);
+            const bool empty = m_new == -__builtin_inff();
+            const float alpha = empty ? 1.0f : expf_cw(m[r] - m_new);
             float sum = 0.0f;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const float e = expf_cw(s[j][r] - m_new);
+                const float e = empty ? 0.0f : expf_cw(s[j][r] - m_new);
                 sum = sum + e;
                 pw[(4 * g + r) * FA_PS + 16 * j + l16] = e;
             }
@@ -443,14 +455,29 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
             }
         }
     }
+    const uint32_t nbc = capacity / LH_ATTN_BLOCK;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
         const uint32_t t = t0 + 4 * g + r;
-        if (t <= last) {
+        if (t > last) {
+            continue;
+        }
+        if (splits == 1) {
             float* dst = out + (size_t)t * LH_QUERY + head * LH_HEAD_DIM + l16;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 dst[16 * i] = o[i][r] / l[r];
+            }
+        } else {
+            const size_t part = ((size_t)t * LH_HEADS + head) * nbc + z;
+            if (l16 == 0) {
+                PM[part] = m[r];
+                PT[part] = l[r];
+            }
+            float* dst = PA + part * LH_HEAD_DIM + l16;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                dst[16 * i] = o[i][r];
             }
         }
     }
@@ -459,13 +486,25 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
 }  // namespace lh
 
 extern "C" int lh_launch_attention_mfma(const float* q, const float* kcache_layer,
-    const float* vcache_layer, uint32_t length, uint32_t count, uint32_t capacity, float* out,
-    hipStream_t s)
+    const float* vcache_layer, const lh_step_params* params, uint32_t length, uint32_t count,
+    uint32_t capacity, float* PM, float* PT, float* PA, float* out, hipStream_t s)
 {
     if (!count || capacity % LH_ATTN_BLOCK || length + count > capacity) {
         return -1;
     }
-    hipLaunchKernelGGL(lh::k_attn_mfma, dim3((count + lh::FA_TQ - 1) / lh::FA_TQ, LH_KV_HEADS),
-        dim3(256), 0, s, q, kcache_layer, vcache_layer, length, count, capacity, out);
+    // KV splits so that about 256 workgroups run: each takes at least 4
+    // blocks of the longest tile, at most one partial per block.
+    const uint32_t tiles = (count + lh::FA_TQ - 1) / lh::FA_TQ;
+    const uint32_t nb = (length + count + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
+    uint32_t splits = 256 / (tiles * LH_KV_HEADS);
+    const uint32_t by_length = nb / 4;
+    splits = splits < by_length ? splits : by_length;
+    splits = splits ? splits : 1;
+    hipLaunchKernelGGL(lh::k_attn_mfma, dim3(tiles, LH_KV_HEADS, splits), dim3(256), 0, s, q,
+        kcache_layer, vcache_layer, length, count, capacity, PM, PT, PA, out);
+    if (splits > 1) {
+        hipLaunchKernelGGL(lh::k_attn_combine, dim3(LH_HEADS, count), dim3(256), 0, s, PM, PT, PA,
+            params, capacity, splits, out);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -32,7 +32,8 @@ int lh_launch_attention(const float *q, const float *kcache_layer, const float *
     float *PT, float *PA, float *out, hipStream_t s);
 /* Matrix-core attention for multi-token steps (tolerance path). */
 int lh_launch_attention_mfma(const float *q, const float *kcache_layer, const float *vcache_layer,
-    uint32_t length, uint32_t count, uint32_t capacity, float *out, hipStream_t s);
+    const lh_step_params *params, uint32_t length, uint32_t count, uint32_t capacity, float *PM,
+    float *PT, float *PA, float *out, hipStream_t s);
 /* Block-grid width of the attention kernel, and its function (graph updates). */
 uint32_t lh_attention_blocks(uint32_t length, uint32_t count);
 const void *lh_attention_blocks_kernel(void);

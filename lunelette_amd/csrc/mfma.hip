@@ -492,8 +492,8 @@ extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, floa
     // o: 3072 rows in tiles of 96, 4096 columns, residual.
     const uint32_t so = splits_for(n, 8);
     if (launched_ok("qkv epilogue") ||
-        lh_launch_attention_mfma(ws->d_q, d_keys, d_values, (uint32_t)ws->length, n, C,
-            ws->d_attn, s) ||
+        lh_launch_attention_mfma(ws->d_q, d_keys, d_values, ws->d_params, (uint32_t)ws->length,
+            n, C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_attn, s) ||
         split_rows(NULL, ws->d_attn, ws->d_split, LH_QUERY, n, B, s) ||
         gemm<6>(w->o, NULL, LH_HIDDEN, LH_HIDDEN, LH_QUERY, ws->d_split, B, n, so, P, s) ||
         combine(P, so, LH_HIDDEN, n, B, w->scale[3], d_x, 1, s)) {

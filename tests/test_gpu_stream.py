@@ -1,0 +1,77 @@
+"""Greedy token streams of the full 26-layer model on the GPU.
+
+Workload: the random-init 26-layer Ministral-3B-shaped FP8 model, context
+4352, a 512-token seeded prompt prefilled in two 256-token chunks, then greedy
+decode (the bench workload). The fixture tests/golden/stream_c4352_26layer.json
+holds the CPU oracle's streams (tests/golden/make_stream_golden.py):
+- the precise path (PREFILL_CUSTOM + decode) must reproduce the oracle's
+  device-mirror stream token for token (it is bit-exact per step);
+- the reference-literal stream is the same up to the fixture's first
+  divergence (an ulp-level difference through a near-tie of the model's
+  one-hot softmax), which this test reports;
+- the MPS path (matrix-core prefill, tolerance-equal logits) must select the
+  same first token, and reports how long its stream agrees.
+"""
+import json
+import os
+
+import numpy as np
+import pytest
+
+import lunelette_amd as lh
+from lunelette_amd import synthetic as syn
+from lunelette_amd.runtime import Runtime
+
+pytestmark = pytest.mark.gpu
+FIXTURE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                       "stream_c4352_26layer.json")
+
+
+def fixture():
+    if not os.path.exists(FIXTURE):
+        pytest.skip("stream fixture not generated (tests/golden/make_stream_golden.py)")
+    with open(FIXTURE) as f:
+        return json.load(f)
+
+
+def run_stream(fx, prefill_mode):
+    rt = Runtime(seed=fx["seed"], layers=fx["layers"], context=fx["context"], block=256,
+                 prefill=prefill_mode)
+    try:
+        prompt = syn.tokens(fx["seed"], 1, fx["prompt"])
+        assert [int(t) for t in prompt[:8]] == fx["prompt_sha_first"]
+        chunk = fx["chunk"]
+        rt.prefill(prompt[:chunk], copy=False)
+        for begin in range(chunk, fx["prompt"], chunk):
+            rt.append(prompt[begin:begin + chunk], copy=False)
+        tokens = [rt.greedy()]
+        for _ in range(fx["decode"] - 1):
+            rt.decode(tokens[-1], copy=False)
+            tokens.append(rt.greedy())
+        return tokens
+    finally:
+        rt.close()
+
+
+def agreement(a, b):
+    return next((i for i in range(min(len(a), len(b))) if a[i] != b[i]), min(len(a), len(b)))
+
+
+def test_precise_stream_matches_oracle_mirror(gpu):
+    fx = fixture()
+    tokens = run_stream(fx, lh.PREFILL_CUSTOM)
+    assert tokens == fx["tokens_mirror"], "first mismatch at %d" % agreement(
+        tokens, fx["tokens_mirror"])
+    ref_agree = agreement(tokens, fx["tokens_ref"])
+    expected = fx["first_divergence"]
+    assert ref_agree == (len(tokens) if expected is None else expected)
+    print("precise stream: %d/%d tokens equal the mirror oracle; %d equal the "
+          "reference-literal oracle" % (len(tokens), len(tokens), ref_agree))
+
+
+def test_mps_stream_first_token_and_agreement(gpu):
+    fx = fixture()
+    tokens = run_stream(fx, lh.PREFILL_MPS)
+    assert tokens[0] == fx["tokens_mirror"][0]
+    n = agreement(tokens, fx["tokens_mirror"])
+    print("MPS stream: first %d/%d tokens equal the mirror oracle" % (n, len(tokens)))
