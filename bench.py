@@ -154,6 +154,97 @@ def time_operators(lh, syn, seed, repeats):
     return result
 
 
+def fp8_linear(lh, syn, seed, copies=16, repeats=8):
+    """One FP8 linear y = s*(W.x), W 9216x3072 (28.3 MB), s = 0.0125, x ~ N(0,1),
+    over `copies` distinct weight copies (453 MB, beyond the 256 MB Infinity
+    Cache): HIP-event time per launch and HBM GB/s."""
+    lib = lh.lib()
+    rows, cols = 9216, 3072
+    w = syn.fp8(seed, 500, rows, cols)
+    weights = lh.DeviceBuffer(w.nbytes * copies)
+    lh.check(lib.lh_memcpy_htod(weights.ptr, w.ctypes.data, w.nbytes))
+    for i in range(1, copies):
+        lh.check(lib.lh_memcpy_dtod(weights.ptr + i * w.nbytes, weights.ptr, w.nbytes))
+    x = lh.DeviceBuffer.from_array(syn.normal_f32(seed, 501, cols))
+    y = lh.DeviceBuffer(rows * 4)
+    stream = lib.lh_stream_create()
+    start, stop = lib.lh_event_create(), lib.lh_event_create()
+    for i in range(copies):
+        lh.check(lib.lh_fp8_matvec(weights.ptr + i * w.nbytes, 0.0125, x.ptr, y.ptr, rows, cols,
+                                   1, 0, stream))
+    n = copies * repeats
+    lh.check(lib.lh_event_record(start, stream))
+    for i in range(n):
+        lh.check(lib.lh_fp8_matvec(weights.ptr + (i % copies) * w.nbytes, 0.0125, x.ptr, y.ptr,
+                                   rows, cols, 1, 0, stream))
+    lh.check(lib.lh_event_record(stop, stream))
+    ms = ctypes.c_float()
+    lh.check(lib.lh_event_elapsed_ms(start, stop, ctypes.byref(ms)))
+    us = ms.value * 1e3 / n
+    nbytes = rows * cols + 4 * (cols + rows)
+    for e in (start, stop):
+        lib.lh_event_destroy(e)
+    lib.lh_stream_destroy(stream)
+    return {"shape": [rows, cols], "us": round(us, 3), "bytes": nbytes,
+            "GBps": round(nbytes / (us * 1e-6) / 1e9, 1),
+            "frac_hbm": round(nbytes / (us * 1e-6) / 1e9 / HBM_PEAK_GBPS, 4)}
+
+
+def prefill_layer(lh, syn, seed, repeats=8):
+    """One decoder layer in chunked-prefill mode on the matrix-core path: 256
+    tokens after a 4096-token prefix (KV N(0,1)), capacity 4352. HIP-event time
+    per layer; GEMM 59.59 GFLOP (x3 BF16 planes on the MFMA units) and
+    attention 17.72 GFLOP."""
+    lib = lh.lib()
+    capacity, length, count = 4352, 4096, 256
+    host = syn.layer(seed, 0)
+    qkv = np.concatenate([host["q"], host["k"], host["v"]], axis=0)
+    keep = []
+    w = lh.LayerWeights()
+    for name, m in (("qkv", qkv), ("o", host["o"]), ("gate", host["gate"]), ("up", host["up"]),
+                    ("down", host["down"])):
+        buf = lh.DeviceBuffer.from_array(m)
+        keep.append(buf)
+        setattr(w, name, buf.ptr)
+    for j, n in enumerate(("q", "k", "v", "o", "gate", "up", "down")):
+        w.scale[j] = host["scale_" + n]
+    for n in ("input_norm", "post_norm"):
+        buf = lh.DeviceBuffer.from_array(syn.bf16_to_f32(host[n]))
+        keep.append(buf)
+        setattr(w, n, buf.ptr)
+    kv_elems = 8 * capacity * 128
+    keys = lh.DeviceBuffer.from_array(syn.normal_f32(seed, 9200, kv_elems))
+    values = lh.DeviceBuffer.from_array(syn.normal_f32(seed, 9201, kv_elems))
+    x0 = lh.DeviceBuffer.from_array(syn.normal_f32(seed, 9202, count * 3072))
+    x = lh.DeviceBuffer(count * 3072 * 4)
+    stream = lib.lh_stream_create()
+    ws = lib.lh_workspace_create(capacity, count)
+    ids = np.arange(count, dtype=np.int64)
+    lh.check(lib.lh_workspace_set_tokens(ws, ids.ctypes.data_as(lh.c_int64_p), length, count,
+                                         stream))
+    start, stop = lib.lh_event_create(), lib.lh_event_create()
+    total = 0.0
+    for rep in range(repeats + 2):
+        lh.check(lib.lh_memcpy_dtod(x.ptr, x0.ptr, count * 3072 * 4))
+        lh.check(lib.lh_event_record(start, stream))
+        lh.check(lib.lh_layer_forward(ctypes.byref(w), x.ptr, keys.ptr, values.ptr, ws,
+                                      lh.PATH_MFMA, stream))
+        lh.check(lib.lh_event_record(stop, stream))
+        ms = ctypes.c_float()
+        lh.check(lib.lh_event_elapsed_ms(start, stop, ctypes.byref(ms)))
+        if rep >= 2:
+            total += ms.value
+    us = total * 1e3 / repeats
+    gemm, attn = 59.59e9, 17.72e9
+    for e in (start, stop):
+        lib.lh_event_destroy(e)
+    lib.lh_workspace_destroy(ws)
+    lib.lh_stream_destroy(stream)
+    return {"tokens": count, "prefix": length, "us": round(us, 1),
+            "algorithmic_TFLOPs": round((gemm + attn) / (us * 1e-6) / 1e12, 1),
+            "gemm_bf16_mfma_util_lower_bound": round(3 * gemm / (us * 1e-6) / 2.5e15, 4)}
+
+
 def long_context(lh, syn, Runtime, seed, prefill_mode):
     """Prefix-reuse workload at the 17920 profile: a 16384-token seeded prompt
     prefilled in 256-token chunks (checkpoint after 15872 tokens), then 8
@@ -333,6 +424,10 @@ def main():
                            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": pmc_traffic(),
                            "bytes_per_launch": dom_bytes, "avg_us": round(ops[dom], 3)}
         log("operators (us): %s" % out["operators_us_at_pos4351"])
+        out["fp8_linear_9216x3072"] = fp8_linear(lh, syn, args.seed)
+        out["prefill_layer_256_after_4096"] = prefill_layer(lh, syn, args.seed)
+        log("fp8 linear: %s" % out["fp8_linear_9216x3072"])
+        log("prefill layer: %s" % out["prefill_layer_256_after_4096"])
     if args.long:
         out["long_context"] = long_context(lh, syn, Runtime, args.seed, prefill_mode)
         log("long context: %s" % out["long_context"])

@@ -52,6 +52,28 @@ def _compile(src):
     return obj
 
 
+def kernel_resources(src):
+    """Per-kernel resources of one HIP source as compiled for gfx950:
+    [(name, vgpr, agpr, lds_bytes, scratch_bytes)], from the code-object
+    metadata of a device-only assembly build with the library's flags."""
+    import re
+    import tempfile
+    inc = ["-I" + os.path.join(ROOT, "include"), "-I" + CSRC]
+    with tempfile.TemporaryDirectory() as tmp:
+        out = os.path.join(tmp, "k.s")
+        _run([HIPCC] + HIP_FLAGS + inc + ["--cuda-device-only", "-S", src, "-o", out])
+        text = open(out).read()
+    kernels = []
+    for block in text.split("  - .agpr_count:")[1:]:
+        def field(key):
+            m = re.search(r"\." + key + r":\s+(\S+)", block)
+            return m.group(1) if m else None
+        kernels.append((field("name"), int(field("vgpr_count")), int(block.split()[0]),
+                        int(field("group_segment_fixed_size")),
+                        int(field("private_segment_fixed_size"))))
+    return kernels
+
+
 def build_library(jobs=8):
     os.makedirs(OBJ, exist_ok=True)
     sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.c")))
