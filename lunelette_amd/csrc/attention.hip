@@ -129,7 +129,7 @@ k_attn_blocks(const float* __restrict__ q, const float* __restrict__ kcache,
 __global__ void __launch_bounds__(256)
 k_attn_combine(const float* __restrict__ PM, const float* __restrict__ PT,
     const float* __restrict__ PA, const lh_step_params* __restrict__ params, uint32_t capacity,
-    uint32_t parts, float* __restrict__ out)
+    uint32_t parts, float* __restrict__ out, uint16_t* __restrict__ xs, uint32_t xs_tokens)
 {
     __shared__ float wmax[4];
     __shared__ float fs[ROUND], ts[ROUND];
@@ -213,8 +213,13 @@ k_attn_combine(const float* __restrict__ PM, const float* __restrict__ PT,
         __syncthreads();
     }
     if (tid < 32) {
-        reinterpret_cast<float4*>(out + (size_t)t * LH_QUERY + h * LH_HEAD_DIM)[c] =
-            make_float4(A.x / T, A.y / T, A.z / T, A.w / T);
+        const float4 o = make_float4(A.x / T, A.y / T, A.z / T, A.w / T);
+        const size_t at = (size_t)t * LH_QUERY + h * LH_HEAD_DIM + 4 * c;
+        if (xs) {
+            store_split4(xs, (size_t)xs_tokens * LH_QUERY, at, o);
+        } else {
+            *reinterpret_cast<float4*>(out + at) = o;
+        }
     }
 }
 
@@ -248,7 +253,7 @@ extern "C" int lh_launch_attention(const float* q, const float* kcache_layer,
     hipLaunchKernelGGL(k_attn_blocks, dim3(lh_attention_blocks(length, count), LH_KV_HEADS, count),
         dim3(256), 0, s, q, kcache_layer, vcache_layer, params, capacity, PM, PT, PA);
     hipLaunchKernelGGL(k_attn_combine, dim3(LH_HEADS, count), dim3(256), 0, s, PM, PT, PA, params,
-        capacity, 0u, out);
+        capacity, 0u, out, (uint16_t*)nullptr, 0u);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -287,7 +292,9 @@ extern "C" int lh_launch_embed(const uint16_t* E, const lh_step_params* params, 
 // out = O / l. grid (ceil(count/16), 8, splits), block 256. With splits > 1
 // split z takes a contiguous range of the tile's blocks and writes its
 // unnormalized (max, sum, O) rows as part z of PM/PT/PA (partial stride
-// capacity/64 per (token, head)), merged by k_attn_combine.
+// capacity/64 per (token, head)), merged by k_attn_combine. With xs set, the
+// output goes to xs as the hi/mid/lo BF16 planes the o-projection GEMM reads
+// (plane stride xs_tokens * 4096) instead of FP32 rows of out.
 namespace lh {
 
 constexpr uint32_t FA_TQ = 16;                      // tokens per workgroup
@@ -316,7 +323,8 @@ __device__ __forceinline__ float quad16_sum(float v)
 __global__ void __launch_bounds__(256)
 k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
     const float* __restrict__ vcache, uint32_t length, uint32_t count, uint32_t capacity,
-    float* __restrict__ PM, float* __restrict__ PT, float* __restrict__ PA, float* __restrict__ out)
+    float* __restrict__ PM, float* __restrict__ PT, float* __restrict__ PA, float* __restrict__ out,
+    uint16_t* __restrict__ xs, uint32_t xs_tokens)
 {
     __shared__ __attribute__((aligned(16))) float Ks[LH_ATTN_BLOCK * FA_KS];
     __shared__ float Vs[LH_ATTN_BLOCK * FA_VS];
@@ -463,10 +471,14 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
             continue;
         }
         if (splits == 1) {
-            float* dst = out + (size_t)t * LH_QUERY + head * LH_HEAD_DIM + l16;
+            const size_t at = (size_t)t * LH_QUERY + head * LH_HEAD_DIM + l16;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                dst[16 * i] = o[i][r] / l[r];
+                if (xs) {
+                    store_split1(xs, (size_t)xs_tokens * LH_QUERY, at + 16 * i, o[i][r] / l[r]);
+                } else {
+                    out[at + 16 * i] = o[i][r] / l[r];
+                }
             }
         } else {
             const size_t part = ((size_t)t * LH_HEADS + head) * nbc + z;
@@ -487,9 +499,11 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
 
 extern "C" int lh_launch_attention_mfma(const float* q, const float* kcache_layer,
     const float* vcache_layer, const lh_step_params* params, uint32_t length, uint32_t count,
-    uint32_t capacity, float* PM, float* PT, float* PA, float* out, hipStream_t s)
+    uint32_t capacity, float* PM, float* PT, float* PA, float* out, uint16_t* xs, uint32_t xs_tokens,
+    hipStream_t s)
 {
-    if (!count || capacity % LH_ATTN_BLOCK || length + count > capacity) {
+    if (!count || capacity % LH_ATTN_BLOCK || length + count > capacity ||
+        (xs && xs_tokens < count)) {
         return -1;
     }
     // KV splits so that about 256 workgroups run: each takes at least 4
@@ -501,10 +515,10 @@ extern "C" int lh_launch_attention_mfma(const float* q, const float* kcache_laye
     splits = splits < by_length ? splits : by_length;
     splits = splits ? splits : 1;
     hipLaunchKernelGGL(lh::k_attn_mfma, dim3(tiles, LH_KV_HEADS, splits), dim3(256), 0, s, q,
-        kcache_layer, vcache_layer, length, count, capacity, PM, PT, PA, out);
+        kcache_layer, vcache_layer, length, count, capacity, PM, PT, PA, out, xs, xs_tokens);
     if (splits > 1) {
         hipLaunchKernelGGL(lh::k_attn_combine, dim3(LH_HEADS, count), dim3(256), 0, s, PM, PT, PA,
-            params, capacity, splits, out);
+            params, capacity, splits, out, xs, xs_tokens);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

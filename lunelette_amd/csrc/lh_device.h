@@ -116,4 +116,41 @@ __device__ __forceinline__ float silu(float v)
     return v / (1.0f + expf_cw(-v));
 }
 
+// Exact split x = hi + mid + lo into three BF16 values (truncations; each
+// residual is exact in FP32 because each step removes the leading 8
+// significant bits), returned as 16-bit patterns.
+struct bf16x3 {
+    uint32_t hi, mid, lo;
+};
+
+__device__ __forceinline__ bf16x3 split3(float x)
+{
+    const uint32_t xb = __float_as_uint(x);
+    const uint32_t hb = xb & 0xffff0000u;
+    const float r1 = x - __uint_as_float(hb);
+    const uint32_t mb = __float_as_uint(r1) & 0xffff0000u;
+    const float r2 = r1 - __uint_as_float(mb);
+    return {hb >> 16, mb >> 16, __float_as_uint(r2) >> 16};
+}
+
+// Four consecutive values split into the hi/mid/lo planes of xs (plane
+// stride `plane` elements), one 8-byte store per plane; `at` is a multiple of 4.
+__device__ __forceinline__ void store_split4(uint16_t* xs, size_t plane, size_t at, float4 v)
+{
+    const bf16x3 a = split3(v.x), b = split3(v.y), c = split3(v.z), d = split3(v.w);
+    *reinterpret_cast<uint2*>(xs + at) = make_uint2(a.hi | (b.hi << 16), c.hi | (d.hi << 16));
+    *reinterpret_cast<uint2*>(xs + plane + at) =
+        make_uint2(a.mid | (b.mid << 16), c.mid | (d.mid << 16));
+    *reinterpret_cast<uint2*>(xs + 2 * plane + at) =
+        make_uint2(a.lo | (b.lo << 16), c.lo | (d.lo << 16));
+}
+
+__device__ __forceinline__ void store_split1(uint16_t* xs, size_t plane, size_t at, float v)
+{
+    const bf16x3 a = split3(v);
+    xs[at] = (uint16_t)a.hi;
+    xs[plane + at] = (uint16_t)a.mid;
+    xs[2 * plane + at] = (uint16_t)a.lo;
+}
+
 }  // namespace lh

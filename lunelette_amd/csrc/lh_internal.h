@@ -30,10 +30,12 @@ int lh_launch_rmsnorm(const float *gamma, const float *x, float *out, uint32_t w
 int lh_launch_attention(const float *q, const float *kcache_layer, const float *vcache_layer,
     const lh_step_params *params, uint32_t length, uint32_t count, uint32_t capacity, float *PM,
     float *PT, float *PA, float *out, hipStream_t s);
-/* Matrix-core attention for multi-token steps (tolerance path). */
+/* Matrix-core attention for multi-token steps (tolerance path). With xs set
+ * the output goes to the BF16 hi/mid/lo planes of xs (token stride xs_tokens)
+ * instead of FP32 rows of out. */
 int lh_launch_attention_mfma(const float *q, const float *kcache_layer, const float *vcache_layer,
     const lh_step_params *params, uint32_t length, uint32_t count, uint32_t capacity, float *PM,
-    float *PT, float *PA, float *out, hipStream_t s);
+    float *PT, float *PA, float *out, uint16_t *xs, uint32_t xs_tokens, hipStream_t s);
 /* Block-grid width of the attention kernel, and its function (graph updates). */
 uint32_t lh_attention_blocks(uint32_t length, uint32_t count);
 const void *lh_attention_blocks_kernel(void);

@@ -29,9 +29,12 @@ struct lh_workspace {
 #ifdef __cplusplus
 extern "C" {
 #endif
-/* Multi-token layer with MFMA GEMM projections (mfma.hip). */
+/* Multi-token layer with MFMA GEMM projections (mfma.hip). input_split: the
+ * workspace split already holds input_norm(x) (written by the previous layer
+ * called with next_norm = this layer's input norm); next_norm: also leave the
+ * split of next_norm(x) for the following layer (NULL for the last layer). */
 int lh_layer_forward_mfma(const lh_layer_weights *w, float *d_x, float *d_keys,
-    float *d_values, lh_workspace *ws, hipStream_t s);
+    float *d_values, lh_workspace *ws, int input_split, const float *next_norm, hipStream_t s);
 /* Allocates the MFMA path's extra workspace buffers (idempotent). */
 int lh_mfma_prepare(lh_workspace *ws);
 #ifdef __cplusplus

@@ -33,6 +33,8 @@
 
 #include <stdlib.h>
 
+#include <type_traits>
+
 namespace lh {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -45,132 +47,180 @@ constexpr uint32_t BK = 64;               // columns per main-loop step
 constexpr uint32_t LDS_STRIDE = BK + 8;   // BF16 elements per LDS weight row
 constexpr uint32_t MAX_N = 2 * LH_INNER;  // widest GEMM: gate|up
 
-// Exact split of x into hi + mid + lo BF16 (truncations; the residuals are
-// exact in FP32 because each step removes the leading 8 significant bits).
-__device__ __forceinline__ void split3(float x, uint16_t out[3])
+// Sum of S split-K partials in split order ((p0 + p1) + p2) + ..., all loads
+// issued before the first add. p points at split 0; stride4 is the split
+// stride in float4 units.
+template <int S>
+__device__ __forceinline__ float4 sum_splits(const float4* __restrict__ p, size_t stride4)
 {
-    const uint32_t xb = __float_as_uint(x);
-    const uint32_t hb = xb & 0xffff0000u;
-    const float r1 = x - __uint_as_float(hb);
-    const uint32_t mb = __float_as_uint(r1) & 0xffff0000u;
-    const float r2 = r1 - __uint_as_float(mb);
-    out[0] = (uint16_t)(hb >> 16);
-    out[1] = (uint16_t)(mb >> 16);
-    out[2] = (uint16_t)(__float_as_uint(r2) >> 16);
+    float4 v[S];
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        v[s] = p[s * stride4];
+    }
+    float4 acc = v[0];
+#pragma unroll
+    for (int s = 1; s < S; s++) {
+        acc.x = acc.x + v[s].x;
+        acc.y = acc.y + v[s].y;
+        acc.z = acc.z + v[s].z;
+        acc.w = acc.w + v[s].w;
+    }
+    return acc;
 }
 
-__device__ __forceinline__ void store_split(uint16_t* xs, size_t plane, size_t at, float v)
+// xs[p][m][k] for p < 3 from FP32 rows, no normalization. grid (count,
+// ceil(width / 2048)), block 256: thread j of the row takes columns
+// 8j .. 8j+7 (width a multiple of 8, rows 16-byte aligned).
+__global__ void __launch_bounds__(256)
+k_split(const float* __restrict__ x, uint16_t* __restrict__ xs, uint32_t width,
+    uint32_t stride_tokens)
 {
-    uint16_t parts[3];
-    split3(v, parts);
-    xs[at] = parts[0];
-    xs[plane + at] = parts[1];
-    xs[2 * plane + at] = parts[2];
+    const uint32_t t = blockIdx.x, j = blockIdx.y * 256 + threadIdx.x;
+    if (8 * j >= width) {
+        return;
+    }
+    const float4* row = reinterpret_cast<const float4*>(x + (size_t)t * width);
+    const float4 a = row[2 * j], b = row[2 * j + 1];
+    const size_t plane = (size_t)stride_tokens * width, at = (size_t)t * width + 8 * j;
+    store_split4(xs, plane, at, a);
+    store_split4(xs, plane, at + 4, b);
 }
 
-// xs[p][m][k] for p < 3 from FP32 rows, optionally RMS-normalized with the
-// canonical schedule first (so the MFMA path sees the same normalized values
-// as the decode path). grid (count), block 64*ceil(width/1024) (<= 16 waves).
-__global__ void __launch_bounds__(1024)
-k_split(const float* __restrict__ gamma, const float* __restrict__ x, uint16_t* __restrict__ xs,
-    uint32_t width, uint32_t stride_tokens)
+// One token row of 3072 per workgroup: with S > 0, the split-K residual
+// combine x[t] = x[t] + scale * (((p0 + p1) + p2) + ...) (the o and down
+// projections, src/metal_encode.m:160,175), written back; then the canonical
+// RMSNorm of the (updated) row, y = gamma * (x * r) with ss by the row-dot
+// schedule (w = x) and r = 1/sqrt(ss/n + 1e-5), the same normalized values the
+// decode kernels compute, split into the hi/mid/lo planes of xs for the next
+// GEMM. S = 0 only normalizes (the first layer's input norm). grid (count),
+// block 768: thread i owns columns 4i .. 4i+3.
+template <int S>
+__global__ void __launch_bounds__(768)
+k_residual_norm_split(const float* __restrict__ partial, size_t split_stride, float scale,
+    float* __restrict__ x, const float* __restrict__ gamma, uint16_t* __restrict__ xs,
+    uint32_t stride_tokens)
 {
-    __shared__ float lds_ss[16];
+    // Row in the [chunk][quad][lane] 16-byte-word layout: lane l's 16 values
+    // of chunk c (columns c*1024 + 16l .. +15) are words (4c + q)*64 + l.
+    __shared__ float4 row_l[LH_HIDDEN / 4];
     __shared__ float r_s;
-    const uint32_t t = blockIdx.x;
-    const float* row = x + (size_t)t * width;
-    float r = 1.0f;
-    if (gamma) {
-        const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-        const uint32_t nch = (width + LH_CHUNK - 1) / LH_CHUNK;
-        const uint32_t col = wave * LH_CHUNK + lane * LH_LANE_COLS;
+    const uint32_t t = blockIdx.x, tid = threadIdx.x;
+    float4* xr = reinterpret_cast<float4*>(x + (size_t)t * LH_HIDDEN);
+    const float4 g = reinterpret_cast<const float4*>(gamma)[tid];
+    float4 v = xr[tid];
+    if constexpr (S > 0) {
+        const float4 acc = sum_splits<S>(
+            reinterpret_cast<const float4*>(partial + (size_t)t * LH_HIDDEN) + tid,
+            split_stride / 4);
+        v.x = v.x + acc.x * scale;
+        v.y = v.y + acc.y * scale;
+        v.z = v.z + acc.z * scale;
+        v.w = v.w + acc.w * scale;
+        xr[tid] = v;
+    }
+    const uint32_t c = tid >> 8, w = tid & 255;
+    row_l[(4 * c + (w & 3)) * 64 + (w >> 2)] = v;
+    __syncthreads();
+    if (tid < 64) {
         float acc = 0.0f;
-        for (uint32_t j = 0; j < 16 && col + j < width; j++) {
-            acc = __builtin_fmaf(row[col + j], row[col + j], acc);
+#pragma unroll
+        for (int k = 0; k < LH_HIDDEN / 256; k++) {
+            const float4 u = row_l[k * 64 + tid];
+            acc = __builtin_fmaf(u.x, u.x, acc);
+            acc = __builtin_fmaf(u.y, u.y, acc);
+            acc = __builtin_fmaf(u.z, u.z, acc);
+            acc = __builtin_fmaf(u.w, u.w, acc);
         }
-        acc = wave_tree64(acc);
-        if (lane == 0) {
-            lds_ss[wave] = acc;
+        const float ss = wave_tree64(acc);
+        if (tid == 0) {
+            r_s = 1.0f / __builtin_sqrtf(ss / (float)LH_HIDDEN + 1e-5f);
         }
-        __syncthreads();
-        if (threadIdx.x == 0) {
-            float ss = lds_ss[0];
-            for (uint32_t c = 1; c < nch; c++) {
-                ss = ss + lds_ss[c];
-            }
-            r_s = 1.0f / __builtin_sqrtf(ss / (float)width + 1e-5f);
-        }
-        __syncthreads();
-        r = r_s;
     }
-    const size_t plane = (size_t)stride_tokens * width;
-    for (uint32_t c = threadIdx.x; c < width; c += blockDim.x) {
-        const float v = gamma ? gamma[c] * (row[c] * r) : row[c];
-        store_split(xs, plane, (size_t)t * width + c, v);
-    }
+    __syncthreads();
+    const float r = r_s;
+    store_split4(xs, (size_t)stride_tokens * LH_HIDDEN, (size_t)t * LH_HIDDEN + 4 * tid,
+        make_float4(g.x * (v.x * r), g.y * (v.y * r), g.z * (v.z * r), g.w * (v.w * r)));
 }
 
 // Down-projection input: SiLU(s_g * gate) * (s_u * up) (src/metal_encode.m:
 // 162-171) from the gate|up GEMM partials P[s][m][0..18432) (gate rows first),
-// summed in split order, split into BF16 planes. grid (count), block 256.
+// summed in split order, split into BF16 planes. grid (count, 5), block 256:
+// thread j < 1152 of the row takes inner columns 8j .. 8j+7.
+template <int S>
 __global__ void __launch_bounds__(256)
-k_split_silu(const float* __restrict__ partial, uint32_t splits, size_t split_stride,
-    float2 scales, uint16_t* __restrict__ xs, uint32_t stride_tokens)
+k_split_silu(const float* __restrict__ partial, size_t split_stride, float2 scales,
+    uint16_t* __restrict__ xs, uint32_t stride_tokens)
 {
-    const uint32_t t = blockIdx.x;
-    const size_t plane = (size_t)stride_tokens * LH_INNER;
-    const float* row = partial + (size_t)t * MAX_N;
-    for (uint32_t i = threadIdx.x; i < LH_INNER; i += 256) {
-        float g = row[i], u = row[LH_INNER + i];
-        for (uint32_t s = 1; s < splits; s++) {
-            g = g + row[s * split_stride + i];
-            u = u + row[s * split_stride + LH_INNER + i];
-        }
-        store_split(xs, plane, (size_t)t * LH_INNER + i, silu(g * scales.x) * (u * scales.y));
+    const uint32_t t = blockIdx.x, j = blockIdx.y * 256 + threadIdx.x;
+    if (8 * j >= LH_INNER) {
+        return;
     }
+    const float4* row = reinterpret_cast<const float4*>(partial + (size_t)t * MAX_N) + 2 * j;
+    const size_t s4 = split_stride / 4;
+    const float4 g0 = sum_splits<S>(row, s4), g1 = sum_splits<S>(row + 1, s4);
+    const float4 u0 = sum_splits<S>(row + LH_INNER / 4, s4);
+    const float4 u1 = sum_splits<S>(row + LH_INNER / 4 + 1, s4);
+    const float sg = scales.x, su = scales.y;
+    const size_t plane = (size_t)stride_tokens * LH_INNER, at = (size_t)t * LH_INNER + 8 * j;
+    store_split4(xs, plane, at,
+        make_float4(silu(g0.x * sg) * (u0.x * su), silu(g0.y * sg) * (u0.y * su),
+            silu(g0.z * sg) * (u0.z * su), silu(g0.w * sg) * (u0.w * su)));
+    store_split4(xs, plane, at + 4,
+        make_float4(silu(g1.x * sg) * (u1.x * su), silu(g1.y * sg) * (u1.y * su),
+            silu(g1.z * sg) * (u1.z * su), silu(g1.w * sg) * (u1.w * su)));
 }
 
 // q|k|v epilogue (src/metal_encode.m:129-153): partials P[s][m][0..6144)
 // summed in split order, per-tensor scale, RoPE (column i < 64 rotates with
 // -x[i+64], column i+64 with x[i]) and the query factor on Q; Q to qout, K and
-// V appended to the cache at position length + m. grid (count), block 256.
+// V appended to the cache at position length + m. grid (count, 3), block 256:
+// thread j < 768 of the row takes pairs i0 .. i0+3 of head j/16, i0 = 4(j%16).
+template <int S>
 __global__ void __launch_bounds__(256)
-k_qkv_epilogue(const float* __restrict__ partial, uint32_t splits, size_t split_stride,
-    float3 scales, const lh_step_params* __restrict__ params, float* __restrict__ qout,
+k_qkv_epilogue(const float* __restrict__ partial, size_t split_stride, float3 scales,
+    const lh_step_params* __restrict__ params, float* __restrict__ qout,
     float* __restrict__ kcache, float* __restrict__ vcache, uint32_t capacity)
 {
-    const uint32_t t = blockIdx.x;
-    const float* row = partial + (size_t)t * LH_QKV_ROWS;
-    const lh_token_params* tp = &params->tokens[t];
+    const uint32_t t = blockIdx.x, j = blockIdx.y * 256 + threadIdx.x;
+    const uint32_t head = j >> 4, i0 = (j & 15) * 4;
+    const float4* row = reinterpret_cast<const float4*>(partial + (size_t)t * LH_QKV_ROWS);
+    const size_t s4 = split_stride / 4;
+    const uint32_t n4 = (head * 128 + i0) / 4;
+    float4 lo = sum_splits<S>(row + n4, s4), hi = sum_splits<S>(row + n4 + 16, s4);
+    const float scale = head < 32 ? scales.x : (head < 40 ? scales.y : scales.z);
+    lo = make_float4(lo.x * scale, lo.y * scale, lo.z * scale, lo.w * scale);
+    hi = make_float4(hi.x * scale, hi.y * scale, hi.z * scale, hi.w * scale);
     const uint32_t position = params->length + t;
-    for (uint32_t pair = threadIdx.x; pair < LH_QKV_ROWS / 2; pair += 256) {
-        const uint32_t head = pair >> 6, i = pair & 63;
-        const uint32_t n = head * 128 + i;
-        float lo = row[n], hi = row[n + 64];
-        for (uint32_t s = 1; s < splits; s++) {
-            lo = lo + row[s * split_stride + n];
-            hi = hi + row[s * split_stride + n + 64];
-        }
-        const float scale = head < 32 ? scales.x : (head < 40 ? scales.y : scales.z);
-        lo = lo * scale;
-        hi = hi * scale;
-        if (head < 40) {
-            const float out_lo = lo * tp->cosine[i] + (-hi) * tp->sine[i];
-            const float out_hi = hi * tp->cosine[i + 64] + lo * tp->sine[i + 64];
-            if (head < 32) {
-                float* qh = qout + (size_t)t * LH_QUERY + head * 128;
-                qh[i] = out_lo * tp->qfactor;
-                qh[i + 64] = out_hi * tp->qfactor;
-            } else {
-                float* kr = kcache + lh_kv_index(capacity, 0, head - 32, position);
-                kr[i] = out_lo;
-                kr[i + 64] = out_hi;
-            }
-        } else {
-            float* vr = vcache + lh_kv_index(capacity, 0, head - 40, position);
-            vr[i] = lo;
-            vr[i + 64] = hi;
-        }
+    if (head >= 40) {
+        float4* vr = reinterpret_cast<float4*>(vcache + lh_kv_index(capacity, 0, head - 40, position));
+        vr[i0 / 4] = lo;
+        vr[i0 / 4 + 16] = hi;
+        return;
+    }
+    const lh_token_params* tp = &params->tokens[t];
+    const float4 cl = *reinterpret_cast<const float4*>(tp->cosine + i0);
+    const float4 ch = *reinterpret_cast<const float4*>(tp->cosine + i0 + 64);
+    const float4 sl = *reinterpret_cast<const float4*>(tp->sine + i0);
+    const float4 sh = *reinterpret_cast<const float4*>(tp->sine + i0 + 64);
+    float4 out_lo, out_hi;
+    out_lo.x = lo.x * cl.x + (-hi.x) * sl.x;
+    out_lo.y = lo.y * cl.y + (-hi.y) * sl.y;
+    out_lo.z = lo.z * cl.z + (-hi.z) * sl.z;
+    out_lo.w = lo.w * cl.w + (-hi.w) * sl.w;
+    out_hi.x = hi.x * ch.x + lo.x * sh.x;
+    out_hi.y = hi.y * ch.y + lo.y * sh.y;
+    out_hi.z = hi.z * ch.z + lo.z * sh.z;
+    out_hi.w = hi.w * ch.w + lo.w * sh.w;
+    if (head < 32) {
+        const float f = tp->qfactor;
+        float4* qh = reinterpret_cast<float4*>(qout + (size_t)t * LH_QUERY + head * 128);
+        qh[i0 / 4] = make_float4(out_lo.x * f, out_lo.y * f, out_lo.z * f, out_lo.w * f);
+        qh[i0 / 4 + 16] = make_float4(out_hi.x * f, out_hi.y * f, out_hi.z * f, out_hi.w * f);
+    } else {
+        float4* kr = reinterpret_cast<float4*>(kcache + lh_kv_index(capacity, 0, head - 32, position));
+        kr[i0 / 4] = out_lo;
+        kr[i0 / 4 + 16] = out_hi;
     }
 }
 
@@ -327,23 +377,28 @@ k_gemm(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint32_t 
     }
 }
 
-// x[m][n] = x[m][n] + scale * (((p0 + p1) + p2) + ...): deterministic split-K
-// combine with the residual add (src/metal_encode.m:160,175); without the
-// residual, x[m][n] = scale * (...). Partials P[s][m][n] with split stride
-// stride_tokens * rows.
-__global__ void k_combine_residual(const float* __restrict__ partial, uint32_t splits,
-    uint32_t rows, uint32_t count, uint32_t stride_tokens, float scale, float* __restrict__ x,
-    int residual)
+// x[i] = x[i] + scale * (((p0 + p1) + p2) + ...) (deterministic split-K
+// combine with the residual add, src/metal_encode.m:160,175); without the
+// residual, x[i] = scale * (...). Partials P[s][i] with split stride
+// split_stride; i runs over count * rows in float4 units. grid
+// ceil(count * rows / 1024), block 256.
+template <int S>
+__global__ void __launch_bounds__(256)
+k_combine_residual(const float* __restrict__ partial, size_t split_stride, size_t n4, float scale,
+    float* __restrict__ x, int residual)
 {
-    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= (size_t)count * rows) {
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= n4) {
         return;
     }
-    float acc = partial[i];
-    for (uint32_t s = 1; s < splits; s++) {
-        acc = acc + partial[(size_t)s * stride_tokens * rows + i];
+    const float4 acc = sum_splits<S>(reinterpret_cast<const float4*>(partial) + i, split_stride / 4);
+    float4* xr = reinterpret_cast<float4*>(x) + i;
+    float4 v = make_float4(acc.x * scale, acc.y * scale, acc.z * scale, acc.w * scale);
+    if (residual) {
+        const float4 o = *xr;
+        v = make_float4(o.x + v.x, o.y + v.y, o.z + v.z, o.w + v.w);
     }
-    x[i] = residual ? x[i] + acc * scale : acc * scale;
+    *xr = v;
 }
 
 }  // namespace lh
@@ -397,12 +452,49 @@ extern "C" int lh_mfma_prepare(lh_workspace* ws)
     return 0;
 }
 
-static int split_rows(const float* gamma, const float* x, uint16_t* xs, uint32_t width,
-    uint32_t count, uint32_t stride, hipStream_t s)
+// Calls f(std::integral_constant<int, S>) for the split count S, which the
+// elementwise kernels take as a template argument so that every partial load
+// issues before the first add. S = 0 (no partials) only where ZERO is set.
+template <bool ZERO = false, typename F>
+static int with_splits(uint32_t splits, const char* what, F&& f)
 {
-    const uint32_t nch = (width + LH_CHUNK - 1) / LH_CHUNK;
-    hipLaunchKernelGGL(k_split, dim3(count), dim3(64 * nch), 0, s, gamma, x, xs, width, stride);
+    switch (splits) {
+    case 0:
+        if constexpr (ZERO) {
+            f(std::integral_constant<int, 0>{});
+            break;
+        }
+        lh_set_error("%s: no partials", what);
+        return -1;
+    case 1: f(std::integral_constant<int, 1>{}); break;
+    case 2: f(std::integral_constant<int, 2>{}); break;
+    case 4: f(std::integral_constant<int, 4>{}); break;
+    case 8: f(std::integral_constant<int, 8>{}); break;
+    case 16: f(std::integral_constant<int, 16>{}); break;
+    default:
+        lh_set_error("%s: unsupported split count %u", what, splits);
+        return -1;
+    }
+    return launched_ok(what);
+}
+
+static int split_rows(const float* x, uint16_t* xs, uint32_t width, uint32_t count,
+    uint32_t stride, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_split, dim3(count, (width / 8 + 255) / 256), dim3(256), 0, s, x, xs,
+        width, stride);
     return launched_ok("split");
+}
+
+// x = x + scale * sum of `splits` partials (0: x unchanged), then the RMSNorm
+// of x with gamma split into xs; rows of 3072.
+static int residual_norm_split(const float* partial, uint32_t splits, uint32_t stride,
+    float scale, float* x, const float* gamma, uint16_t* xs, uint32_t count, hipStream_t s)
+{
+    return with_splits<true>(splits, "residual norm split", [&](auto S) {
+        hipLaunchKernelGGL(k_residual_norm_split<decltype(S)::value>, dim3(count), dim3(768), 0, s,
+            partial, (size_t)stride * LH_HIDDEN, scale, x, gamma, xs, stride);
+    });
 }
 
 // P[s][m][n] for n < N over `splits` equal K ranges. N / (16*NF) must be a
@@ -427,10 +519,12 @@ static int gemm(const uint8_t* W0, const uint8_t* W1, uint32_t boundary, uint32_
 static int combine(const float* partial, uint32_t splits, uint32_t rows, uint32_t count,
     uint32_t stride, float scale, float* x, int residual, hipStream_t s)
 {
-    const size_t n = (size_t)count * rows;
-    hipLaunchKernelGGL(k_combine_residual, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, s,
-        partial, splits, rows, count, stride, scale, x, residual);
-    return launched_ok("split-K combine");
+    const size_t n4 = (size_t)count * rows / 4;
+    return with_splits(splits, "split-K combine", [&](auto S) {
+        hipLaunchKernelGGL(k_combine_residual<decltype(S)::value>,
+            dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, partial,
+            (size_t)stride * rows, n4, scale, x, residual);
+    });
 }
 
 // K splits giving about 512 workgroups: `base` for two token tiles, twice as
@@ -459,7 +553,7 @@ extern "C" int lh_fp8_gemm(lh_workspace* ws, const uint8_t* d_w, float scale, co
     hipStream_t s = (hipStream_t)stream;
     const uint32_t B = padded_block(ws), n = (uint32_t)tokens;
     const uint32_t splits = splits_for(n, 1);
-    if (split_rows(NULL, d_x, ws->d_split, (uint32_t)cols, n, B, s) ||
+    if (split_rows(d_x, ws->d_split, (uint32_t)cols, n, B, s) ||
         gemm<4>(d_w, NULL, (uint32_t)rows, (uint32_t)rows, (uint32_t)cols, ws->d_split, B, n,
             splits, ws->d_gemm, s)) {
         return -1;
@@ -467,8 +561,12 @@ extern "C" int lh_fp8_gemm(lh_workspace* ws, const uint8_t* d_w, float scale, co
     return combine(ws->d_gemm, splits, (uint32_t)rows, n, B, scale, d_y, 0, s);
 }
 
+// One layer over ws->count tokens. input_split: ws->d_split already holds the
+// BF16 split of input_norm(x) (the previous layer's last kernel wrote it);
+// next_norm: the last kernel also writes the split of next_norm(x) for the
+// following layer (NULL: plain residual combine).
 extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, float* d_keys,
-    float* d_values, lh_workspace* ws, hipStream_t s)
+    float* d_values, lh_workspace* ws, int input_split, const float* next_norm, hipStream_t s)
 {
     if (!w->qkv || !w->o || !w->gate || !w->up || !w->down) {
         lh_set_error("MFMA path needs compact FP8 weights");
@@ -480,40 +578,46 @@ extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, floa
     const uint32_t n = (uint32_t)ws->count, C = (uint32_t)ws->capacity;
     const uint32_t B = padded_block(ws);
     float* P = ws->d_gemm;
-    // q|k|v: 6144 rows in tiles of 96, 3072 columns.
+    uint16_t* xs = ws->d_split;
+    // q|k|v: 6144 rows in tiles of 96, 3072 columns; scales, RoPE and the KV
+    // append in the epilogue.
     const uint32_t sq = splits_for(n, 4);
-    if (split_rows(w->input_norm, d_x, ws->d_split, LH_HIDDEN, n, B, s) ||
-        gemm<6>(w->qkv, NULL, LH_QKV_ROWS, LH_QKV_ROWS, LH_HIDDEN, ws->d_split, B, n, sq, P, s)) {
+    if ((!input_split &&
+            residual_norm_split(NULL, 0, B, 1.0f, d_x, w->input_norm, xs, n, s)) ||
+        gemm<6>(w->qkv, NULL, LH_QKV_ROWS, LH_QKV_ROWS, LH_HIDDEN, xs, B, n, sq, P, s) ||
+        with_splits(sq, "qkv epilogue", [&](auto S) {
+            hipLaunchKernelGGL(k_qkv_epilogue<decltype(S)::value>, dim3(n, 3), dim3(256), 0, s,
+                P, (size_t)B * LH_QKV_ROWS, make_float3(w->scale[0], w->scale[1], w->scale[2]),
+                ws->d_params, ws->d_q, d_keys, d_values, C);
+        })) {
         return -1;
     }
-    hipLaunchKernelGGL(k_qkv_epilogue, dim3(n), dim3(256), 0, s, P, sq,
-        (size_t)B * LH_QKV_ROWS, make_float3(w->scale[0], w->scale[1], w->scale[2]),
-        ws->d_params, ws->d_q, d_keys, d_values, C);
-    // o: 3072 rows in tiles of 96, 4096 columns, residual.
+    // Attention writes the o projection's input split; o: 3072 rows in tiles
+    // of 96, 4096 columns; residual, post-norm and the gate|up split after it.
     const uint32_t so = splits_for(n, 8);
-    if (launched_ok("qkv epilogue") ||
-        lh_launch_attention_mfma(ws->d_q, d_keys, d_values, ws->d_params, (uint32_t)ws->length,
-            n, C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_attn, s) ||
-        split_rows(NULL, ws->d_attn, ws->d_split, LH_QUERY, n, B, s) ||
-        gemm<6>(w->o, NULL, LH_HIDDEN, LH_HIDDEN, LH_QUERY, ws->d_split, B, n, so, P, s) ||
-        combine(P, so, LH_HIDDEN, n, B, w->scale[3], d_x, 1, s)) {
+    if (lh_launch_attention_mfma(ws->d_q, d_keys, d_values, ws->d_params, (uint32_t)ws->length,
+            n, C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_attn, xs, B, s) ||
+        launched_ok("attention") ||
+        gemm<6>(w->o, NULL, LH_HIDDEN, LH_HIDDEN, LH_QUERY, xs, B, n, so, P, s) ||
+        residual_norm_split(P, so, B, w->scale[3], d_x, w->post_norm, xs, n, s)) {
         return -1;
     }
     // gate|up: 18432 rows in tiles of 144, 3072 columns; SiLU(gate)*up in the
     // down projection's split.
     const uint32_t sg = splits_for(n, 2);
-    if (split_rows(w->post_norm, d_x, ws->d_split, LH_HIDDEN, n, B, s) ||
-        gemm<9>(w->gate, w->up, LH_INNER, MAX_N, LH_HIDDEN, ws->d_split, B, n, sg, P, s)) {
+    if (gemm<9>(w->gate, w->up, LH_INNER, MAX_N, LH_HIDDEN, xs, B, n, sg, P, s) ||
+        with_splits(sg, "silu split", [&](auto S) {
+            hipLaunchKernelGGL(k_split_silu<decltype(S)::value>, dim3(n, 5), dim3(256), 0, s, P,
+                (size_t)B * MAX_N, make_float2(w->scale[4], w->scale[5]), xs, B);
+        })) {
         return -1;
     }
-    hipLaunchKernelGGL(k_split_silu, dim3(n), dim3(256), 0, s, P, sg, (size_t)B * MAX_N,
-        make_float2(w->scale[4], w->scale[5]), ws->d_split, B);
-    // down: 3072 rows in tiles of 96, 9216 columns, residual.
+    // down: 3072 rows in tiles of 96, 9216 columns, residual (and the next
+    // layer's input split).
     const uint32_t sd = splits_for(n, 8);
-    if (launched_ok("silu split") ||
-        gemm<6>(w->down, NULL, LH_HIDDEN, LH_HIDDEN, LH_INNER, ws->d_split, B, n, sd, P, s) ||
-        combine(P, sd, LH_HIDDEN, n, B, w->scale[6], d_x, 1, s)) {
+    if (gemm<6>(w->down, NULL, LH_HIDDEN, LH_HIDDEN, LH_INNER, xs, B, n, sd, P, s)) {
         return -1;
     }
-    return 0;
+    return next_norm ? residual_norm_split(P, sd, B, w->scale[6], d_x, next_norm, xs, n, s)
+                     : combine(P, sd, LH_HIDDEN, n, B, w->scale[6], d_x, 1, s);
 }

@@ -611,8 +611,17 @@ static int launch_step(lh_runtime *rt, size_t count, int path, hipStream_t s)
         return -1;
     }
     for (uint32_t l = 0; l < rt->layers; l++) {
-        if (lh_layer_forward(&rt->layer[l], rt->d_x, rt->d_keys + l * per_layer,
-                rt->d_values + l * per_layer, rt->ws, path, s)) {
+        float *keys = rt->d_keys + l * per_layer, *values = rt->d_values + l * per_layer;
+        int rc;
+        if (path == LH_PATH_MFMA) {
+            /* Each layer's last kernel also splits the next layer's input. */
+            const float *next = l + 1 < rt->layers ? rt->layer[l + 1].input_norm : NULL;
+            rc = lh_layer_forward_mfma(&rt->layer[l], rt->d_x, keys, values, rt->ws, l > 0, next,
+                s);
+        } else {
+            rc = lh_layer_forward(&rt->layer[l], rt->d_x, keys, values, rt->ws, path, s);
+        }
+        if (rc) {
             return -1;
         }
     }
