@@ -123,13 +123,12 @@ k_attn_blocks(const float* __restrict__ q, const float* __restrict__ kcache,
 }
 
 // grid (32 heads, count), 256 threads: thread (c = tid & 31, s = tid >> 5)
-// owns dims 4c..4c+3 of groups s and s + 8 of each 128-block round. The
-// partials are the token's 64-position blocks (parts = 0) or `parts` KV
-// splits of the matrix-core kernel (same (max, sum, P.V) form).
+// owns dims 4c..4c+3 of groups s and s + 8 of each 128-block round; the
+// partials are the token's 64-position blocks.
 __global__ void __launch_bounds__(256)
 k_attn_combine(const float* __restrict__ PM, const float* __restrict__ PT,
     const float* __restrict__ PA, const lh_step_params* __restrict__ params, uint32_t capacity,
-    uint32_t parts, float* __restrict__ out, uint16_t* __restrict__ xs, uint32_t xs_tokens)
+    float* __restrict__ out)
 {
     __shared__ float wmax[4];
     __shared__ float fs[ROUND], ts[ROUND];
@@ -137,7 +136,7 @@ k_attn_combine(const float* __restrict__ PM, const float* __restrict__ PT,
     __shared__ float ug[ROUND / GROUP];
     const uint32_t h = blockIdx.x, t = blockIdx.y;
     const uint32_t n = params->length + t + 1;
-    const uint32_t nb = parts ? parts : (n + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
+    const uint32_t nb = (n + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
     const uint32_t nbc = capacity / LH_ATTN_BLOCK;
     const size_t th = (size_t)t * LH_HEADS + h;
     const float* pm = PM + th * nbc;
@@ -213,13 +212,8 @@ k_attn_combine(const float* __restrict__ PM, const float* __restrict__ PT,
         __syncthreads();
     }
     if (tid < 32) {
-        const float4 o = make_float4(A.x / T, A.y / T, A.z / T, A.w / T);
-        const size_t at = (size_t)t * LH_QUERY + h * LH_HEAD_DIM + 4 * c;
-        if (xs) {
-            store_split4(xs, (size_t)xs_tokens * LH_QUERY, at, o);
-        } else {
-            *reinterpret_cast<float4*>(out + at) = o;
-        }
+        reinterpret_cast<float4*>(out + (size_t)t * LH_QUERY + h * LH_HEAD_DIM)[c] =
+            make_float4(A.x / T, A.y / T, A.z / T, A.w / T);
     }
 }
 
@@ -253,7 +247,7 @@ extern "C" int lh_launch_attention(const float* q, const float* kcache_layer,
     hipLaunchKernelGGL(k_attn_blocks, dim3(lh_attention_blocks(length, count), LH_KV_HEADS, count),
         dim3(256), 0, s, q, kcache_layer, vcache_layer, params, capacity, PM, PT, PA);
     hipLaunchKernelGGL(k_attn_combine, dim3(LH_HEADS, count), dim3(256), 0, s, PM, PT, PA, params,
-        capacity, 0u, out, (uint16_t*)nullptr, 0u);
+        capacity, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -292,7 +286,7 @@ extern "C" int lh_launch_embed(const uint16_t* E, const lh_step_params* params, 
 // out = O / l. grid (ceil(count/16), 8, splits), block 256. With splits > 1
 // split z takes a contiguous range of the tile's blocks and writes its
 // unnormalized (max, sum, O) rows as part z of PM/PT/PA (partial stride
-// capacity/64 per (token, head)), merged by k_attn_combine. With xs set, the
+// capacity/64 per (token, head)), merged by k_attn_merge. With xs set, the
 // output goes to xs as the hi/mid/lo BF16 planes the o-projection GEMM reads
 // (plane stride xs_tokens * 4096) instead of FP32 rows of out.
 namespace lh {
@@ -495,6 +489,49 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
     }
 }
 
+// Merge of k_attn_mfma's KV splits (tolerance path): per (token, head)
+// M = max m_z, f_z = exp(m_z - M), out = (sum f_z O_z) / (sum f_z l_z) with
+// the sums in split order. A split whose positions are all masked for the row
+// holds m = -inf, l = 0, O = 0 and contributes nothing; split 0 always holds
+// position 0, so M is finite. grid (count * 8), block 256: one wave per
+// (token, head), lane l owns dims 2l and 2l + 1.
+__global__ void __launch_bounds__(256)
+k_attn_merge(const float* __restrict__ PM, const float* __restrict__ PT,
+    const float* __restrict__ PA, uint32_t capacity, uint32_t parts, uint32_t count,
+    float* __restrict__ out, uint16_t* __restrict__ xs, uint32_t xs_tokens)
+{
+    const uint32_t th = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (th >= count * LH_HEADS) {
+        return;
+    }
+    const uint32_t nbc = capacity / LH_ATTN_BLOCK;
+    const float* pm = PM + (size_t)th * nbc;
+    const float* pt = PT + (size_t)th * nbc;
+    const float2* pa = reinterpret_cast<const float2*>(PA + (size_t)th * nbc * LH_HEAD_DIM) + lane;
+    float M = -__builtin_inff();
+    for (uint32_t z = 0; z < parts; z++) {
+        M = fmaxf(M, pm[z]);
+    }
+    float2 A = make_float2(0.0f, 0.0f);
+    float T = 0.0f;
+    for (uint32_t z = 0; z < parts; z++) {
+        const float f = expf_cw(pm[z] - M);
+        const float2 a = pa[(size_t)z * (LH_HEAD_DIM / 2)];
+        A.x = __builtin_fmaf(f, a.x, A.x);
+        A.y = __builtin_fmaf(f, a.y, A.y);
+        T = __builtin_fmaf(f, pt[z], T);
+    }
+    const uint32_t t = th / LH_HEADS, h = th % LH_HEADS;
+    const size_t at = (size_t)t * LH_QUERY + h * LH_HEAD_DIM + 2 * lane;
+    if (xs) {
+        const size_t plane = (size_t)xs_tokens * LH_QUERY;
+        store_split1(xs, plane, at, A.x / T);
+        store_split1(xs, plane, at + 1, A.y / T);
+    } else {
+        *reinterpret_cast<float2*>(out + at) = make_float2(A.x / T, A.y / T);
+    }
+}
+
 }  // namespace lh
 
 extern "C" int lh_launch_attention_mfma(const float* q, const float* kcache_layer,
@@ -517,8 +554,8 @@ extern "C" int lh_launch_attention_mfma(const float* q, const float* kcache_laye
     hipLaunchKernelGGL(lh::k_attn_mfma, dim3(tiles, LH_KV_HEADS, splits), dim3(256), 0, s, q,
         kcache_layer, vcache_layer, length, count, capacity, PM, PT, PA, out, xs, xs_tokens);
     if (splits > 1) {
-        hipLaunchKernelGGL(lh::k_attn_combine, dim3(LH_HEADS, count), dim3(256), 0, s, PM, PT, PA,
-            params, capacity, splits, out, xs, xs_tokens);
+        hipLaunchKernelGGL(lh::k_attn_merge, dim3(count * LH_HEADS / 4), dim3(256), 0, s, PM, PT,
+            PA, capacity, splits, count, out, xs, xs_tokens);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
