@@ -8,20 +8,23 @@
 //   BF16 exactly (v_cvt_scalef32_pk_bf16_fp8, unit scale: every E4M3FN value
 //   has at most 4 significant bits). Every MFMA product is exact; the three
 //   plane products accumulate in FP32.
-// - k_gemm: a 256-thread workgroup owns 128 tokens x 16*NF weight rows of one
-//   K split. Each 64-column step, the workgroup converts its weight tile once
-//   into a double-buffered BF16 LDS tile (row stride 72 BF16, so the 16 rows a
-//   fragment load touches fall in different banks; the next step's tile is
-//   fetched during this step's MFMAs), while each wave loads its 32 tokens'
-//   activation planes straight into v_mfma_f32_16x16x32_bf16 operand
-//   registers. Lane group g = lane/16 supplies columns 16g .. 16g+15 of the
-//   step to both operands (a K permutation shared by A and B, so the sum is
-//   unchanged) as two 8-column MFMA k-slices. Register use stays under 256 so
-//   two workgroups share a CU and hide each other's loads, conversions and
-//   barriers; the grids hold about 512 workgroups (split-K where N is small).
-// - Workgroup ids map the (token tile, split) work of one weight tile onto one
-//   XCD (dispatch is round-robin over the 8 XCDs), so the tile's second read
-//   comes from that XCD's L2.
+// - k_gemm: a 256-thread workgroup owns 64 tokens x 256 weight rows of one K
+//   split; each wave owns 64 weight rows and all 64 tokens (4 x 4 MFMA
+//   tiles). Per 64-column stage the activation tile (64 tokens x 3 planes,
+//   24 KB) goes to LDS by direct loads (global_load_lds_dwordx4) in
+//   fragment-major order, so each v_mfma_f32_16x16x32_bf16 A operand is one
+//   conflict-free 16-byte LDS read, shared by the four waves; each wave's
+//   weight rows (16 FP8 codes per lane and row fragment, 16 KB per stage for
+//   the workgroup) take the same direct route into a per-lane LDS slot, and
+//   the lane converts its own codes to BF16 in registers. The next stage's
+//   loads are in flight (two LDS buffers) while the current stage's 96
+//   MFMAs per wave run. Lane group g = lane/16 supplies columns
+//   16g .. 16g+15 of the stage to both operands (a K permutation shared by
+//   A and B, so the sum is unchanged) as two 8-column k-slices. Two
+//   workgroups share a CU (80 KB LDS and <= 256 registers each).
+// - Workgroup ids deal the (weight tile, split) columns round-robin to the 8
+//   XCDs and run a column's token tiles back to back on one XCD, so the
+//   weight tile is read from HBM once per XCD and from L2 after that.
 // - Scales and epilogues live in the consumers: k_qkv_epilogue (scales, RoPE,
 //   query factor, KV append), k_split_silu (SiLU(gate)*up feeding the down
 //   projection's split) and k_combine_residual (split-K sum in split order,
@@ -42,9 +45,12 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int NSPLIT = 3;                 // BF16 planes per activation
-constexpr uint32_t BM = 128;              // tokens per workgroup tile (4 waves x 32)
-constexpr uint32_t BK = 64;               // columns per main-loop step
-constexpr uint32_t LDS_STRIDE = BK + 8;   // BF16 elements per LDS weight row
+constexpr uint32_t GM = 64;               // tokens per workgroup tile
+constexpr uint32_t GN = 256;              // weight rows per workgroup tile (4 waves x 64)
+constexpr uint32_t BK = 64;               // columns per pipeline stage
+constexpr uint32_t A_FRAGS = 4 * 3 * 2;   // 1 KB activation fragments per stage
+constexpr uint32_t W_FRAGS = 4 * 4;       // 1 KB weight fragments per stage
+constexpr uint32_t SPLIT_ROWS = 128;      // token stride granule of the split planes
 constexpr uint32_t MAX_N = 2 * LH_INNER;  // widest GEMM: gate|up
 
 // Sum of S split-K partials in split order ((p0 + p1) + p2) + ..., all loads
@@ -224,153 +230,157 @@ k_qkv_epilogue(const float* __restrict__ partial, size_t split_stride, float3 sc
     }
 }
 
-// Eight FP8 codes (two dwords) -> eight BF16 at out (16-byte aligned), exact.
-__device__ __forceinline__ void fp8x8_to_bf16(uint32_t lo, uint32_t hi, uint16_t* out)
+// FP8 -> BF16 weight fragments: the 16 codes of u (row bytes 16g .. 16g+15
+// of the step) give the two 8-column k-slices h = 0 (bytes 0..7) and h = 1.
+__device__ __forceinline__ void fp8x16_to_bf16x8x2(u32x4 u, bf16x8& lo, bf16x8& hi)
 {
-    const auto a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, false);
-    const auto b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(lo, 1.0f, true);
-    const auto c = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, false);
-    const auto d = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(hi, 1.0f, true);
-    u32x4 v;
-    v.x = __builtin_bit_cast(uint32_t, a);
-    v.y = __builtin_bit_cast(uint32_t, b);
-    v.z = __builtin_bit_cast(uint32_t, c);
-    v.w = __builtin_bit_cast(uint32_t, d);
-    *reinterpret_cast<u32x4*>(out) = v;
+    u32x4 a, b;
+    a.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(u.x, 1.0f, false));
+    a.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(u.x, 1.0f, true));
+    a.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(u.y, 1.0f, false));
+    a.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(u.y, 1.0f, true));
+    b.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(u.z, 1.0f, false));
+    b.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(u.z, 1.0f, true));
+    b.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(u.w, 1.0f, false));
+    b.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(u.w, 1.0f, true));
+    lo = __builtin_bit_cast(bf16x8, a);
+    hi = __builtin_bit_cast(bf16x8, b);
 }
 
-// grid: n_tiles * m_tiles * splits workgroups of 256 threads (n_tiles a
-// multiple of 8), two resident per CU so one workgroup's loads, conversions
-// and barriers overlap the other's MFMAs. W0 holds rows [0, boundary), W1 rows
-// [boundary, N) (gate|up as two tensors); boundary is a multiple of 16*NF.
+// grid: n_tiles * m_tiles * splits workgroups of 256 threads, two resident per
+// CU; (n_tiles * splits) a multiple of 8. W0 holds rows [0, boundary), W1
+// rows [boundary, N) (gate|up as two tensors); boundary a multiple of 256.
 // out: P[s][m][n] with split stride stride_tokens * N; token rows >= count
-// are not written.
-template <int NF>
+// are not written (their activation rows, < m_tiles * 64 <= stride_tokens,
+// are read).
 __global__ void __launch_bounds__(256, 2)
 k_gemm(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint32_t boundary,
     uint32_t N, uint32_t K, const uint16_t* __restrict__ xs, uint32_t stride_tokens,
     uint32_t count, uint32_t m_tiles, uint32_t splits, float* __restrict__ out)
 {
-    constexpr uint32_t BN = 16 * NF;
-    constexpr uint32_t CHUNKS = BN * (BK / 16);   // 16-code chunks per step
-    constexpr uint32_t BCH = (CHUNKS + 255) / 256;
-    __shared__ __attribute__((aligned(16))) uint16_t Bs[2][BN * LDS_STRIDE];
-
+    __shared__ __attribute__((aligned(1024))) uint8_t As0[A_FRAGS * 1024];
+    __shared__ __attribute__((aligned(1024))) uint8_t As1[A_FRAGS * 1024];
+    __shared__ __attribute__((aligned(1024))) uint8_t Ws0[W_FRAGS * 1024];
+    __shared__ __attribute__((aligned(1024))) uint8_t Ws1[W_FRAGS * 1024];
+    // (weight tile, split) columns are dealt round-robin to the 8 XCDs; each
+    // XCD runs a column's token tiles back to back, so they share its
+    // weight tile in L2.
     const uint32_t xcd = blockIdx.x & 7u, q = blockIdx.x >> 3;
-    const uint32_t inner = m_tiles * splits;
-    const uint32_t nt = (q / inner) * 8u + xcd;
-    const uint32_t mt = (q % inner) % m_tiles, s = (q % inner) / m_tiles;
-    const uint32_t kps = K / splits;
-    const uint32_t k0 = s * kps, steps = kps / BK;
-    const uint32_t n0 = nt * BN;
-    const uint8_t* Wt = n0 < boundary ? W0 + (size_t)n0 * K : W1 + (size_t)(n0 - boundary) * K;
-
+    const uint32_t mt = q % m_tiles, col = (q / m_tiles) * 8u + xcd;
+    const uint32_t s = col % splits, nt = col / splits;
+    const uint32_t kps = K / splits, k0 = s * kps, steps = kps / BK;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t g = lane >> 4, l16 = lane & 15;
-    const uint32_t m_base = mt * BM + wave * 32;
+    const uint32_t m0 = mt * GM, n0 = nt * GN + wave * 64;
+    const uint8_t* Wt = n0 < boundary ? W0 + (size_t)n0 * K : W1 + (size_t)(n0 - boundary) * K;
+    const uint8_t* wrow = Wt + (size_t)l16 * K + k0 + 16 * g;
     const size_t plane = (size_t)stride_tokens * K;
-    const uint16_t* arow0 = xs + (size_t)(m_base + l16) * K + 16 * g + k0;
-    const uint16_t* arow1 = arow0 + (size_t)16 * K;
-
-    // Weight chunk c (row c/4, 16 codes at column 16*(c%4) of the step): the
-    // loads are unconditional (threads past the tile reload its last chunk),
-    // only the LDS store is predicated.
-    const uint8_t* bsrc[BCH];
-    uint32_t bdst[BCH];
-    bool bown[BCH];
+    // This wave's six A fragments of each stage: f = 6*wave + i, f = (mf*3 + p)*2 + h.
+    const uint16_t* asrc[6];
 #pragma unroll
-    for (uint32_t i = 0; i < BCH; i++) {
-        const uint32_t c = tid + 256 * i;
-        const uint32_t cc = c < CHUNKS ? c : CHUNKS - 1;
-        bsrc[i] = Wt + (size_t)(cc >> 2) * K + 16 * (cc & 3) + k0;
-        bdst[i] = (cc >> 2) * LDS_STRIDE + 16 * (cc & 3);
-        bown[i] = c < CHUNKS;
+    for (int i = 0; i < 6; i++) {
+        const uint32_t f = 6 * wave + i, mf = f / 6, p = (f / 2) % 3, h = f % 2;
+        asrc[i] = xs + p * plane + (size_t)(m0 + 16 * mf + l16) * K + k0 + 16 * g + 8 * h;
     }
-    u32x4 bw[BCH];
-    auto load_b = [&](uint32_t dk) {
+    auto load_a = [&](uint32_t dk, uint8_t* buf) {
 #pragma unroll
-        for (uint32_t i = 0; i < BCH; i++) {
-            bw[i] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bsrc[i] + dk));
+        for (int i = 0; i < 6; i++) {
+            __builtin_amdgcn_global_load_lds(asrc[i] + dk, buf + (6 * wave + i) * 1024, 16, 0, 0);
         }
     };
-    auto store_b = [&](uint32_t stage) {
+    // Weight fragment nf of this wave: lane l's 16 codes at (4*wave + nf)*1024
+    // + 16*l, read back by the same lane.
+    auto load_w = [&](uint32_t dk, uint8_t* buf) {
 #pragma unroll
-        for (uint32_t i = 0; i < BCH; i++) {
-            if (bown[i]) {
-                uint16_t* dst = &Bs[stage][bdst[i]];
-                fp8x8_to_bf16(bw[i].x, bw[i].y, dst);
-                fp8x8_to_bf16(bw[i].z, bw[i].w, dst + 8);
-            }
+        for (int nf = 0; nf < 4; nf++) {
+            __builtin_amdgcn_global_load_lds(wrow + (size_t)16 * nf * K + dk,
+                buf + (4 * wave + nf) * 1024, 16, 0, 0);
         }
     };
-    bf16x8 a[2][NSPLIT][2];
-    auto load_a = [&](uint32_t dk) {
+    floatx4 acc[4][4];
 #pragma unroll
-        for (int p = 0; p < NSPLIT; p++) {
+    for (int mf = 0; mf < 4; mf++) {
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                a[0][p][h] = __builtin_bit_cast(bf16x8,
-                    *reinterpret_cast<const u32x4*>(arow0 + p * plane + dk + 8 * h));
-                a[1][p][h] = __builtin_bit_cast(bf16x8,
-                    *reinterpret_cast<const u32x4*>(arow1 + p * plane + dk + 8 * h));
-            }
-        }
-    };
-    floatx4 acc[2][NF];
-#pragma unroll
-    for (int mf = 0; mf < 2; mf++) {
-#pragma unroll
-        for (int nf = 0; nf < NF; nf++) {
+        for (int nf = 0; nf < 4; nf++) {
             acc[mf][nf] = floatx4{0.f, 0.f, 0.f, 0.f};
         }
     }
-    load_b(0);
-    store_b(0);
-    __syncthreads();
-    for (uint32_t step = 0; step < steps; step++) {
-        const bool more = step + 1 < steps;
-        load_a(step * BK);
-        if (more) {
-            load_b((step + 1) * BK);
+    // One stage: A fragments (mf, p, h) read from LDS one (p, h) group of four
+    // ahead of its MFMAs; each fragment feeds the four weight fragments.
+    auto compute = [&](const uint8_t* buf, const uint8_t* wbuf) {
+        bf16x8 b[4][2];
+#pragma unroll
+        for (int nf = 0; nf < 4; nf++) {
+            fp8x16_to_bf16x8x2(*reinterpret_cast<const u32x4*>(wbuf + (4 * wave + nf) * 1024 +
+                16 * lane), b[nf][0], b[nf][1]);
         }
-        const uint16_t* bs = &Bs[step & 1][l16 * LDS_STRIDE + 16 * g];
+        bf16x8 ac[4], an[4];
+        auto read_group = [&](int j, bf16x8 (&dst)[4]) {
+            const int h = j / 3, p = 2 - j % 3;
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            bf16x8 b[NF];
-#pragma unroll
-            for (int nf = 0; nf < NF; nf++) {
-                b[nf] = __builtin_bit_cast(bf16x8,
-                    *reinterpret_cast<const u32x4*>(bs + nf * 16 * LDS_STRIDE + 8 * h));
+            for (int mf = 0; mf < 4; mf++) {
+                dst[mf] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(
+                    buf + ((mf * 3 + p) * 2 + h) * 1024 + 16 * lane));
             }
+        };
+        read_group(0, ac);
 #pragma unroll
-            for (int nf = 0; nf < NF; nf++) {
+        for (int j = 0; j < 6; j++) {
+            if (j < 5) {
+                read_group(j + 1, an);
+            }
+            __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                for (int mf = 0; mf < 2; mf++) {
+            for (int mf = 0; mf < 4; mf++) {
 #pragma unroll
-                    for (int p = NSPLIT - 1; p >= 0; p--) {
-                        acc[mf][nf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a[mf][p][h], b[nf],
-                            acc[mf][nf], 0, 0, 0);
-                    }
+                for (int nf = 0; nf < 4; nf++) {
+                    acc[mf][nf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac[mf], b[nf][j / 3],
+                        acc[mf][nf], 0, 0, 0);
                 }
             }
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int mf = 0; mf < 4; mf++) {
+                ac[mf] = an[mf];
+            }
         }
-        if (more) {
-            store_b((step + 1) & 1);
-        }
+    };
+    // Double-buffered stages: the next stage's direct-to-LDS loads are issued
+    // after the barrier that ends every read of the buffers they overwrite,
+    // and complete (s_waitcnt 0 + barrier) before its MFMAs.
+    load_a(0, As0);
+    load_w(0, Ws0);
+    for (uint32_t st = 0; st < steps; st += 2) {
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+        if (st + 1 < steps) {
+            load_a((st + 1) * BK, As1);
+            load_w((st + 1) * BK, Ws1);
+        }
+        compute(As0, Ws0);
+        if (st + 1 >= steps) {
+            break;
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+        if (st + 2 < steps) {
+            load_a((st + 2) * BK, As0);
+            load_w((st + 2) * BK, Ws0);
+        }
+        compute(As1, Ws1);
     }
     // D layout of v_mfma_f32_16x16x32_bf16: lane l holds rows 4*(l/16) + r,
     // column l%16 of each 16x16 tile.
     float* o = out + (size_t)s * stride_tokens * N;
 #pragma unroll
-    for (int mf = 0; mf < 2; mf++) {
+    for (int mf = 0; mf < 4; mf++) {
 #pragma unroll
         for (int r = 0; r < 4; r++) {
-            const uint32_t m = m_base + 16 * mf + 4 * g + r;
+            const uint32_t m = m0 + 16 * mf + 4 * g + r;
             if (m < count) {
 #pragma unroll
-                for (int nf = 0; nf < NF; nf++) {
-                    o[(size_t)m * N + n0 + 16 * nf + l16] = acc[mf][nf][r];
+                for (int nf = 0; nf < 4; nf++) {
+                    o[(size_t)m * N + nt * GN + wave * 64 + 16 * nf + l16] = acc[mf][nf][r];
                 }
             }
         }
@@ -419,7 +429,7 @@ static int launched_ok(const char* what)
 // activation row a tile reads lies inside the split buffer.
 static uint32_t padded_block(const lh_workspace* ws)
 {
-    return (uint32_t)((ws->block + BM - 1) / BM * BM);
+    return (uint32_t)((ws->block + SPLIT_ROWS - 1) / SPLIT_ROWS * SPLIT_ROWS);
 }
 
 // Partial buffer: four 18432-wide splits per token (or more, narrower ones).
@@ -497,21 +507,21 @@ static int residual_norm_split(const float* partial, uint32_t splits, uint32_t s
     });
 }
 
-// P[s][m][n] for n < N over `splits` equal K ranges. N / (16*NF) must be a
-// multiple of 8, K a multiple of 64*splits, boundary a multiple of 16*NF.
-template <int NF>
+// P[s][m][n] for n < N over `splits` equal K ranges. N and boundary multiples
+// of 256, K a multiple of 64*splits, (N/256 * splits) a multiple of 8.
 static int gemm(const uint8_t* W0, const uint8_t* W1, uint32_t boundary, uint32_t N, uint32_t K,
     const uint16_t* xs, uint32_t stride, uint32_t count, uint32_t splits, float* out,
     hipStream_t s)
 {
-    const uint32_t n_tiles = N / (16 * NF);
-    const uint32_t m_tiles = (count + BM - 1) / BM;
-    if (!count || N % (16 * NF) || n_tiles % 8 || K % (BK * splits) || boundary % (16 * NF) ||
-        m_tiles * BM > stride || (size_t)splits * stride * N > partial_floats(stride)) {
+    const uint32_t n_tiles = N / GN;
+    const uint32_t m_tiles = (count + GM - 1) / GM;
+    if (!count || !splits || N % GN || (n_tiles * splits) % 8 || K % (BK * splits) ||
+        boundary % GN || m_tiles * GM > stride ||
+        (size_t)splits * stride * N > partial_floats(stride)) {
         lh_set_error("gemm: unsupported shape N=%u K=%u splits=%u", N, K, splits);
         return -1;
     }
-    hipLaunchKernelGGL(k_gemm<NF>, dim3(n_tiles * m_tiles * splits), dim3(256), 0, s, W0,
+    hipLaunchKernelGGL(k_gemm, dim3(n_tiles * m_tiles * splits), dim3(256), 0, s, W0,
         W1 ? W1 : W0, boundary, N, K, xs, stride, count, m_tiles, splits, out);
     return launched_ok("gemm");
 }
@@ -525,13 +535,6 @@ static int combine(const float* partial, uint32_t splits, uint32_t rows, uint32_
             dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, partial,
             (size_t)stride * rows, n4, scale, x, residual);
     });
-}
-
-// K splits giving about 512 workgroups: `base` for two token tiles, twice as
-// deep for one.
-static uint32_t splits_for(uint32_t count, uint32_t base)
-{
-    return count > BM ? base : 2 * base;
 }
 
 // Kernel-level MFMA projection y[t][r] = scale * sum_c dec(W[r][c]) x[t][c]
@@ -552,9 +555,11 @@ extern "C" int lh_fp8_gemm(lh_workspace* ws, const uint8_t* d_w, float scale, co
     }
     hipStream_t s = (hipStream_t)stream;
     const uint32_t B = padded_block(ws), n = (uint32_t)tokens;
-    const uint32_t splits = splits_for(n, 1);
+    // Deepest K split (<= 16) that divides the 64-column stages.
+    const uint32_t stages = (uint32_t)cols / BK;
+    const uint32_t splits = stages % 16 == 0 ? 16 : (stages % 8 == 0 ? 8 : 4);
     if (split_rows(d_x, ws->d_split, (uint32_t)cols, n, B, s) ||
-        gemm<4>(d_w, NULL, (uint32_t)rows, (uint32_t)rows, (uint32_t)cols, ws->d_split, B, n,
+        gemm(d_w, NULL, (uint32_t)rows, (uint32_t)rows, (uint32_t)cols, ws->d_split, B, n,
             splits, ws->d_gemm, s)) {
         return -1;
     }
@@ -579,12 +584,14 @@ extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, floa
     const uint32_t B = padded_block(ws);
     float* P = ws->d_gemm;
     uint16_t* xs = ws->d_split;
-    // q|k|v: 6144 rows in tiles of 96, 3072 columns; scales, RoPE and the KV
-    // append in the epilogue.
-    const uint32_t sq = splits_for(n, 4);
+    // K splits (measured at 256 tokens): gate|up 4 (the partial buffer's
+    // limit), q|k|v 8, o 8, down 16.
+    // q|k|v: 6144 rows, 3072 columns; scales, RoPE and the KV append in the
+    // epilogue.
+    const uint32_t sq = 8;
     if ((!input_split &&
             residual_norm_split(NULL, 0, B, 1.0f, d_x, w->input_norm, xs, n, s)) ||
-        gemm<6>(w->qkv, NULL, LH_QKV_ROWS, LH_QKV_ROWS, LH_HIDDEN, xs, B, n, sq, P, s) ||
+        gemm(w->qkv, NULL, LH_QKV_ROWS, LH_QKV_ROWS, LH_HIDDEN, xs, B, n, sq, P, s) ||
         with_splits(sq, "qkv epilogue", [&](auto S) {
             hipLaunchKernelGGL(k_qkv_epilogue<decltype(S)::value>, dim3(n, 3), dim3(256), 0, s,
                 P, (size_t)B * LH_QKV_ROWS, make_float3(w->scale[0], w->scale[1], w->scale[2]),
@@ -592,30 +599,30 @@ extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, floa
         })) {
         return -1;
     }
-    // Attention writes the o projection's input split; o: 3072 rows in tiles
-    // of 96, 4096 columns; residual, post-norm and the gate|up split after it.
-    const uint32_t so = splits_for(n, 8);
+    // Attention writes the o projection's input split; o: 3072 rows, 4096
+    // columns; residual, post-norm and the gate|up split after it.
+    const uint32_t so = 8;
     if (lh_launch_attention_mfma(ws->d_q, d_keys, d_values, ws->d_params, (uint32_t)ws->length,
             n, C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_attn, xs, B, s) ||
         launched_ok("attention") ||
-        gemm<6>(w->o, NULL, LH_HIDDEN, LH_HIDDEN, LH_QUERY, xs, B, n, so, P, s) ||
+        gemm(w->o, NULL, LH_HIDDEN, LH_HIDDEN, LH_QUERY, xs, B, n, so, P, s) ||
         residual_norm_split(P, so, B, w->scale[3], d_x, w->post_norm, xs, n, s)) {
         return -1;
     }
-    // gate|up: 18432 rows in tiles of 144, 3072 columns; SiLU(gate)*up in the
-    // down projection's split.
-    const uint32_t sg = splits_for(n, 2);
-    if (gemm<9>(w->gate, w->up, LH_INNER, MAX_N, LH_HIDDEN, xs, B, n, sg, P, s) ||
+    // gate|up: 18432 rows, 3072 columns; SiLU(gate)*up in the down
+    // projection's split.
+    const uint32_t sg = 4;
+    if (gemm(w->gate, w->up, LH_INNER, MAX_N, LH_HIDDEN, xs, B, n, sg, P, s) ||
         with_splits(sg, "silu split", [&](auto S) {
             hipLaunchKernelGGL(k_split_silu<decltype(S)::value>, dim3(n, 5), dim3(256), 0, s, P,
                 (size_t)B * MAX_N, make_float2(w->scale[4], w->scale[5]), xs, B);
         })) {
         return -1;
     }
-    // down: 3072 rows in tiles of 96, 9216 columns, residual (and the next
-    // layer's input split).
-    const uint32_t sd = splits_for(n, 8);
-    if (gemm<6>(w->down, NULL, LH_HIDDEN, LH_HIDDEN, LH_INNER, xs, B, n, sd, P, s)) {
+    // down: 3072 rows, 9216 columns, residual (and the next layer's input
+    // split).
+    const uint32_t sd = 16;
+    if (gemm(w->down, NULL, LH_HIDDEN, LH_HIDDEN, LH_INNER, xs, B, n, sd, P, s)) {
         return -1;
     }
     return next_norm ? residual_norm_split(P, sd, B, w->scale[6], d_x, next_norm, xs, n, s)
