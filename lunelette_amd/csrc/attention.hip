@@ -365,19 +365,27 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
     const uint32_t b_end = b_begin + per < nb ? b_begin + per : nb;
     const size_t head_base = lh_kv_index(capacity, 0, kvh, 0);
     float* pw = Ps[wave];
-    for (uint32_t b = b_begin; b < b_end; b++) {
-        // Stage K (float4 rows, stride 132) and V (stride 129) of the block;
-        // every row is inside the capacity (the block count never exceeds it).
+    // K and V of block b in registers (thread tid holds float4 words
+    // tid + 256i of each 64 x 128 tile); the next block's loads are issued
+    // before this block's MFMAs, so their latency overlaps the compute. Every
+    // row is inside the capacity (the block count never exceeds it).
+    fa_floatx4 kr[8], vr[8];
+    auto load_block = [&](uint32_t b) {
         const fa_floatx4* kb = reinterpret_cast<const fa_floatx4*>(
             kcache + head_base + (size_t)b * LH_ATTN_BLOCK * LH_HEAD_DIM);
         const fa_floatx4* vb = reinterpret_cast<const fa_floatx4*>(
             vcache + head_base + (size_t)b * LH_ATTN_BLOCK * LH_HEAD_DIM);
-        fa_floatx4 kr[8], vr[8];
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             kr[i] = kb[tid + 256 * i];
             vr[i] = vb[tid + 256 * i];
         }
+    };
+    if (b_begin < b_end) {
+        load_block(b_begin);
+    }
+    for (uint32_t b = b_begin; b < b_end; b++) {
+        // Stage K (float4 rows, stride 132) and V (stride 129) of the block.
         __syncthreads();   // the previous block's tiles are consumed
 #pragma unroll
         for (int i = 0; i < 8; i++) {
@@ -390,6 +398,9 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
             vd[3] = vr[i].w;
         }
         __syncthreads();
+        if (b + 1 < b_end) {
+            load_block(b + 1);
+        }
         // S tiles j = 0..3: positions 16j + l16 of the block.
         fa_floatx4 s[4];
 #pragma unroll

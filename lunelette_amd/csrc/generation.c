@@ -1,8 +1,10 @@
 /* Greedy selection and the full-prefix generation loop (contract of the
  * reference include/generation.h:38-71, behaviour of src/generation.c:8-136). */
 #include "lunelette_generation.h"
+#include "lh_scan.h"
 
 #include <math.h>
+#include <stdint.h>
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
@@ -14,28 +16,25 @@ static void say(char *error, size_t capacity, const char *text)
     }
 }
 
+/* The reference's forward scan with a strict > keeps the first index of the
+ * maximum (-0.0 and +0.0 compare equal) and fails at the first nonfinite
+ * logit; the same result comes from three vectorized passes: the first
+ * nonfinite index, the maximum, the first index equal to it. */
 int lunelette_select_greedy(const float *logits, int64_t *token, char *error, size_t capacity)
 {
     if (!logits || !token) {
         say(error, capacity, "selection: require logits and token");
         return -1;
     }
-    size_t best = 0;
-    float best_value = logits[0];
-    for (size_t i = 0; i < LUNELETTE_VOCAB_SIZE; i++) {
-        const float value = logits[i];
-        if (!isfinite(value)) {
-            if (error && capacity) {
-                snprintf(error, capacity, "selection: nonfinite logit at token %zu", i);
-            }
-            return -1;
+    const size_t bad = lh_first_nonfinite(logits, LUNELETTE_VOCAB_SIZE);
+    if (bad < LUNELETTE_VOCAB_SIZE) {
+        if (error && capacity) {
+            snprintf(error, capacity, "selection: nonfinite logit at token %zu", bad);
         }
-        if (value > best_value) {
-            best_value = value;
-            best = i;
-        }
+        return -1;
     }
-    *token = (int64_t)best;
+    const float best_value = lh_max(logits, LUNELETTE_VOCAB_SIZE);
+    *token = (int64_t)lh_first_equal(logits, LUNELETTE_VOCAB_SIZE, best_value);
     if (error && capacity) {
         error[0] = '\0';
     }

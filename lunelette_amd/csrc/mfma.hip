@@ -13,15 +13,16 @@
 //   tiles). Per 64-column stage the activation tile (64 tokens x 3 planes,
 //   24 KB) goes to LDS by direct loads (global_load_lds_dwordx4) in
 //   fragment-major order, so each v_mfma_f32_16x16x32_bf16 A operand is one
-//   conflict-free 16-byte LDS read, shared by the four waves; each wave's
-//   weight rows (16 FP8 codes per lane and row fragment, 16 KB per stage for
-//   the workgroup) take the same direct route into a per-lane LDS slot, and
-//   the lane converts its own codes to BF16 in registers. The next stage's
-//   loads are in flight (two LDS buffers) while the current stage's 96
-//   MFMAs per wave run. Lane group g = lane/16 supplies columns
+//   conflict-free 16-byte LDS read, shared by the four waves; each wave
+//   streams its weight rows straight into registers (16 FP8 codes per lane
+//   and row fragment) and converts them there. The next stage's loads are
+//   in flight (two LDS buffers, two weight register sets) while the current
+//   stage's 96 MFMAs per wave run. Lane group g = lane/16 supplies columns
 //   16g .. 16g+15 of the stage to both operands (a K permutation shared by
 //   A and B, so the sum is unchanged) as two 8-column k-slices. Two
-//   workgroups share a CU (80 KB LDS and <= 256 registers each).
+//   workgroups share a CU (48 KB LDS and <= 256 registers each). Measured
+//   alternatives: weights through LDS as well (slower on gate|up, equal
+//   elsewhere); a third stage in flight (spills at two workgroups per CU).
 // - Workgroup ids deal the (weight tile, split) columns round-robin to the 8
 //   XCDs and run a column's token tiles back to back on one XCD, so the
 //   weight tile is read from HBM once per XCD and from L2 after that.
@@ -49,7 +50,6 @@ constexpr uint32_t GM = 64;               // tokens per workgroup tile
 constexpr uint32_t GN = 256;              // weight rows per workgroup tile (4 waves x 64)
 constexpr uint32_t BK = 64;               // columns per pipeline stage
 constexpr uint32_t A_FRAGS = 4 * 3 * 2;   // 1 KB activation fragments per stage
-constexpr uint32_t W_FRAGS = 4 * 4;       // 1 KB weight fragments per stage
 constexpr uint32_t SPLIT_ROWS = 128;      // token stride granule of the split planes
 constexpr uint32_t MAX_N = 2 * LH_INNER;  // widest GEMM: gate|up
 
@@ -260,8 +260,6 @@ k_gemm(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint32_t 
 {
     __shared__ __attribute__((aligned(1024))) uint8_t As0[A_FRAGS * 1024];
     __shared__ __attribute__((aligned(1024))) uint8_t As1[A_FRAGS * 1024];
-    __shared__ __attribute__((aligned(1024))) uint8_t Ws0[W_FRAGS * 1024];
-    __shared__ __attribute__((aligned(1024))) uint8_t Ws1[W_FRAGS * 1024];
     // (weight tile, split) columns are dealt round-robin to the 8 XCDs; each
     // XCD runs a column's token tiles back to back, so they share its
     // weight tile in L2.
@@ -288,13 +286,11 @@ k_gemm(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint32_t 
             __builtin_amdgcn_global_load_lds(asrc[i] + dk, buf + (6 * wave + i) * 1024, 16, 0, 0);
         }
     };
-    // Weight fragment nf of this wave: lane l's 16 codes at (4*wave + nf)*1024
-    // + 16*l, read back by the same lane.
-    auto load_w = [&](uint32_t dk, uint8_t* buf) {
+    u32x4 wr[4];
+    auto load_w = [&](uint32_t dk) {
 #pragma unroll
         for (int nf = 0; nf < 4; nf++) {
-            __builtin_amdgcn_global_load_lds(wrow + (size_t)16 * nf * K + dk,
-                buf + (4 * wave + nf) * 1024, 16, 0, 0);
+            wr[nf] = *reinterpret_cast<const u32x4*>(wrow + (size_t)16 * nf * K + dk);
         }
     };
     floatx4 acc[4][4];
@@ -307,12 +303,11 @@ k_gemm(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint32_t 
     }
     // One stage: A fragments (mf, p, h) read from LDS one (p, h) group of four
     // ahead of its MFMAs; each fragment feeds the four weight fragments.
-    auto compute = [&](const uint8_t* buf, const uint8_t* wbuf) {
+    auto compute = [&](const uint8_t* buf, const u32x4 (&w)[4]) {
         bf16x8 b[4][2];
 #pragma unroll
         for (int nf = 0; nf < 4; nf++) {
-            fp8x16_to_bf16x8x2(*reinterpret_cast<const u32x4*>(wbuf + (4 * wave + nf) * 1024 +
-                16 * lane), b[nf][0], b[nf][1]);
+            fp8x16_to_bf16x8x2(w[nf], b[nf][0], b[nf][1]);
         }
         bf16x8 ac[4], an[4];
         auto read_group = [&](int j, bf16x8 (&dst)[4]) {
@@ -345,29 +340,39 @@ k_gemm(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint32_t 
             }
         }
     };
-    // Double-buffered stages: the next stage's direct-to-LDS loads are issued
-    // after the barrier that ends every read of the buffers they overwrite,
-    // and complete (s_waitcnt 0 + barrier) before its MFMAs.
+    // Double-buffered stages: the next stage's activation (direct to LDS) and
+    // weight loads are issued after the barrier that ends every read of the
+    // LDS buffer they overwrite, and complete (s_waitcnt 0 + barrier) before
+    // its MFMAs.
+    u32x4 wc[4];
     load_a(0, As0);
-    load_w(0, Ws0);
+    load_w(0);
     for (uint32_t st = 0; st < steps; st += 2) {
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+#pragma unroll
+        for (int nf = 0; nf < 4; nf++) {
+            wc[nf] = wr[nf];
+        }
         if (st + 1 < steps) {
             load_a((st + 1) * BK, As1);
-            load_w((st + 1) * BK, Ws1);
+            load_w((st + 1) * BK);
         }
-        compute(As0, Ws0);
+        compute(As0, wc);
         if (st + 1 >= steps) {
             break;
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+#pragma unroll
+        for (int nf = 0; nf < 4; nf++) {
+            wc[nf] = wr[nf];
+        }
         if (st + 2 < steps) {
             load_a((st + 2) * BK, As0);
-            load_w((st + 2) * BK, Ws0);
+            load_w((st + 2) * BK);
         }
-        compute(As1, Ws1);
+        compute(As1, wc);
     }
     // D layout of v_mfma_f32_16x16x32_bf16: lane l holds rows 4*(l/16) + r,
     // column l%16 of each 16x16 tile.

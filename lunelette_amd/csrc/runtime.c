@@ -12,6 +12,7 @@
 #include "lunelette_kernels.h"
 #include "lh_internal.h"
 #include "lh_layer.h"
+#include "lh_scan.h"
 
 #include <math.h>
 #include <stdatomic.h>
@@ -774,11 +775,10 @@ static int execute(lunelette_metal *context, const int64_t *ids, size_t count, b
         rt->inject = 0;
         rt->h_logits[LH_VOCAB - 1] = INFINITY;
     }
-    for (size_t i = 0; i < LH_VOCAB; i++) {
-        if (!isfinite(rt->h_logits[i])) {
-            snprintf(error, capacity, "nonfinite logit %zu; reset required", i);
-            return -1;
-        }
+    const size_t bad = lh_first_nonfinite(rt->h_logits, LH_VOCAB);
+    if (bad < LH_VOCAB) {
+        snprintf(error, capacity, "nonfinite logit %zu; reset required", bad);
+        return -1;
     }
     rt->length += count;
     rt->valid = true;
@@ -819,16 +819,15 @@ int lunelette_metal_checkpoint_create(lunelette_metal *context,
         report(error, capacity, "%scheckpoint requires valid endpoint/available epoch", NULL);
         return -1;
     }
-    for (size_t i = 0; i < LH_VOCAB; i++) {
-        if (!isfinite(rt->h_logits[i])) {
-            if (error && capacity) {
-                snprintf(error, capacity, "checkpoint nonfinite logit %zu", i);
-            }
-            rt->valid = false;
-            rt->endpoint_logits_valid = false;
-            rt->active_checkpoint = NULL;
-            return -1;
+    const size_t bad = lh_first_nonfinite(rt->h_logits, LH_VOCAB);
+    if (bad < LH_VOCAB) {
+        if (error && capacity) {
+            snprintf(error, capacity, "checkpoint nonfinite logit %zu", bad);
         }
+        rt->valid = false;
+        rt->endpoint_logits_valid = false;
+        rt->active_checkpoint = NULL;
+        return -1;
     }
     lunelette_metal_checkpoint *saved = NULL;
     if (rt->inject == 3) {
