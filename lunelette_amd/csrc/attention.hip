@@ -26,7 +26,7 @@
 namespace lh {
 
 constexpr uint32_t GROUP = 8;     // blocks chained per combine group
-constexpr uint32_t ROUND = 128;   // blocks per combine round (16 groups)
+constexpr uint32_t ROUND = 256;   // blocks per combine round (32 groups)
 
 __global__ void __launch_bounds__(256)
 k_attn_blocks(const float* __restrict__ q, const float* __restrict__ kcache,
@@ -122,9 +122,12 @@ k_attn_blocks(const float* __restrict__ q, const float* __restrict__ kcache,
     *reinterpret_cast<float2*>(PA + (th * nbc + b) * LH_HEAD_DIM + d0) = make_float2(a0, a1);
 }
 
-// grid (32 heads, count), 256 threads: thread (c = tid & 31, s = tid >> 5)
-// owns dims 4c..4c+3 of groups s and s + 8 of each 128-block round; the
-// partials are the token's 64-position blocks.
+// grid (32 heads x 4 dimension quarters, count), 256 threads: thread
+// (c = tid & 7, s = tid >> 3) owns dims 32q + 4c .. +3 of group s of each
+// 256-block round; every quarter recomputes M and the block factors, so the
+// four workgroups of a head are independent. Bitwise the schedule above (the
+// dims never mix; groups start at multiples of 8 from block 0 and add left
+// to right across rounds).
 __global__ void __launch_bounds__(256)
 k_attn_combine(const float* __restrict__ PM, const float* __restrict__ PT,
     const float* __restrict__ PA, const lh_step_params* __restrict__ params, uint32_t capacity,
@@ -132,17 +135,17 @@ k_attn_combine(const float* __restrict__ PM, const float* __restrict__ PT,
 {
     __shared__ float wmax[4];
     __shared__ float fs[ROUND], ts[ROUND];
-    __shared__ float4 sg[ROUND / GROUP][LH_HEAD_DIM / 4];
+    __shared__ float4 sg[ROUND / GROUP][8];
     __shared__ float ug[ROUND / GROUP];
-    const uint32_t h = blockIdx.x, t = blockIdx.y;
+    const uint32_t h = blockIdx.x >> 2, qd = blockIdx.x & 3, t = blockIdx.y;
     const uint32_t n = params->length + t + 1;
     const uint32_t nb = (n + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
     const uint32_t nbc = capacity / LH_ATTN_BLOCK;
     const size_t th = (size_t)t * LH_HEADS + h;
     const float* pm = PM + th * nbc;
     const float* pt = PT + th * nbc;
-    const float4* pa = reinterpret_cast<const float4*>(PA + th * nbc * LH_HEAD_DIM);
-    const uint32_t tid = threadIdx.x, c = tid & 31, s = tid >> 5;
+    const uint32_t tid = threadIdx.x, c = tid & 7, s = tid >> 3;
+    const float4* pa = reinterpret_cast<const float4*>(PA + th * nbc * LH_HEAD_DIM) + 8 * qd + c;
     float M = -__builtin_inff();
     for (uint32_t j = tid; j < nb; j += 256) {
         M = fmaxf(M, pm[j]);
@@ -157,44 +160,37 @@ k_attn_combine(const float* __restrict__ PM, const float* __restrict__ PT,
     float T = 0.0f;
     for (uint32_t r0 = 0; r0 < nb; r0 += ROUND) {
         // Every load of the round issues before the first wait (clamped rows).
-        float4 a[2][GROUP];
+        float4 a[GROUP];
 #pragma unroll
-        for (int gi = 0; gi < 2; gi++) {
-#pragma unroll
-            for (uint32_t k = 0; k < GROUP; k++) {
-                const uint32_t bb = r0 + (s + 8 * gi) * GROUP + k;
-                a[gi][k] = pa[(size_t)(bb < nb ? bb : nb - 1) * (LH_HEAD_DIM / 4) + c];
-            }
+        for (uint32_t k = 0; k < GROUP; k++) {
+            const uint32_t bb = r0 + s * GROUP + k;
+            a[k] = pa[(size_t)(bb < nb ? bb : nb - 1) * (LH_HEAD_DIM / 4)];
         }
-        if (tid < ROUND) {
+        {
             const uint32_t bb = r0 + tid;
             fs[tid] = bb < nb ? expf_cw(pm[bb] - M) : 0.0f;
             ts[tid] = bb < nb ? pt[bb] : 0.0f;
         }
         __syncthreads();
+        float4 Sg = make_float4(0.f, 0.f, 0.f, 0.f);
+        float Ug = 0.0f;
 #pragma unroll
-        for (int gi = 0; gi < 2; gi++) {
-            const uint32_t g = s + 8 * gi;
-            float4 Sg = make_float4(0.f, 0.f, 0.f, 0.f);
-            float Ug = 0.0f;
-#pragma unroll
-            for (uint32_t k = 0; k < GROUP; k++) {
-                if (r0 + g * GROUP + k < nb) {
-                    const float f = fs[g * GROUP + k];
-                    Sg.x = __builtin_fmaf(f, a[gi][k].x, Sg.x);
-                    Sg.y = __builtin_fmaf(f, a[gi][k].y, Sg.y);
-                    Sg.z = __builtin_fmaf(f, a[gi][k].z, Sg.z);
-                    Sg.w = __builtin_fmaf(f, a[gi][k].w, Sg.w);
-                    Ug = __builtin_fmaf(f, ts[g * GROUP + k], Ug);
-                }
-            }
-            sg[g][c] = Sg;
-            if (c == 0) {
-                ug[g] = Ug;
+        for (uint32_t k = 0; k < GROUP; k++) {
+            if (r0 + s * GROUP + k < nb) {
+                const float f = fs[s * GROUP + k];
+                Sg.x = __builtin_fmaf(f, a[k].x, Sg.x);
+                Sg.y = __builtin_fmaf(f, a[k].y, Sg.y);
+                Sg.z = __builtin_fmaf(f, a[k].z, Sg.z);
+                Sg.w = __builtin_fmaf(f, a[k].w, Sg.w);
+                Ug = __builtin_fmaf(f, ts[s * GROUP + k], Ug);
             }
         }
+        sg[s][c] = Sg;
+        if (c == 0) {
+            ug[s] = Ug;
+        }
         __syncthreads();
-        if (tid < 32) {
+        if (tid < 8) {
             for (uint32_t g = 0; g < ROUND / GROUP && r0 + g * GROUP < nb; g++) {
                 const float4 v = sg[g][c];
                 if (r0 == 0 && g == 0) {
@@ -211,8 +207,8 @@ k_attn_combine(const float* __restrict__ PM, const float* __restrict__ PT,
         }
         __syncthreads();
     }
-    if (tid < 32) {
-        reinterpret_cast<float4*>(out + (size_t)t * LH_QUERY + h * LH_HEAD_DIM)[c] =
+    if (tid < 8) {
+        reinterpret_cast<float4*>(out + (size_t)t * LH_QUERY + h * LH_HEAD_DIM)[8 * qd + c] =
             make_float4(A.x / T, A.y / T, A.z / T, A.w / T);
     }
 }
@@ -246,7 +242,7 @@ extern "C" int lh_launch_attention(const float* q, const float* kcache_layer,
     }
     hipLaunchKernelGGL(k_attn_blocks, dim3(lh_attention_blocks(length, count), LH_KV_HEADS, count),
         dim3(256), 0, s, q, kcache_layer, vcache_layer, params, capacity, PM, PT, PA);
-    hipLaunchKernelGGL(k_attn_combine, dim3(LH_HEADS, count), dim3(256), 0, s, PM, PT, PA, params,
+    hipLaunchKernelGGL(k_attn_combine, dim3(LH_HEADS * 4, count), dim3(256), 0, s, PM, PT, PA, params,
         capacity, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
