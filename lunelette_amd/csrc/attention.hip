@@ -285,6 +285,12 @@ extern "C" int lh_launch_embed(const uint16_t* E, const lh_step_params* params, 
 // capacity/64 per (token, head)), merged by k_attn_merge. With xs set, the
 // output goes to xs as the hi/mid/lo BF16 planes the o-projection GEMM reads
 // (plane stride xs_tokens * 4096) instead of FP32 rows of out.
+// LDS is the K tile (33 KiB, reused for the four P tiles after a barrier) and
+// the V tile (33 KiB), under 184 registers, so two workgroups share a CU and
+// the launcher sizes splits for about 512 workgroups. Measured alternative:
+// BF16 MFMA with both operands split in three exact planes (six products per
+// k chunk) ran at 1.2x on long prefixes and 0.6x on short ones, its K/V
+// splitting and transposes costing as much VALU time as the MFMAs saved.
 namespace lh {
 
 constexpr uint32_t FA_TQ = 16;                      // tokens per workgroup
@@ -310,7 +316,7 @@ __device__ __forceinline__ float quad16_sum(float v)
     return v + __shfl_xor(v, 8, 64);
 }
 
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(256, 2)
 k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
     const float* __restrict__ vcache, uint32_t length, uint32_t count, uint32_t capacity,
     float* __restrict__ PM, float* __restrict__ PT, float* __restrict__ PA, float* __restrict__ out,
@@ -318,7 +324,9 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
 {
     __shared__ __attribute__((aligned(16))) float Ks[LH_ATTN_BLOCK * FA_KS];
     __shared__ float Vs[LH_ATTN_BLOCK * FA_VS];
-    __shared__ __attribute__((aligned(16))) float Ps[4][FA_TQ * FA_PS];
+    // Each wave's P tile reuses the K tile's space once every wave has read K.
+    float (*Ps)[FA_TQ * FA_PS] = reinterpret_cast<float (*)[FA_TQ * FA_PS]>(Ks);
+    static_assert(4 * FA_TQ * FA_PS <= LH_ATTN_BLOCK * FA_KS, "P tiles fit the K tile");
     const uint32_t t0 = blockIdx.x * FA_TQ, kvh = blockIdx.y;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t g = lane >> 4, l16 = lane & 15;
@@ -362,9 +370,9 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
     const size_t head_base = lh_kv_index(capacity, 0, kvh, 0);
     float* pw = Ps[wave];
     // K and V of block b in registers (thread tid holds float4 words
-    // tid + 256i of each 64 x 128 tile); the next block's loads are issued
-    // before this block's MFMAs, so their latency overlaps the compute. Every
-    // row is inside the capacity (the block count never exceeds it).
+    // tid + 256i of each 64 x 128 tile); every row is inside the capacity
+    // (the block count never exceeds it). Two workgroups share a CU, so one
+    // stages its tiles while the other runs MFMAs.
     fa_floatx4 kr[8], vr[8];
     auto load_block = [&](uint32_t b) {
         const fa_floatx4* kb = reinterpret_cast<const fa_floatx4*>(
@@ -377,10 +385,8 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
             vr[i] = vb[tid + 256 * i];
         }
     };
-    if (b_begin < b_end) {
-        load_block(b_begin);
-    }
     for (uint32_t b = b_begin; b < b_end; b++) {
+        load_block(b);
         // Stage K (float4 rows, stride 132) and V (stride 129) of the block.
         __syncthreads();   // the previous block's tiles are consumed
 #pragma unroll
@@ -394,9 +400,6 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
             vd[3] = vr[i].w;
         }
         __syncthreads();
-        if (b + 1 < b_end) {
-            load_block(b + 1);
-        }
         // S tiles j = 0..3: positions 16j + l16 of the block.
         fa_floatx4 s[4];
 #pragma unroll
@@ -412,6 +415,7 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
                 s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[i].w, kk.w, s[j], 0, 0, 0);
             }
         }
+        __syncthreads();   // every wave has read K; P tiles reuse its space
         // Scale, causal mask, online softmax; P to this wave's LDS tile.
 #pragma unroll
         for (int r = 0; r < 4; r++) {
@@ -550,11 +554,11 @@ extern "C" int lh_launch_attention_mfma(const float* q, const float* kcache_laye
         (xs && xs_tokens < count)) {
         return -1;
     }
-    // KV splits so that about 256 workgroups run: each takes at least 4
-    // blocks of the longest tile, at most one partial per block.
+    // KV splits so that about 512 workgroups run (two per CU): each takes at
+    // least 4 blocks of the longest tile, at most one partial per block.
     const uint32_t tiles = (count + lh::FA_TQ - 1) / lh::FA_TQ;
     const uint32_t nb = (length + count + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
-    uint32_t splits = 256 / (tiles * LH_KV_HEADS);
+    uint32_t splits = 512 / (tiles * LH_KV_HEADS);
     const uint32_t by_length = nb / 4;
     splits = splits < by_length ? splits : by_length;
     splits = splits ? splits : 1;
