@@ -6,11 +6,13 @@ decode (the bench workload). The fixture tests/golden/stream_c4352_26layer.json
 holds the CPU oracle's streams (tests/golden/make_stream_golden.py):
 - the precise path (PREFILL_CUSTOM + decode) must reproduce the oracle's
   device-mirror stream token for token (it is bit-exact per step);
-- the reference-literal stream is the same up to the fixture's first
-  divergence (an ulp-level difference through a near-tie of the model's
-  one-hot softmax), which this test reports;
+- the precise stream must also agree with the reference-literal stream up to
+  the fixture's first divergence between the two oracle schedules (None: the
+  two schedules select the same 1024 tokens for this seed, so the GPU stream
+  equals the reference-literal one throughout);
 - the MPS path (matrix-core prefill, tolerance-equal logits) must select the
-  same first token, and reports how long its stream agrees.
+  same first token, and reports how long its stream agrees (1024 of 1024 on
+  the MI355X for this fixture).
 """
 import json
 import os
