@@ -159,6 +159,22 @@ float lh_synth_scale(uint64_t seed, uint32_t tensor);
 /* Uniform token ids in [0, 131072). */
 void lh_synth_tokens(uint64_t seed, uint32_t stream_id, int64_t *out, size_t n);
 
+/* ---- checkpoint files (safetensors) ----
+ * The container reader replaces st_open/st_find/st_read
+ * (include/safetensors.h:47-53, src/safetensors.c:352-424); the tensor
+ * contract replaces lunelette_metal_weights_open (src/metal_weights.c:40-150).
+ * lunelette_metal_create*(path) loads through them. */
+/* Opens and validates path; on success writes one line per tensor in header
+ * order, "name|dtype|rank|d0,d1,..|begin|end\n", into listing. */
+int lh_st_inspect(const char *path, char *listing, size_t listing_capacity, char *error,
+    size_t capacity);
+/* Bytes [offset, offset + bytes) of tensor `name`, bounds-checked. */
+int lh_st_read_tensor(const char *path, const char *name, uint64_t offset, void *out,
+    size_t bytes, char *error, size_t capacity);
+/* Container + tensor contract + scales of a model checkpoint; scales
+ * [2 + 26*9] (slot order of src/metal_weights.h, 1 for non-FP8 slots) or NULL. */
+int lh_checkpoint_check(const char *path, float *scales, char *error, size_t capacity);
+
 /* ---- test seams (no counterpart in the reference ABI) ----
  * Host-forced failures equivalent to the reference's mocked command failures
  * (tests/test_metal.m:629-860), for state-machine tests on a live context:

@@ -138,6 +138,11 @@ def lib():
            c_void, c_size)
     _proto(l, "lh_synth_scale", f, ctypes.c_uint64, ctypes.c_uint32)
     _proto(l, "lh_synth_tokens", v, ctypes.c_uint64, ctypes.c_uint32, c_int64_p, c_size)
+    _proto(l, "lh_st_inspect", i, ctypes.c_char_p, ctypes.c_char_p, c_size, ctypes.c_char_p,
+           c_size)
+    _proto(l, "lh_st_read_tensor", i, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_uint64,
+           c_void, c_size, ctypes.c_char_p, c_size)
+    _proto(l, "lh_checkpoint_check", i, ctypes.c_char_p, c_float_p, ctypes.c_char_p, c_size)
     err = ctypes.c_char_p
     _proto(l, "lunelette_metal_create", c_void, ctypes.c_char_p, err, c_size)
     _proto(l, "lunelette_metal_create_with_options", c_void, ctypes.c_char_p,

@@ -13,6 +13,7 @@
 #include "lh_internal.h"
 #include "lh_layer.h"
 #include "lh_scan.h"
+#include "lh_weights.h"
 
 #include <math.h>
 #include <stdatomic.h>
@@ -232,10 +233,69 @@ static int stage_push(uploader *up, void *dst, size_t bytes, char *error, size_t
     return 0;
 }
 
+/* Where the tensor bytes come from: the seeded synthetic generator or a
+ * checkpoint file. read() copies elements [offset, offset + count) of a slot
+ * (FP8 codes, 1 byte each; BF16 bits, 2 bytes each, little-endian). */
+typedef struct weight_source {
+    int (*read)(struct weight_source *src, uint32_t slot, uint64_t offset, void *dst,
+        size_t count);
+    float (*scale)(struct weight_source *src, uint32_t slot);
+    uint64_t seed;
+    lh_weights *file;
+} weight_source;
+
+static bool norm_slot(uint32_t slot)
+{
+    return slot == 1 || (slot >= 2 && ((slot - 2) % 9 == 0 || (slot - 2) % 9 == 5));
+}
+
+static int synthetic_read(weight_source *src, uint32_t slot, uint64_t offset, void *dst,
+    size_t count)
+{
+    if (slot == 0) {
+        lh_synth_normal_bf16(src->seed, 0, offset, 0.0f, 0.02f, dst, count);
+    } else if (norm_slot(slot)) {
+        lh_synth_normal_bf16(src->seed, slot, offset, 1.0f, 0.02f, dst, count);
+    } else {
+        lh_synth_fp8(src->seed, slot, offset, dst, count);
+    }
+    return 0;
+}
+
+static float synthetic_scale(weight_source *src, uint32_t slot)
+{
+    return lh_synth_scale(src->seed, slot);
+}
+
+static int file_read(weight_source *src, uint32_t slot, uint64_t offset, void *dst, size_t count)
+{
+    const lh_st_tensor *t = src->file->slot[slot].tensor;
+    const size_t esize = t->dtype == LH_ST_F8_E4M3 ? 1 : 2;
+    return lh_st_read(&src->file->file, t, offset * esize, dst, count * esize);
+}
+
+static float file_scale(weight_source *src, uint32_t slot)
+{
+    return src->file->slot[slot].scale;
+}
+
+static int source_read(weight_source *src, uint32_t slot, uint64_t offset, void *dst, size_t count,
+    char *error, size_t capacity)
+{
+    if (src->read(src, slot, offset, dst, count)) {
+        if (error && capacity) {
+            snprintf(error, capacity, "checkpoint read failed: %s",
+                src->file ? src->file->slot[slot].tensor->name : "synthetic");
+        }
+        return -1;
+    }
+    return 0;
+}
+
 /* FP8 tensor `tensor` of n codes: admit, then store the codes (compact) or
  * their exact FP32 decode (resident); both strategies multiply the row total
  * by the per-tensor scale, so their results are bitwise identical. */
-static int upload_fp8(uploader *up, uint64_t seed, uint32_t tensor, float scale, size_t n,
+static int upload_fp8(uploader *up, weight_source *src, uint32_t tensor, float scale, size_t n,
     bool resident, void *dst, char *error, size_t capacity)
 {
     unsigned char allowed[256];
@@ -260,7 +320,10 @@ static int upload_fp8(uploader *up, uint64_t seed, uint32_t tensor, float scale,
         size_t m = n - offset < chunk ? n - offset : chunk;
         void *slot = stage_slot(up);
         uint8_t *dst_codes = resident ? codes : (uint8_t *)slot;
-        lh_synth_fp8(seed, tensor, offset, dst_codes, m);
+        if (source_read(src, tensor, offset, dst_codes, m, error, capacity)) {
+            free(codes);
+            return -1;
+        }
         for (size_t i = 0; i < m; i++) {
             if (!allowed[dst_codes[i]]) {
                 if (error && capacity) {
@@ -290,15 +353,15 @@ static int upload_fp8(uploader *up, uint64_t seed, uint32_t tensor, float scale,
     return 0;
 }
 
-static int upload_bf16_normal(uploader *up, uint64_t seed, uint32_t tensor, float mean, float std,
-    size_t n, uint16_t *dst, char *error, size_t capacity)
+static int upload_bf16(uploader *up, weight_source *src, uint32_t tensor, size_t n, uint16_t *dst,
+    char *error, size_t capacity)
 {
     const size_t chunk = STAGE_BYTES / 2;
     for (size_t offset = 0; offset < n; offset += chunk) {
         size_t m = n - offset < chunk ? n - offset : chunk;
         uint16_t *slot = stage_slot(up);
-        lh_synth_normal_bf16(seed, tensor, offset, mean, std, slot, m);
-        if (stage_push(up, dst + offset, m * sizeof(uint16_t), error, capacity)) {
+        if (source_read(src, tensor, offset, slot, m, error, capacity) ||
+            stage_push(up, dst + offset, m * sizeof(uint16_t), error, capacity)) {
             return -1;
         }
     }
@@ -306,11 +369,13 @@ static int upload_bf16_normal(uploader *up, uint64_t seed, uint32_t tensor, floa
 }
 
 /* Norm vectors are BF16 in the checkpoint and widened to FP32 (exact). */
-static int upload_norm(uploader *up, uint64_t seed, uint32_t tensor, float *dst, char *error,
+static int upload_norm(uploader *up, weight_source *src, uint32_t tensor, float *dst, char *error,
     size_t capacity)
 {
     uint16_t bits[LH_HIDDEN];
-    lh_synth_normal_bf16(seed, tensor, 0, 1.0f, 0.02f, bits, LH_HIDDEN);
+    if (source_read(src, tensor, 0, bits, LH_HIDDEN, error, capacity)) {
+        return -1;
+    }
     float *slot = stage_slot(up);
     for (size_t i = 0; i < LH_HIDDEN; i++) {
         uint32_t word = (uint32_t)bits[i] << 16;
@@ -319,28 +384,12 @@ static int upload_norm(uploader *up, uint64_t seed, uint32_t tensor, float *dst,
     return stage_push(up, dst, LH_HIDDEN * sizeof(float), error, capacity);
 }
 
-lunelette_metal *lunelette_metal_create_synthetic(const lunelette_synthetic_config *config,
-    const lunelette_metal_options *options, const lunelette_metal_limits *limits,
-    char *error, size_t capacity)
+/* Device residency for `layers` layers from src, after the profile and the
+ * options have been resolved. */
+static lunelette_metal *build_runtime(weight_source *src, uint32_t layers,
+    lunelette_metal_limits resolved, lunelette_metal_options selected, char *error,
+    size_t capacity)
 {
-    char fallback[512];
-    if (!error || !capacity) {
-        error = fallback;
-        capacity = sizeof fallback;
-    }
-    lunelette_metal_limits resolved = limits ? *limits : (lunelette_metal_limits){256, 256};
-    if (!profile_supported(resolved)) {
-        snprintf(error, capacity, "unsupported context/block profile");
-        return NULL;
-    }
-    lunelette_metal_options selected;
-    if (resolve_options(options, &selected, error, capacity)) {
-        return NULL;
-    }
-    if (!config || config->layers < 1 || config->layers > LH_LAYERS) {
-        snprintf(error, capacity, "synthetic model needs 1..26 layers");
-        return NULL;
-    }
     int devices = 0;
     if (hipGetDeviceCount(&devices) != hipSuccess || devices < 1) {
         snprintf(error, capacity, "no HIP device: the gfx950 runtime needs an MI355X");
@@ -354,7 +403,7 @@ lunelette_metal *lunelette_metal_create_synthetic(const lunelette_synthetic_conf
     rt->limits = resolved;
     rt->prefill_mode = selected.prefill;
     rt->strategy = selected.strategy;
-    rt->layers = config->layers;
+    rt->layers = layers;
     /* LUNELETTE_HIP_GRAPHS=1 replays one-token steps as a HIP graph (opt-in:
      * on MI355X it measures level with kernel-by-kernel launches, and
      * rocprofv3 kernel tracing of graph replays has crashed the host process). */
@@ -368,7 +417,6 @@ lunelette_metal *lunelette_metal_create_synthetic(const lunelette_synthetic_conf
     const uint64_t norm_bytes = (2ull * rt->layers + 1) * LH_HIDDEN * sizeof(float);
     const uint64_t kv_bytes = 2ull * rt->layers * LH_KV_HEADS * C * LH_HEAD_DIM * sizeof(float);
     uploader up = {0};
-    uint64_t seed = config->seed;
     if (hip_ok(hipStreamCreate(&rt->stream), "stream creation", error, capacity) ||
         hip_ok(hipEventCreate(&rt->started), "event creation", error, capacity) ||
         hip_ok(hipEventCreate(&rt->finished), "event creation", error, capacity)) {
@@ -416,9 +464,9 @@ lunelette_metal *lunelette_metal_create_synthetic(const lunelette_synthetic_conf
             goto failure;
         }
     }
-    if (upload_bf16_normal(&up, seed, 0, 0.0f, 0.02f, (size_t)LH_VOCAB * LH_HIDDEN,
-            rt->d_embedding, error, capacity) ||
-        upload_norm(&up, seed, 1, rt->d_norms + 2ull * rt->layers * LH_HIDDEN, error, capacity)) {
+    if (upload_bf16(&up, src, 0, (size_t)LH_VOCAB * LH_HIDDEN, rt->d_embedding, error,
+            capacity) ||
+        upload_norm(&up, src, 1, rt->d_norms + 2ull * rt->layers * LH_HIDDEN, error, capacity)) {
         goto failure;
     }
     static const size_t rows[7] = {LH_QUERY, LH_KV, LH_KV, LH_HIDDEN, LH_INNER, LH_INNER, LH_HIDDEN};
@@ -434,8 +482,8 @@ lunelette_metal *lunelette_metal_create_synthetic(const lunelette_synthetic_conf
         for (int i = 0; i < 7; i++) {
             const uint32_t tensor = 2 + 9 * l + slot[i];
             ptr[i] = base + offset;
-            w->scale[i] = lh_synth_scale(seed, tensor);
-            if (upload_fp8(&up, seed, tensor, w->scale[i], rows[i] * cols[i], resident, ptr[i],
+            w->scale[i] = src->scale(src, tensor);
+            if (upload_fp8(&up, src, tensor, w->scale[i], rows[i] * cols[i], resident, ptr[i],
                     error, capacity)) {
                 goto failure;
             }
@@ -456,8 +504,8 @@ lunelette_metal *lunelette_metal_create_synthetic(const lunelette_synthetic_conf
         }
         float *in_norm = rt->d_norms + 2ull * l * LH_HIDDEN;
         float *post_norm = in_norm + LH_HIDDEN;
-        if (upload_norm(&up, seed, 2 + 9 * l + 0, in_norm, error, capacity) ||
-            upload_norm(&up, seed, 2 + 9 * l + 5, post_norm, error, capacity)) {
+        if (upload_norm(&up, src, 2 + 9 * l + 0, in_norm, error, capacity) ||
+            upload_norm(&up, src, 2 + 9 * l + 5, post_norm, error, capacity)) {
             goto failure;
         }
         w->input_norm = in_norm;
@@ -509,6 +557,35 @@ failure:
     return NULL;
 }
 
+lunelette_metal *lunelette_metal_create_synthetic(const lunelette_synthetic_config *config,
+    const lunelette_metal_options *options, const lunelette_metal_limits *limits,
+    char *error, size_t capacity)
+{
+    char fallback[512];
+    if (!error || !capacity) {
+        error = fallback;
+        capacity = sizeof fallback;
+    }
+    lunelette_metal_limits resolved = limits ? *limits : (lunelette_metal_limits){256, 256};
+    if (!profile_supported(resolved)) {
+        snprintf(error, capacity, "unsupported context/block profile");
+        return NULL;
+    }
+    lunelette_metal_options selected;
+    if (resolve_options(options, &selected, error, capacity)) {
+        return NULL;
+    }
+    if (!config || config->layers < 1 || config->layers > LH_LAYERS) {
+        snprintf(error, capacity, "synthetic model needs 1..26 layers");
+        return NULL;
+    }
+    weight_source src = {synthetic_read, synthetic_scale, config->seed, NULL};
+    return build_runtime(&src, config->layers, resolved, selected, error, capacity);
+}
+
+/* src/metal_runtime.m:199-330: profile, options, then the checkpoint
+ * (container, tensor contract, scales) before any device allocation; FP8
+ * codes are admitted tensor by tensor during the upload. */
 lunelette_metal *lunelette_metal_create_configured(const char *path,
     const lunelette_metal_options *options, const lunelette_metal_limits *limits,
     char *error, size_t capacity)
@@ -527,13 +604,21 @@ lunelette_metal *lunelette_metal_create_configured(const char *path,
     if (resolve_options(options, &selected, error, capacity)) {
         return NULL;
     }
-    if (!path) {
-        snprintf(error, capacity, "requires one explicit FP8 safetensors path");
+    lh_weights *checkpoint = malloc(sizeof *checkpoint);
+    if (!checkpoint) {
+        snprintf(error, capacity, "checkpoint handle allocation failed");
         return NULL;
     }
-    snprintf(error, capacity, "safetensors checkpoint loading is not built in this library; "
-        "use lunelette_metal_create_synthetic");
-    return NULL;
+    if (lh_weights_open(checkpoint, path, error, capacity)) {
+        free(checkpoint);
+        return NULL;
+    }
+    weight_source src = {file_read, file_scale, 0, checkpoint};
+    lunelette_metal *context = build_runtime(&src, LH_LAYERS, resolved, selected, error,
+        capacity);
+    lh_weights_close(checkpoint);
+    free(checkpoint);
+    return context;
 }
 
 lunelette_metal *lunelette_metal_create_with_options(const char *path,

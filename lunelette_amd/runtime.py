@@ -17,15 +17,24 @@ class RuntimeError_(RuntimeError):
 
 
 class Runtime:
+    """A runtime context over the seeded synthetic model, or over the FP8
+    safetensors checkpoint at `path` (lunelette_metal_create_configured; all
+    26 layers)."""
+
     def __init__(self, seed=1, layers=26, context=4352, block=256, prefill=PREFILL_MPS,
-                 strategy=COMPACT_FP8_ARITHMETIC):
+                 strategy=COMPACT_FP8_ARITHMETIC, path=None):
         self._lib = lib()
         self._err = ctypes.create_string_buffer(512)
-        cfg = SyntheticConfig(seed, layers)
         opts = Options(prefill, strategy)
         lim = Limits(context, block)
-        self.handle = self._lib.lunelette_metal_create_synthetic(
-            ctypes.byref(cfg), ctypes.byref(opts), ctypes.byref(lim), self._err, 512)
+        if path is None:
+            cfg = SyntheticConfig(seed, layers)
+            self.handle = self._lib.lunelette_metal_create_synthetic(
+                ctypes.byref(cfg), ctypes.byref(opts), ctypes.byref(lim), self._err, 512)
+        else:
+            layers = 26
+            self.handle = self._lib.lunelette_metal_create_configured(
+                str(path).encode(), ctypes.byref(opts), ctypes.byref(lim), self._err, 512)
         if not self.handle:
             raise RuntimeError_("create failed: " + self._err.value.decode())
         self.layers, self.context, self.block = layers, context, block

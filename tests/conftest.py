@@ -12,6 +12,9 @@ if HERE not in sys.path:
 
 
 def pytest_configure(config):
+    # Temporary files (checkpoint containers) stay inside the repository tree.
+    if not config.option.basetemp:
+        config.option.basetemp = os.path.join(ROOT, ".pytest_tmp")
     config.addinivalue_line("markers", "gpu: needs an MI355X (gfx950) device")
     config.addinivalue_line("markers", "slow: long CPU oracle runs")
 

@@ -72,7 +72,8 @@ def load():
 
 
 def load_ref():
-    """The reference's own C (FP8/BF16 decode, YaRN, greedy), or None."""
+    """The reference's own C (safetensors container, checkpoint contract, FP8/BF16
+    decode, YaRN, greedy), or None."""
     global _ref
     if _ref is None and os.path.exists(REFLIB):
         l = ctypes.CDLL(REFLIB)
