@@ -275,7 +275,7 @@ extern "C" int lh_launch_embed(const uint16_t* E, const lh_step_params* params, 
 // Per 64-position block:
 //   S[16 x 64] = Q[16 x 128] K^T: lane group g = lane/16 feeds dims
 //     32g .. 32g+31 (one per MFMA step) of both operands; Q stays in registers.
-//   online softmax per token row (exp as in the decode kernels), causal mask
+//   online softmax per token row in the base-2 domain (v_exp_f32), causal mask
 //   p <= length + t;
 //   O[16 x 128] += P[16 x 64] V through a per-wave P tile in LDS: lane group g
 //     feeds positions 16g .. 16g+15.
@@ -297,6 +297,10 @@ constexpr uint32_t FA_TQ = 16;                      // tokens per workgroup
 constexpr uint32_t FA_KS = LH_HEAD_DIM + 4;         // K tile row stride (floats)
 constexpr uint32_t FA_VS = LH_HEAD_DIM + 1;         // V tile row stride
 constexpr uint32_t FA_PS = LH_ATTN_BLOCK + 4;       // P tile row stride
+// Scores in the base-2 domain: s = q.k * (1/sqrt(128)) * log2(e), so the
+// softmax weights are exp2(s - m) on the hardware v_exp_f32; the row maxima
+// in PM are in this domain too (k_attn_merge).
+constexpr float FA_SCALE_LOG2 = 0.12751743074062763f;
 
 typedef float fa_floatx4 __attribute__((ext_vector_type(4)));
 
@@ -423,7 +427,7 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const uint32_t p = b * LH_ATTN_BLOCK + 16 * j + l16;
-                const float v = p <= limit[r] ? s[j][r] * LH_SCORE_SCALE : -__builtin_inff();
+                const float v = p <= limit[r] ? s[j][r] * FA_SCALE_LOG2 : -__builtin_inff();
                 s[j][r] = v;
                 mx = fmaxf(mx, v);
             }
@@ -432,11 +436,11 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
             // the row empty (no exp of -inf - -inf).
             const float m_new = fmaxf(m[r], mx);
             const bool empty = m_new == -__builtin_inff();
-            const float alpha = empty ? 1.0f : expf_cw(m[r] - m_new);
+            const float alpha = empty ? 1.0f : __builtin_amdgcn_exp2f(m[r] - m_new);
             float sum = 0.0f;
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const float e = empty ? 0.0f : expf_cw(s[j][r] - m_new);
+                const float e = empty ? 0.0f : __builtin_amdgcn_exp2f(s[j][r] - m_new);
                 sum = sum + e;
                 pw[(4 * g + r) * FA_PS + 16 * j + l16] = e;
             }
@@ -501,7 +505,7 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
 }
 
 // Merge of k_attn_mfma's KV splits (tolerance path): per (token, head)
-// M = max m_z, f_z = exp(m_z - M), out = (sum f_z O_z) / (sum f_z l_z) with
+// M = max m_z, f_z = exp2(m_z - M) (base-2 maxima), out = (sum f_z O_z) / (sum f_z l_z) with
 // the sums in split order. A split whose positions are all masked for the row
 // holds m = -inf, l = 0, O = 0 and contributes nothing; split 0 always holds
 // position 0, so M is finite. grid (count * 8), block 256: one wave per
@@ -526,7 +530,7 @@ k_attn_merge(const float* __restrict__ PM, const float* __restrict__ PT,
     float2 A = make_float2(0.0f, 0.0f);
     float T = 0.0f;
     for (uint32_t z = 0; z < parts; z++) {
-        const float f = expf_cw(pm[z] - M);
+        const float f = __builtin_amdgcn_exp2f(pm[z] - M);
         const float2 a = pa[(size_t)z * (LH_HEAD_DIM / 2)];
         A.x = __builtin_fmaf(f, a.x, A.x);
         A.y = __builtin_fmaf(f, a.y, A.y);
