@@ -286,7 +286,7 @@ extern "C" int lh_launch_embed(const uint16_t* E, const lh_step_params* params, 
 // output goes to xs as the hi/mid/lo BF16 planes the o-projection GEMM reads
 // (plane stride xs_tokens * 4096) instead of FP32 rows of out.
 // LDS is the K tile (33 KiB, reused for the four P tiles after a barrier) and
-// the V tile (33 KiB), under 184 registers, so two workgroups share a CU and
+// the V tile (33 KiB), under 256 registers, so two workgroups share a CU and
 // the launcher sizes splits for about 512 workgroups. Measured alternative:
 // BF16 MFMA with both operands split in three exact planes (six products per
 // k chunk) ran at 1.2x on long prefixes and 0.6x on short ones, its K/V
@@ -375,7 +375,8 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
     float* pw = Ps[wave];
     // K and V of block b in registers (thread tid holds float4 words
     // tid + 256i of each 64 x 128 tile); every row is inside the capacity
-    // (the block count never exceeds it). Two workgroups share a CU, so one
+    // (the block count never exceeds it). The next block's loads are issued
+    // before this block's MFMAs, and two workgroups share a CU, so one
     // stages its tiles while the other runs MFMAs.
     fa_floatx4 kr[8], vr[8];
     auto load_block = [&](uint32_t b) {
@@ -389,8 +390,10 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
             vr[i] = vb[tid + 256 * i];
         }
     };
+    if (b_begin < b_end) {
+        load_block(b_begin);
+    }
     for (uint32_t b = b_begin; b < b_end; b++) {
-        load_block(b);
         // Stage K (float4 rows, stride 132) and V (stride 129) of the block.
         __syncthreads();   // the previous block's tiles are consumed
 #pragma unroll
@@ -404,6 +407,9 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
             vd[3] = vr[i].w;
         }
         __syncthreads();
+        if (b + 1 < b_end) {
+            load_block(b + 1);   // in flight during this block's MFMAs
+        }
         // S tiles j = 0..3: positions 16j + l16 of the block.
         fa_floatx4 s[4];
 #pragma unroll
