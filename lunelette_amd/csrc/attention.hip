@@ -565,11 +565,12 @@ extern "C" int lh_launch_attention_mfma(const float* q, const float* kcache_laye
         return -1;
     }
     // KV splits so that about 512 workgroups run (two per CU): each takes at
-    // least 4 blocks of the longest tile, at most one partial per block.
+    // least 2 blocks of the longest tile (a 256-token chunk with no prefix
+    // runs 2 splits), at most one partial per block.
     const uint32_t tiles = (count + lh::FA_TQ - 1) / lh::FA_TQ;
     const uint32_t nb = (length + count + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
     uint32_t splits = 512 / (tiles * LH_KV_HEADS);
-    const uint32_t by_length = nb / 4;
+    const uint32_t by_length = nb / 2;
     splits = splits < by_length ? splits : by_length;
     splits = splits ? splits : 1;
     hipLaunchKernelGGL(lh::k_attn_mfma, dim3(tiles, LH_KV_HEADS, splits), dim3(256), 0, s, q,
