@@ -104,12 +104,15 @@ def test_mfma_layer_small_odd_block(gpu):
     assert np.max(np.abs(gx - wx) / np.max(np.abs(wx), axis=1, keepdims=True)) < 1e-3
 
 
-def test_runtime_mps_prefill_then_decode(gpu):
+@pytest.mark.parametrize("prompt", [64, 200])
+def test_runtime_mps_prefill_then_decode(gpu, prompt):
+    """Chained layers (each layer's last kernel splits the next layer's
+    input); 200 tokens end in a partial 64-token GEMM tile."""
     from test_gpu_runtime import LAYERS, SEED as RSEED, oracle_model
     embedding = syn.embedding(RSEED)
     host = (embedding, syn.final_norm(RSEED), [syn.layer(RSEED, i) for i in range(LAYERS)])
     model = oracle_model(host)
-    ids = syn.tokens(RSEED, 11, 64)
+    ids = syn.tokens(RSEED, 11, prompt)
     with Runtime(seed=RSEED, layers=LAYERS, context=256, block=256,
                  prefill=lh.PREFILL_MPS) as rt:
         got = rt.prefill(ids)
