@@ -138,16 +138,32 @@ k_attn_combine(const float* __restrict__ PM, const float* __restrict__ PT,
     __shared__ float4 sg[ROUND / GROUP][8];
     __shared__ float ug[ROUND / GROUP];
     const uint32_t h = blockIdx.x >> 2, qd = blockIdx.x & 3, t = blockIdx.y;
-    const uint32_t n = params->length + t + 1;
-    const uint32_t nb = (n + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
     const uint32_t nbc = capacity / LH_ATTN_BLOCK;
     const size_t th = (size_t)t * LH_HEADS + h;
     const float* pm = PM + th * nbc;
     const float* pt = PT + th * nbc;
     const uint32_t tid = threadIdx.x, c = tid & 7, s = tid >> 3;
     const float4* pa = reinterpret_cast<const float4*>(PA + th * nbc * LH_HEAD_DIM) + 8 * qd + c;
-    float M = -__builtin_inff();
-    for (uint32_t j = tid; j < nb; j += 256) {
+    // A round's partial loads are clamped to the capacity, not to the valid
+    // block count, so the first round's issue before the step record is
+    // read; rows past the valid count never enter arithmetic.
+    float4 a[GROUP];
+    float m_own, t_own;
+    auto load_round = [&](uint32_t r0) {
+#pragma unroll
+        for (uint32_t k = 0; k < GROUP; k++) {
+            const uint32_t bb = r0 + s * GROUP + k;
+            a[k] = pa[(size_t)(bb < nbc ? bb : nbc - 1) * (LH_HEAD_DIM / 4)];
+        }
+        const uint32_t bb = r0 + tid < nbc ? r0 + tid : nbc - 1;
+        m_own = pm[bb];
+        t_own = pt[bb];
+    };
+    load_round(0);
+    const uint32_t n = params->length + t + 1;
+    const uint32_t nb = (n + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
+    float M = tid < nb ? m_own : -__builtin_inff();
+    for (uint32_t j = tid + ROUND; j < nb; j += ROUND) {
         M = fmaxf(M, pm[j]);
     }
     M = wave_max64(M);
@@ -159,17 +175,13 @@ k_attn_combine(const float* __restrict__ PM, const float* __restrict__ PT,
     float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
     float T = 0.0f;
     for (uint32_t r0 = 0; r0 < nb; r0 += ROUND) {
-        // Every load of the round issues before the first wait (clamped rows).
-        float4 a[GROUP];
-#pragma unroll
-        for (uint32_t k = 0; k < GROUP; k++) {
-            const uint32_t bb = r0 + s * GROUP + k;
-            a[k] = pa[(size_t)(bb < nb ? bb : nb - 1) * (LH_HEAD_DIM / 4)];
+        if (r0) {
+            load_round(r0);
         }
         {
             const uint32_t bb = r0 + tid;
-            fs[tid] = bb < nb ? expf_cw(pm[bb] - M) : 0.0f;
-            ts[tid] = bb < nb ? pt[bb] : 0.0f;
+            fs[tid] = bb < nb ? expf_cw(m_own - M) : 0.0f;
+            ts[tid] = bb < nb ? t_own : 0.0f;
         }
         __syncthreads();
         float4 Sg = make_float4(0.f, 0.f, 0.f, 0.f);
