@@ -18,22 +18,23 @@ static void say(char *error, size_t capacity, const char *text)
 
 /* The reference's forward scan with a strict > keeps the first index of the
  * maximum (-0.0 and +0.0 compare equal) and fails at the first nonfinite
- * logit; the same result comes from three vectorized passes: the first
- * nonfinite index, the maximum, the first index equal to it. */
+ * logit; the same result comes from two vectorized passes: the maximum
+ * together with a nonfinite flag (then, only on failure, the first
+ * nonfinite index), and the first index equal to the maximum. */
 int lunelette_select_greedy(const float *logits, int64_t *token, char *error, size_t capacity)
 {
     if (!logits || !token) {
         say(error, capacity, "selection: require logits and token");
         return -1;
     }
-    const size_t bad = lh_first_nonfinite(logits, LUNELETTE_VOCAB_SIZE);
-    if (bad < LUNELETTE_VOCAB_SIZE) {
+    float best_value;
+    if (!lh_max_all_finite(logits, LUNELETTE_VOCAB_SIZE, &best_value)) {
         if (error && capacity) {
-            snprintf(error, capacity, "selection: nonfinite logit at token %zu", bad);
+            snprintf(error, capacity, "selection: nonfinite logit at token %zu",
+                lh_first_nonfinite(logits, LUNELETTE_VOCAB_SIZE));
         }
         return -1;
     }
-    const float best_value = lh_max(logits, LUNELETTE_VOCAB_SIZE);
     *token = (int64_t)lh_first_equal(logits, LUNELETTE_VOCAB_SIZE, best_value);
     if (error && capacity) {
         error[0] = '\0';

@@ -37,23 +37,33 @@ __attribute__((optimize("tree-vectorize"))) static inline size_t lh_first_nonfin
     return i;
 }
 
-/* Maximum of n finite values (n a positive multiple of LH_SCAN_LANES). */
-__attribute__((optimize("tree-vectorize"))) static inline float lh_max(const float *v, size_t n)
+/* One pass: the maximum of v into *best and whether every value is finite
+ * (n a positive multiple of LH_SCAN_LANES); *best is meaningful only when
+ * every value is finite. */
+__attribute__((optimize("tree-vectorize"))) static inline int lh_max_all_finite(const float *v,
+    size_t n, float *best)
 {
     float lane_max[LH_SCAN_LANES];
+    uint32_t lane_bad[LH_SCAN_LANES] = {0};
     for (size_t k = 0; k < LH_SCAN_LANES; k++) {
         lane_max[k] = v[k];
     }
     for (size_t i = 0; i < n; i += LH_SCAN_LANES) {
         for (size_t k = 0; k < LH_SCAN_LANES; k++) {
+            uint32_t bits;
+            memcpy(&bits, &v[i + k], sizeof bits);
+            lane_bad[k] |= (bits & 0x7f800000u) == 0x7f800000u;
             lane_max[k] = v[i + k] > lane_max[k] ? v[i + k] : lane_max[k];
         }
     }
-    float best = lane_max[0];
-    for (size_t k = 1; k < LH_SCAN_LANES; k++) {
-        best = lane_max[k] > best ? lane_max[k] : best;
+    uint32_t bad = 0;
+    float m = lane_max[0];
+    for (size_t k = 0; k < LH_SCAN_LANES; k++) {
+        bad |= lane_bad[k];
+        m = lane_max[k] > m ? lane_max[k] : m;
     }
-    return best;
+    *best = m;
+    return !bad;
 }
 
 /* First index whose value equals x (x occurs in v[0, n)). */
