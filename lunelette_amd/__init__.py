@@ -2,9 +2,9 @@
 
 The product is the C-ABI shared library lunelette_amd/liblunelette_hip.so
 (include/lunelette_runtime.h, include/lunelette_kernels.h,
-include/lunelette_generation.h). This module only loads it and declares
-prototypes; it never substitutes another implementation. If the library has
-not been built, `lib()` raises.
+include/lunelette_generation.h, include/lunelette_session.h). This module
+only loads it and declares prototypes; it never substitutes another
+implementation. If the library has not been built, `lib()` raises.
 """
 import ctypes
 import os
@@ -172,8 +172,53 @@ def lib():
     _proto(l, "lunelette_generate_with_logits_capacity", i, LOGITS_FN, c_void, c_int64_p, c_size,
            c_size, ctypes.POINTER(GenerationConfig), ctypes.POINTER(GenerationResult), err,
            c_size)
+    declare_session(l)
     _lib = l
     return l
+
+
+class SessionWork(ctypes.Structure):
+    """lunelette_session_work: the receipt of the last materialize/restore."""
+    _fields_ = [(name, ctypes.c_uint) for name in (
+        "reused", "full_attempted", "full_committed", "suffix_attempted", "suffix_committed",
+        "pending_attempted", "pending_committed", "prefill_calls", "append_calls",
+        "decode_calls", "decode_attempted", "decode_committed", "logit_restores",
+        "recompute_attempted", "recompute_committed")]
+
+
+class SessionOptions(ctypes.Structure):
+    _fields_ = [("context", c_size), ("block", c_size), ("prefix_reuse", ctypes.c_int),
+                ("replay_path", ctypes.c_char_p)]
+
+
+def declare_session(l):
+    """Prototypes of include/lunelette_session.h on a loaded library (the
+    product, or a test library that links the adapter with another runtime)."""
+    i, u, v = ctypes.c_int, ctypes.c_uint, None
+    err = ctypes.c_char_p
+    u_p = ctypes.POINTER(ctypes.c_uint)
+    _proto(l, "lunelette_session_open", c_void, ctypes.c_char_p, ctypes.POINTER(Options),
+           ctypes.POINTER(SessionOptions), err, c_size)
+    _proto(l, "lunelette_session_adopt", c_void, c_void, ctypes.POINTER(Options),
+           ctypes.POINTER(SessionOptions), err, c_size)
+    _proto(l, "lunelette_session_destroy", v, c_void)
+    _proto(l, "lunelette_session_materialize", i, c_void, u_p, u)
+    _proto(l, "lunelette_session_materialize_step", i, c_void, u_p, u, u_p)
+    _proto(l, "lunelette_session_next", i, c_void)
+    _proto(l, "lunelette_session_replay_next", i, c_void, u)
+    _proto(l, "lunelette_session_save", i, c_void)
+    _proto(l, "lunelette_session_restore", i, c_void)
+    _proto(l, "lunelette_session_begin", v, c_void)
+    _proto(l, "lunelette_session_take_work", v, c_void, ctypes.POINTER(SessionWork))
+    _proto(l, "lunelette_session_invalidate", v, c_void)
+    _proto(l, "lunelette_session_reset", v, c_void)
+    _proto(l, "lunelette_session_length", u, c_void)
+    _proto(l, "lunelette_session_context_capacity", u, c_void)
+    _proto(l, "lunelette_session_block_capacity", u, c_void)
+    _proto(l, "lunelette_session_prefix_reuse", u, c_void)
+    _proto(l, "lunelette_session_error", ctypes.c_char_p, c_void)
+    _proto(l, "lunelette_session_logits", c_float_p, c_void)
+    _proto(l, "lunelette_session_info", ctypes.c_char_p, c_void)
 
 
 def last_error():

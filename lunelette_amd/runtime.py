@@ -38,6 +38,7 @@ class Runtime:
         if not self.handle:
             raise RuntimeError_("create failed: " + self._err.value.decode())
         self.layers, self.context, self.block = layers, context, block
+        self.prefill_mode, self.strategy = prefill, strategy
         self._logits = c_float_p()
 
     def close(self):
