@@ -18,24 +18,23 @@ static void say(char *error, size_t capacity, const char *text)
 
 /* The reference's forward scan with a strict > keeps the first index of the
  * maximum (-0.0 and +0.0 compare equal) and fails at the first nonfinite
- * logit; the same result comes from two vectorized passes: the maximum
- * together with a nonfinite flag (then, only on failure, the first
- * nonfinite index), and the first index equal to the maximum. */
+ * logit; lh_argmax_all_finite gives the same index in one vectorized pass,
+ * and only on failure a second pass names the first nonfinite logit. */
 int lunelette_select_greedy(const float *logits, int64_t *token, char *error, size_t capacity)
 {
     if (!logits || !token) {
         say(error, capacity, "selection: require logits and token");
         return -1;
     }
-    float best_value;
-    if (!lh_max_all_finite(logits, LUNELETTE_VOCAB_SIZE, &best_value)) {
+    size_t best;
+    if (!lh_argmax_all_finite(logits, LUNELETTE_VOCAB_SIZE, &best)) {
         if (error && capacity) {
             snprintf(error, capacity, "selection: nonfinite logit at token %zu",
                 lh_first_nonfinite(logits, LUNELETTE_VOCAB_SIZE));
         }
         return -1;
     }
-    *token = (int64_t)lh_first_equal(logits, LUNELETTE_VOCAB_SIZE, best_value);
+    *token = (int64_t)best;
     if (error && capacity) {
         error[0] = '\0';
     }

@@ -1,5 +1,8 @@
-/* Host scans over the 131072 logits of a step, written so that gcc -O2
- * vectorizes them (16 independent lanes, no early exit in the hot loop). */
+/* Host scans over the 131072 logits of a step: GCC vector types with four
+ * independent accumulators, branch-free over whole vectors. Two instances
+ * are built from lh_scan_body.h, 16-byte vectors for the x86-64 baseline and
+ * 32-byte vectors for AVX2, and each call takes the AVX2 one when the CPU
+ * has it (about 3x faster). n is a multiple of 32 in every function. */
 #ifndef LH_SCAN_H
 #define LH_SCAN_H
 
@@ -8,83 +11,44 @@
 #include <stdint.h>
 #include <string.h>
 
-#define LH_SCAN_LANES 16
+#define LH_SCAN_ISA sse2
+#define LH_SCAN_TARGET
+#define LH_SCAN_BYTES 16
+#include "lh_scan_body.h"
+#undef LH_SCAN_BYTES
+#undef LH_SCAN_TARGET
+#undef LH_SCAN_ISA
+
+#define LH_SCAN_ISA avx2
+#define LH_SCAN_TARGET __attribute__((target("avx2")))
+#define LH_SCAN_BYTES 32
+#include "lh_scan_body.h"
+#undef LH_SCAN_BYTES
+#undef LH_SCAN_TARGET
+#undef LH_SCAN_ISA
+
+static inline int lh_scan_avx2(void)
+{
+    return __builtin_cpu_supports("avx2");
+}
 
 /* Index of the first nonfinite value (exponent bits all ones), or n when
- * every value is finite; n a multiple of LH_SCAN_LANES. */
-__attribute__((optimize("tree-vectorize"))) static inline size_t lh_first_nonfinite(
-    const float *v, size_t n)
-{
-    uint32_t lane_bad[LH_SCAN_LANES] = {0};
-    for (size_t i = 0; i < n; i += LH_SCAN_LANES) {
-        for (size_t k = 0; k < LH_SCAN_LANES; k++) {
-            uint32_t bits;
-            memcpy(&bits, &v[i + k], sizeof bits);
-            lane_bad[k] |= (bits & 0x7f800000u) == 0x7f800000u;
-        }
-    }
-    uint32_t bad = 0;
-    for (size_t k = 0; k < LH_SCAN_LANES; k++) {
-        bad |= lane_bad[k];
-    }
-    if (!bad) {
-        return n;
-    }
-    size_t i = 0;
-    while (isfinite(v[i])) {
-        i++;
-    }
-    return i;
-}
-
-/* One pass: the maximum of v into *best and whether every value is finite
- * (n a positive multiple of LH_SCAN_LANES); *best is meaningful only when
  * every value is finite. */
-__attribute__((optimize("tree-vectorize"))) static inline int lh_max_all_finite(const float *v,
-    size_t n, float *best)
+static inline size_t lh_first_nonfinite(const float *v, size_t n)
 {
-    float lane_max[LH_SCAN_LANES];
-    uint32_t lane_bad[LH_SCAN_LANES] = {0};
-    for (size_t k = 0; k < LH_SCAN_LANES; k++) {
-        lane_max[k] = v[k];
-    }
-    for (size_t i = 0; i < n; i += LH_SCAN_LANES) {
-        for (size_t k = 0; k < LH_SCAN_LANES; k++) {
-            uint32_t bits;
-            memcpy(&bits, &v[i + k], sizeof bits);
-            lane_bad[k] |= (bits & 0x7f800000u) == 0x7f800000u;
-            lane_max[k] = v[i + k] > lane_max[k] ? v[i + k] : lane_max[k];
-        }
-    }
-    uint32_t bad = 0;
-    float m = lane_max[0];
-    for (size_t k = 0; k < LH_SCAN_LANES; k++) {
-        bad |= lane_bad[k];
-        m = lane_max[k] > m ? lane_max[k] : m;
-    }
-    *best = m;
-    return !bad;
+    return lh_scan_avx2() ? lh_first_nonfinite_avx2(v, n) : lh_first_nonfinite_sse2(v, n);
 }
 
-/* First index whose value equals x (x occurs in v[0, n)). */
-__attribute__((optimize("tree-vectorize"))) static inline size_t lh_first_equal(const float *v,
-    size_t n, float x)
+/* One pass over v: whether every value is finite and, if so, the first
+ * index of the maximum in *index. Each lane of the four accumulators keeps
+ * the maximum of its residue class of indices under a strict '>' and the
+ * pass in which it first occurred; the first index of the overall maximum
+ * is the smallest such index among the lanes that hold it (-0.0 and +0.0
+ * compare equal), which is what a forward scan with a strict '>' selects. */
+static inline int lh_argmax_all_finite(const float *v, size_t n, size_t *index)
 {
-    size_t block = 0;
-    for (; block < n; block += LH_SCAN_LANES) {
-        uint32_t hit = 0;
-        for (size_t k = 0; k < LH_SCAN_LANES; k++) {
-            hit |= v[block + k] == x;
-        }
-        if (hit) {
-            break;
-        }
-    }
-    size_t i = block;
-    while (i < n && v[i] != x) {
-        i++;
-    }
-    return i;
+    return lh_scan_avx2() ? lh_argmax_all_finite_avx2(v, n, index) :
+        lh_argmax_all_finite_sse2(v, n, index);
 }
 
 #endif
