@@ -2,9 +2,10 @@
 
 The product is the C-ABI shared library lunelette_amd/liblunelette_hip.so
 (include/lunelette_runtime.h, include/lunelette_kernels.h,
-include/lunelette_generation.h, include/lunelette_session.h). This module
-only loads it and declares prototypes; it never substitutes another
-implementation. If the library has not been built, `lib()` raises.
+include/lunelette_generation.h, include/lunelette_session.h,
+include/lunelette_artifacts.h). This module only loads it and declares
+prototypes; it never substitutes another implementation. If the library has
+not been built, `lib()` raises.
 """
 import ctypes
 import os
@@ -173,6 +174,7 @@ def lib():
            c_size, ctypes.POINTER(GenerationConfig), ctypes.POINTER(GenerationResult), err,
            c_size)
     declare_session(l)
+    declare_artifacts(l)
     _lib = l
     return l
 
@@ -276,3 +278,31 @@ class DeviceBuffer:
 def check(status, what="call"):
     if status != 0:
         raise RuntimeError("%s failed: %s" % (what, last_error()))
+
+
+class LogitMetrics(ctypes.Structure):
+    """lunelette_logit_metrics."""
+    _fields_ = [("finite_a", c_size), ("finite_b", c_size), ("exact", ctypes.c_int),
+                ("top1_a", c_size), ("top1_b", c_size), ("top5", c_size), ("top20", c_size),
+                ("top64", c_size), ("max_abs", ctypes.c_double), ("rms", ctypes.c_double),
+                ("cosine", ctypes.c_double)]
+
+
+class NativeTrajectory(ctypes.Structure):
+    """lunelette_native_trajectory."""
+    _fields_ = [("magic", ctypes.c_uint32), ("strategy", ctypes.c_int), ("mode", ctypes.c_uint32),
+                ("count", c_size), ("ids", ctypes.c_int64 * 248), ("forced", ctypes.c_int64 * 8)]
+
+
+def declare_artifacts(l):
+    """Prototypes of include/lunelette_artifacts.h on a loaded library."""
+    i, err = ctypes.c_int, ctypes.c_char_p
+    traj = ctypes.POINTER(NativeTrajectory)
+    metrics = ctypes.POINTER(LogitMetrics)
+    _proto(l, "lunelette_logits_top64", None, c_float_p, c_size, ctypes.POINTER(c_size))
+    _proto(l, "lunelette_logits_compare", i, c_float_p, c_float_p, c_size, metrics)
+    _proto(l, "lunelette_native_write", i, ctypes.c_char_p, traj, c_float_p, err, c_size)
+    _proto(l, "lunelette_native_read", i, ctypes.c_char_p, traj, c_float_p, err, c_size)
+    _proto(l, "lunelette_native_compare_files", i, ctypes.c_char_p, ctypes.c_char_p,
+           ctypes.c_uint32, c_size, ctypes.c_int, metrics, err, c_size)
+    _proto(l, "lunelette_native_run", i, c_void, ctypes.c_char_p, traj, i, metrics, err, c_size)

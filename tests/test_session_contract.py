@@ -21,6 +21,7 @@ import numpy as np
 import pytest
 
 import lunelette_amd as lh
+from lunelette_amd import artifacts
 from lunelette_amd.session import LEGACY, MORE, REUSE_OFF, REUSE_ON, Session
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
@@ -440,6 +441,12 @@ def test_replay_capture(stub, tmp_path):
     s.close()
     records = read_capture(path)
     assert len(records) == 16
+    # The replay tool's reader accepts the capture and correlates it with the
+    # authoritative trajectory.
+    forced_ids = [int(t) for t in ids[3:]]
+    steps = [dict(replay_tokens=forced_ids, actual_ids=forced_ids,
+                  before_prefix_ids=[int(t) for t in ids[:3]])]
+    assert artifacts.verify_replay(path, steps)["verified_records"] == 16
     for k, (index, prefix, forced, greedy, logits) in enumerate(records):
         assert index == k and prefix == ids[:3 + k] and forced == ids[3 + k]
         assert greedy == GREEDY
