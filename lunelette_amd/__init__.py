@@ -3,7 +3,8 @@
 The product is the C-ABI shared library lunelette_amd/liblunelette_hip.so
 (include/lunelette_runtime.h, include/lunelette_kernels.h,
 include/lunelette_generation.h, include/lunelette_session.h,
-include/lunelette_artifacts.h). This module only loads it and declares
+include/lunelette_artifacts.h, include/lunelette_tokenizer.h,
+include/lunelette_chat.h). This module only loads it and declares
 prototypes; it never substitutes another implementation. If the library has
 not been built, `lib()` raises.
 """
@@ -175,6 +176,7 @@ def lib():
            c_size)
     declare_session(l)
     declare_artifacts(l)
+    declare_tokenizer(l)
     _lib = l
     return l
 
@@ -306,3 +308,25 @@ def declare_artifacts(l):
     _proto(l, "lunelette_native_compare_files", i, ctypes.c_char_p, ctypes.c_char_p,
            ctypes.c_uint32, c_size, ctypes.c_int, metrics, err, c_size)
     _proto(l, "lunelette_native_run", i, c_void, ctypes.c_char_p, traj, i, metrics, err, c_size)
+
+
+def declare_tokenizer(l):
+    """Prototypes of include/lunelette_tokenizer.h and include/lunelette_chat.h
+    (the product, or the reference's tokenizer built from source)."""
+    i, err = ctypes.c_int, ctypes.c_char_p
+    u32_pp = ctypes.POINTER(ctypes.POINTER(ctypes.c_uint32))
+    u8_pp = ctypes.POINTER(ctypes.POINTER(ctypes.c_ubyte))
+    size_p = ctypes.POINTER(c_size)
+    _proto(l, "lunelette_tokenizer_open", i, ctypes.c_char_p, ctypes.POINTER(c_void), err, c_size)
+    _proto(l, "lunelette_tokenizer_close", None, c_void)
+    _proto(l, "lunelette_tokenizer_encode", i, c_void, ctypes.c_char_p, c_size, u32_pp, size_p,
+           err, c_size)
+    _proto(l, "lunelette_tokenizer_encode_with_limit", i, c_void, ctypes.c_char_p, c_size, c_size,
+           u32_pp, size_p, err, c_size)
+    _proto(l, "lunelette_tokenizer_decode", i, c_void, ctypes.POINTER(ctypes.c_uint32), c_size,
+           u8_pp, size_p, err, c_size)
+    _proto(l, "lunelette_chat_prompt", i, c_void, ctypes.c_char_p, ctypes.c_char_p, i,
+           c_int64_p, size_p, err, c_size)
+    if hasattr(l, "lunelette_tokenizer_split"):
+        _proto(l, "lunelette_tokenizer_split", ctypes.c_long, ctypes.c_char_p, c_size, size_p,
+               c_size)
