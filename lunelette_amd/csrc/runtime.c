@@ -62,8 +62,8 @@ typedef struct lh_runtime {
     float *d_kv;              /* keys [layers][8][C][128] then values */
     float *d_keys, *d_values;
     float *d_x;               /* [B][3072] residual stream */
-    float *d_logits;          /* [131072] */
-    float *h_logits;          /* pinned; borrowed by callers */
+    float *h_logits;          /* [131072] pinned, coherent; borrowed by callers */
+    float *d_logits;          /* the same buffer as the head kernel addresses it */
     lh_workspace *ws;
     size_t length;
     bool valid, endpoint_logits_valid;
@@ -133,8 +133,7 @@ static void destroy_runtime(lh_runtime *rt)
     if (rt->stream) {
         (void)hipStreamSynchronize(rt->stream);
     }
-    void *device[] = {rt->d_weights, rt->d_embedding, rt->d_norms, rt->d_kv, rt->d_x,
-        rt->d_logits};
+    void *device[] = {rt->d_weights, rt->d_embedding, rt->d_norms, rt->d_kv, rt->d_x};
     for (size_t i = 0; i < sizeof device / sizeof device[0]; i++) {
         if (device[i]) {
             (void)hipFree(device[i]);
@@ -442,10 +441,12 @@ static lunelette_metal *build_runtime(weight_source *src, uint32_t layers,
         hip_ok(hipMalloc((void **)&rt->d_kv, kv_bytes), "KV allocation", error, capacity) ||
         hip_ok(hipMalloc((void **)&rt->d_x, B * LH_HIDDEN * sizeof(float)), "scratch allocation",
             error, capacity) ||
-        hip_ok(hipMalloc((void **)&rt->d_logits, LH_VOCAB * sizeof(float)), "logit allocation",
-            error, capacity) ||
+        /* The head kernel writes the logits straight into coherent pinned
+         * memory: no device-to-host copy after the step. */
         hip_ok(hipHostMalloc((void **)&rt->h_logits, LH_VOCAB * sizeof(float),
-            hipHostMallocDefault), "pinned logits", error, capacity)) {
+            hipHostMallocMapped | hipHostMallocCoherent), "pinned logits", error, capacity) ||
+        hip_ok(hipHostGetDevicePointer((void **)&rt->d_logits, rt->h_logits, 0),
+            "mapped logits", error, capacity)) {
         goto failure;
     }
     rt->d_keys = rt->d_kv;
@@ -523,8 +524,7 @@ static lunelette_metal *build_runtime(weight_source *src, uint32_t layers,
     rt->memory.strategy = rt->strategy;
     rt->memory.weight_bytes = weight_bytes + embedding_bytes + norm_bytes;
     rt->memory.conversion_stage_bytes = 0;
-    rt->memory.scratch_bytes = rt->ws->bytes + B * LH_HIDDEN * sizeof(float) +
-        LH_VOCAB * sizeof(float);
+    rt->memory.scratch_bytes = rt->ws->bytes + B * LH_HIDDEN * sizeof(float);
     rt->memory.kv_bytes = kv_bytes;
     rt->memory.total_bytes = rt->memory.weight_bytes + rt->memory.scratch_bytes + kv_bytes;
     uint64_t previous = atomic_load(&last_identity);
@@ -844,9 +844,7 @@ static int execute(lunelette_metal *context, const int64_t *ids, size_t count, b
     const int path = select_path(rt, count);
     int failed = hipEventRecord(rt->started, s) != hipSuccess ||
         (count == 1 && rt->graphs ? graph_step(rt, path, s) : launch_step(rt, count, path, s)) ||
-        hipEventRecord(rt->finished, s) != hipSuccess ||
-        hipMemcpyAsync(rt->h_logits, rt->d_logits, LH_VOCAB * sizeof(float),
-            hipMemcpyDeviceToHost, s) != hipSuccess;
+        hipEventRecord(rt->finished, s) != hipSuccess;
     hipError_t status = hipStreamSynchronize(s);
     if (failed || status != hipSuccess) {
         snprintf(error, capacity, "execution failed; reset required: %s",
