@@ -137,6 +137,11 @@ int lh_fp8_gemm(lh_workspace *ws, const uint8_t *d_w, float scale, const float *
 /* Final RMSNorm + tied BF16 head on one row (src/metal_encode.m:204-210). */
 int lh_head_forward(const uint16_t *d_embedding, const float *d_gamma, const float *d_xrow,
     float *d_logits, void *stream);
+/* Additive: the runtime's head step. The same logits, and *d_nonfinite = 1
+ * when any of them is Inf or NaN (the caller clears it first), which stands in
+ * for the host finite scan of src/metal_runtime.m:418-424 on finite steps. */
+int lh_head_forward_checked(const uint16_t *d_embedding, const float *d_gamma,
+    const float *d_xrow, float *d_logits, uint32_t *d_nonfinite, void *stream);
 /* Embedding gather of the workspace's ids into d_x [count][3072]. */
 int lh_embed_forward(const uint16_t *d_embedding, float *d_x, lh_workspace *ws, void *stream);
 

@@ -125,6 +125,7 @@ def lib():
     _proto(l, "lh_layer_forward", i, ctypes.POINTER(LayerWeights), c_void, c_void, c_void,
            c_void, i, c_void)
     _proto(l, "lh_head_forward", i, c_void, c_void, c_void, c_void, c_void)
+    _proto(l, "lh_head_forward_checked", i, c_void, c_void, c_void, c_void, c_void, c_void)
     _proto(l, "lh_fp8_gemm", i, c_void, c_void, f, c_void, c_void, c_size, c_size, c_size, c_void)
     _proto(l, "lh_layer_operator", i, i, ctypes.POINTER(LayerWeights), c_void, c_void, c_void,
            c_void, c_void)

@@ -294,8 +294,19 @@ int lh_head_forward(const uint16_t *d_embedding, const float *d_gamma, const flo
         lh_set_error("head_forward: missing argument");
         return -1;
     }
-    return launched(lh_launch_head(d_embedding, d_gamma, d_xrow, d_logits, (hipStream_t)stream),
-        "head");
+    return launched(lh_launch_head(d_embedding, d_gamma, d_xrow, d_logits, NULL,
+        (hipStream_t)stream), "head");
+}
+
+int lh_head_forward_checked(const uint16_t *d_embedding, const float *d_gamma,
+    const float *d_xrow, float *d_logits, uint32_t *d_nonfinite, void *stream)
+{
+    if (!d_embedding || !d_gamma || !d_xrow || !d_logits || !d_nonfinite) {
+        lh_set_error("head_forward_checked: missing argument");
+        return -1;
+    }
+    return launched(lh_launch_head(d_embedding, d_gamma, d_xrow, d_logits, d_nonfinite,
+        (hipStream_t)stream), "head");
 }
 
 int lh_embed_forward(const uint16_t *d_embedding, float *d_x, lh_workspace *ws, void *stream)

@@ -21,8 +21,9 @@ int lh_launch_qkv_rope(int lookup, const uint8_t *Wqkv, float sq, float sk, floa
     float *q, float *kcache_layer, float *vcache_layer, uint32_t capacity, hipStream_t s);
 int lh_launch_gateup_silu(int lookup, const uint8_t *Wgate, const uint8_t *Wup, float sg,
     float su, const float *gamma, const float *x, uint32_t count, float *gated, hipStream_t s);
+/* nonfinite (may be NULL) is set to 1 when any written logit is Inf or NaN. */
 int lh_launch_head(const uint16_t *E, const float *gamma, const float *xrow, float *logits,
-    hipStream_t s);
+    uint32_t *nonfinite, hipStream_t s);
 int lh_launch_rmsnorm(const float *gamma, const float *x, float *out, uint32_t width,
     uint32_t tokens, hipStream_t s);
 /* Query token t attends positions [0, params->length + t]; length (equal to

@@ -440,10 +440,12 @@ k_gateup_silu(const uint8_t* __restrict__ Wgate, const uint8_t* __restrict__ Wup
 }
 
 // Final RMSNorm -> tied BF16 head (src/metal_encode.m:204-210); the embedding
-// stays BF16 in HBM and widens exactly in registers. grid (VOCAB/16).
+// stays BF16 in HBM and widens exactly in registers. grid (VOCAB/16). With
+// nonfinite set, a workgroup that writes an Inf or NaN logit stores 1 there
+// (the caller clears it first), so the host need not scan every logit.
 __global__ void __launch_bounds__(256)
 k_head(const uint16_t* __restrict__ E, const float* __restrict__ gamma,
-    const float* __restrict__ xrow, float* __restrict__ logits)
+    const float* __restrict__ xrow, float* __restrict__ logits, uint32_t* __restrict__ nonfinite)
 {
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t row0 = (blockIdx.x * 4 + wave) * 4;
@@ -457,9 +459,14 @@ k_head(const uint16_t* __restrict__ E, const float* __restrict__ gamma,
     float dots[4];
     dot_rows<K_BF16, false, 3, 4>(wv, xin_s, nullptr, dots);
     if (lane == 0) {
+        uint32_t bad = 0;
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             logits[row0 + r] = dots[r];
+            bad |= (__float_as_uint(dots[r]) & 0x7f800000u) == 0x7f800000u;
+        }
+        if (bad && nonfinite) {
+            *nonfinite = 1u;
         }
     }
 }
@@ -615,9 +622,10 @@ extern "C" int lh_launch_gateup_silu(int lookup, const uint8_t* Wgate, const uin
 }
 
 extern "C" int lh_launch_head(const uint16_t* E, const float* gamma, const float* xrow,
-    float* logits, hipStream_t s)
+    float* logits, uint32_t* nonfinite, hipStream_t s)
 {
-    hipLaunchKernelGGL(k_head, dim3(LH_VOCAB / 16), dim3(256), 0, s, E, gamma, xrow, logits);
+    hipLaunchKernelGGL(k_head, dim3(LH_VOCAB / 16), dim3(256), 0, s, E, gamma, xrow, logits,
+        nonfinite);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 

@@ -64,6 +64,8 @@ typedef struct lh_runtime {
     float *d_x;               /* [B][3072] residual stream */
     float *h_logits;          /* [131072] pinned, coherent; borrowed by callers */
     float *d_logits;          /* the same buffer as the head kernel addresses it */
+    volatile uint32_t *h_nonfinite; /* pinned, coherent: set by the head kernel */
+    uint32_t *d_nonfinite;
     lh_workspace *ws;
     size_t length;
     bool valid, endpoint_logits_valid;
@@ -141,6 +143,9 @@ static void destroy_runtime(lh_runtime *rt)
     }
     if (rt->h_logits) {
         (void)hipHostFree(rt->h_logits);
+    }
+    if (rt->h_nonfinite) {
+        (void)hipHostFree((void *)rt->h_nonfinite);
     }
     for (size_t i = 0; i < sizeof rt->decode / sizeof rt->decode[0]; i++) {
         if (rt->decode[i].exec) {
@@ -446,7 +451,11 @@ static lunelette_metal *build_runtime(weight_source *src, uint32_t layers,
         hip_ok(hipHostMalloc((void **)&rt->h_logits, LH_VOCAB * sizeof(float),
             hipHostMallocMapped | hipHostMallocCoherent), "pinned logits", error, capacity) ||
         hip_ok(hipHostGetDevicePointer((void **)&rt->d_logits, rt->h_logits, 0),
-            "mapped logits", error, capacity)) {
+            "mapped logits", error, capacity) ||
+        hip_ok(hipHostMalloc((void **)&rt->h_nonfinite, 64,
+            hipHostMallocMapped | hipHostMallocCoherent), "pinned flag", error, capacity) ||
+        hip_ok(hipHostGetDevicePointer((void **)&rt->d_nonfinite, (void *)rt->h_nonfinite, 0),
+            "mapped flag", error, capacity)) {
         goto failure;
     }
     rt->d_keys = rt->d_kv;
@@ -711,8 +720,8 @@ static int launch_step(lh_runtime *rt, size_t count, int path, hipStream_t s)
             return -1;
         }
     }
-    return lh_head_forward(rt->d_embedding, rt->d_norms + 2ull * rt->layers * LH_HIDDEN,
-        rt->d_x + (count - 1) * LH_HIDDEN, rt->d_logits, s);
+    return lh_head_forward_checked(rt->d_embedding, rt->d_norms + 2ull * rt->layers * LH_HIDDEN,
+        rt->d_x + (count - 1) * LH_HIDDEN, rt->d_logits, rt->d_nonfinite, s);
 }
 
 static int graph_fail(hipError_t status, const char *what)
@@ -842,6 +851,9 @@ static int execute(lunelette_metal *context, const int64_t *ids, size_t count, b
         return -1;
     }
     const int path = select_path(rt, count);
+    /* The head kernel sets the flag on an Inf/NaN logit; the host then scans
+     * only to name the first one. */
+    *rt->h_nonfinite = 0;
     int failed = hipEventRecord(rt->started, s) != hipSuccess ||
         (count == 1 && rt->graphs ? graph_step(rt, path, s) : launch_step(rt, count, path, s)) ||
         hipEventRecord(rt->finished, s) != hipSuccess;
@@ -857,8 +869,9 @@ static int execute(lunelette_metal *context, const int64_t *ids, size_t count, b
     if (rt->inject == 2) {
         rt->inject = 0;
         rt->h_logits[LH_VOCAB - 1] = INFINITY;
+        *rt->h_nonfinite = 1;
     }
-    const size_t bad = lh_first_nonfinite(rt->h_logits, LH_VOCAB);
+    const size_t bad = *rt->h_nonfinite ? lh_first_nonfinite(rt->h_logits, LH_VOCAB) : LH_VOCAB;
     if (bad < LH_VOCAB) {
         snprintf(error, capacity, "nonfinite logit %zu; reset required", bad);
         return -1;

@@ -173,3 +173,32 @@ def test_rope_bitwise_oracle(gpu, oracle):
     lh.check(gpu.lh_rope(d["x"].ptr, d["c"].ptr, d["s"].ptr, d["f"].ptr, out.ptr, width,
                          len(positions), None))
     assert np.array_equal(bits(out.download(np.float32)), bits(expected))
+
+
+def test_head_nonfinite_flag(gpu):
+    """The runtime's head step flags Inf/NaN logits on the device (in place of
+    the host finite scan, src/metal_runtime.m:418-424): the logits equal the
+    plain head's bitwise, the flag stays clear on finite output and is set
+    when one row of the tied embedding makes its logit Inf or NaN."""
+    vocab, width = lh.VOCAB, lh.HIDDEN
+    gamma = lh.DeviceBuffer.from_array(np.ones(width, np.float32))
+    xrow = lh.DeviceBuffer.from_array(syn.normal_f32(7, 1, width))
+    table = np.zeros((vocab, width), np.uint16)
+    table[::977] = 0x3F80                                # 1.0 on some rows
+    cases = [("finite", None, 0), ("inf", 0x7F80, 1), ("nan", 0x7FC1, 1)]
+    for name, bad, want in cases:
+        if bad is not None:
+            table[4242, 17] = bad
+        emb = lh.DeviceBuffer.from_array(table)
+        plain = lh.DeviceBuffer(vocab * 4)
+        checked = lh.DeviceBuffer(vocab * 4)
+        flag = lh.DeviceBuffer.from_array(np.zeros(16, np.uint32))
+        lh.check(gpu.lh_head_forward(emb.ptr, gamma.ptr, xrow.ptr, plain.ptr, None), "head")
+        lh.check(gpu.lh_head_forward_checked(emb.ptr, gamma.ptr, xrow.ptr, checked.ptr, flag.ptr,
+                                             None), "head checked")
+        lh.check(gpu.lh_device_synchronize(), "sync")
+        a, b = plain.download(np.float32), checked.download(np.float32)
+        assert np.array_equal(a.view(np.uint32), b.view(np.uint32)), name
+        assert int(flag.download(np.uint32)[0]) == want, name
+        assert np.isfinite(b).all() == (want == 0), name
+        del emb
