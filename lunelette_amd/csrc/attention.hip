@@ -238,9 +238,48 @@ k_embed(const uint16_t* __restrict__ E, const lh_step_params* __restrict__ param
     }
 }
 
+// One decode token without a host upload of the step record: workgroup 0
+// writes params (the YaRN row of position length expands to the
+// [cos | cos], [sin | sin] halves the RoPE reads), and the three workgroups
+// widen the 3072 BF16 values of row id, four per thread. grid 3, block 256.
+__global__ void __launch_bounds__(256)
+k_step_embed(const uint16_t* __restrict__ E, const float* __restrict__ yarn, int32_t id,
+    uint32_t length, float qfactor, lh_step_params* __restrict__ params, float* __restrict__ x)
+{
+    const uint32_t tid = threadIdx.x, g = blockIdx.x * 256 + tid;
+    const uint2 raw = reinterpret_cast<const uint2*>(E + (size_t)id * LH_HIDDEN)[g];
+    reinterpret_cast<float4*>(x)[g] = make_float4(bf16_to_f32((uint16_t)raw.x),
+        bf16_to_f32((uint16_t)(raw.x >> 16)), bf16_to_f32((uint16_t)raw.y),
+        bf16_to_f32((uint16_t)(raw.y >> 16)));
+    if (blockIdx.x == 0) {
+        lh_token_params* tp = &params->tokens[0];
+        const float* row = yarn + (size_t)length * 128;
+        if (tid < 64) {
+            tp->cosine[tid] = tp->cosine[tid + 64] = row[tid];
+        } else if (tid < 128) {
+            tp->sine[tid - 64] = tp->sine[tid] = row[tid];
+        } else if (tid == 128) {
+            params->length = length;
+            params->count = 1;
+            tp->id = id;
+            tp->qfactor = qfactor;
+            tp->position = length;
+        }
+    }
+}
+
 }  // namespace lh
 
 using namespace lh;
+
+extern "C" int lh_launch_step_embed(const uint16_t* E, const float* yarn, int32_t id,
+    uint32_t length, float qfactor, lh_step_params* params, float* x, hipStream_t s)
+{
+    static_assert(LH_HIDDEN == 3 * 256 * 4, "three workgroups of four values per thread");
+    hipLaunchKernelGGL(k_step_embed, dim3(3), dim3(256), 0, s, E, yarn, id, length, qfactor,
+        params, x);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
 
 // The kernels read the step length from params (device memory, so a captured
 // graph replays with new lengths); `length` here must equal params->length and

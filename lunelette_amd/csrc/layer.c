@@ -72,7 +72,7 @@ void lh_workspace_destroy(lh_workspace *ws)
     }
     void *device[] = {ws->d_params, ws->d_q, ws->d_attn, ws->d_gated, ws->d_up, ws->d_xn,
         ws->d_qraw, ws->d_kraw, ws->d_vraw, ws->d_PM, ws->d_PT, ws->d_PA,
-        ws->d_split, ws->d_gemm};
+        ws->d_split, ws->d_gemm, ws->d_yarn};
     for (size_t i = 0; i < sizeof device / sizeof device[0]; i++) {
         if (device[i]) {
             (void)hipFree(device[i]);
@@ -122,6 +122,52 @@ int lh_workspace_set_tokens(lh_workspace *ws, const int64_t *ids, size_t length,
     }
     ws->length = length;
     ws->count = count;
+    return 0;
+}
+
+int lh_workspace_prepare_decode(lh_workspace *ws)
+{
+    if (!ws) {
+        lh_set_error("prepare_decode: require a workspace");
+        return -1;
+    }
+    if (ws->d_yarn) {
+        return 0;
+    }
+    const size_t floats = ws->capacity * 128;
+    float *table = malloc(floats * sizeof(float));
+    if (!table) {
+        lh_set_error("prepare_decode: host allocation failed");
+        return -1;
+    }
+    float cosine[128], sine[128];
+    for (size_t p = 0; p < ws->capacity; p++) {
+        lh_yarn((uint32_t)p, cosine, sine);
+        memcpy(table + p * 128, cosine, 64 * sizeof(float));
+        memcpy(table + p * 128 + 64, sine, 64 * sizeof(float));
+    }
+    const int failed = alloc_device((void **)&ws->d_yarn, floats * sizeof(float), &ws->bytes) ||
+        check(hipMemcpy(ws->d_yarn, table, floats * sizeof(float), hipMemcpyHostToDevice),
+            "prepare_decode upload");
+    free(table);
+    return failed ? -1 : 0;
+}
+
+int lh_workspace_set_decode(lh_workspace *ws, const uint16_t *d_embedding, int64_t id,
+    size_t length, float *d_x, hipStream_t s)
+{
+    if (!ws || !ws->d_yarn || !d_embedding || !d_x || id < 0 || id >= LH_VOCAB ||
+        length >= ws->capacity) {
+        lh_set_error("set_decode: require a prepared workspace, a valid id and length < capacity");
+        return -1;
+    }
+    ws->length = length;
+    ws->count = 1;
+    if (lh_launch_step_embed(d_embedding, ws->d_yarn, (int32_t)id, (uint32_t)length,
+            lh_query_factor((uint32_t)length), ws->d_params, d_x, s)) {
+        lh_set_error("step embed launch failed: %s", hipGetErrorString(hipGetLastError()));
+        return -1;
+    }
     return 0;
 }
 

@@ -42,6 +42,10 @@ uint32_t lh_attention_blocks(uint32_t length, uint32_t count);
 const void *lh_attention_blocks_kernel(void);
 int lh_launch_embed(const uint16_t *E, const lh_step_params *params, uint32_t count, float *x,
     hipStream_t s);
+/* One decode token: writes params (length, count 1, id, qfactor, cos/sin of
+ * position length from yarn [C][128]) and the widened embedding row of id. */
+int lh_launch_step_embed(const uint16_t *E, const float *yarn, int32_t id, uint32_t length,
+    float qfactor, lh_step_params *params, float *x, hipStream_t s);
 int lh_launch_element(int mode, const float *a, const float *b, float *out, size_t n,
     hipStream_t s);
 int lh_launch_silu_mul(const float *gate, const float *up, float *out, size_t n, hipStream_t s);

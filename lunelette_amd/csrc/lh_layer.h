@@ -21,6 +21,7 @@ struct lh_workspace {
     float *d_qraw, *d_kraw, *d_vraw;
     float *d_PM, *d_PT;            /* [B][32][C/64] block maxima and sums */
     float *d_PA;                   /* [B][32][C/64][128] block P.V partials */
+    float *d_yarn;                 /* [C][128]: cos[64], sin[64] per position (decode) */
     /* MFMA path: BF16 hi/mid/lo splits of the GEMM inputs, [3][B][K]. */
     uint16_t *d_split;
     float *d_gemm;                 /* [B][18432] GEMM outputs */
@@ -37,6 +38,14 @@ int lh_layer_forward_mfma(const lh_layer_weights *w, float *d_x, float *d_keys,
     float *d_values, lh_workspace *ws, int input_split, const float *next_norm, hipStream_t s);
 /* Allocates the MFMA path's extra workspace buffers (idempotent). */
 int lh_mfma_prepare(lh_workspace *ws);
+/* Builds the device YaRN table of every position below the capacity from the
+ * host YaRN (idempotent), for lh_workspace_set_decode. */
+int lh_workspace_prepare_decode(lh_workspace *ws);
+/* A single-token step without a host upload: one kernel writes the step
+ * record (position length, the table's cos/sin, the query factor) and the
+ * embedding row of id into d_x, on stream. */
+int lh_workspace_set_decode(lh_workspace *ws, const uint16_t *d_embedding, int64_t id,
+    size_t length, float *d_x, hipStream_t s);
 #ifdef __cplusplus
 }
 #endif

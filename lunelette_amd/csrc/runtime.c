@@ -435,7 +435,7 @@ static lunelette_metal *build_runtime(weight_source *src, uint32_t layers,
         goto failure;
     }
     rt->ws = lh_workspace_create(C, B);
-    if (!rt->ws || lh_mfma_prepare(rt->ws)) {
+    if (!rt->ws || lh_mfma_prepare(rt->ws) || lh_workspace_prepare_decode(rt->ws)) {
         snprintf(error, capacity, "workspace: %s", lh_last_error());
         goto failure;
     }
@@ -699,10 +699,12 @@ static int select_path(const lh_runtime *rt, size_t count)
 
 /* src/metal_runtime.m:349-432. */
 /* Device work of one step: embedding gather, every layer, final norm + head. */
-static int launch_step(lh_runtime *rt, size_t count, int path, hipStream_t s)
+/* embed: gather the step's embedding rows first (a device-side decode step
+ * has already written its row together with the step record). */
+static int launch_step(lh_runtime *rt, size_t count, int path, int embed, hipStream_t s)
 {
     const size_t per_layer = (size_t)LH_KV_HEADS * rt->limits.context * LH_HEAD_DIM;
-    if (lh_embed_forward(rt->d_embedding, rt->d_x, rt->ws, s)) {
+    if (embed && lh_embed_forward(rt->d_embedding, rt->d_x, rt->ws, s)) {
         return -1;
     }
     for (uint32_t l = 0; l < rt->layers; l++) {
@@ -736,7 +738,7 @@ static int capture_step(lh_runtime *rt, decode_graph *g, int path, uint32_t bloc
     if (status != hipSuccess) {
         return graph_fail(status, "capture");
     }
-    const int failed = launch_step(rt, 1, path, s);
+    const int failed = launch_step(rt, 1, path, 1, s);
     hipGraph_t graph = NULL;
     status = hipStreamEndCapture(s, &graph);
     if (failed || status != hipSuccess || !graph) {
@@ -846,7 +848,10 @@ static int execute(lunelette_metal *context, const int64_t *ids, size_t count, b
         return -1;
     }
     hipStream_t s = rt->stream;
-    if (lh_workspace_set_tokens(rt->ws, ids, rt->length, count, s)) {
+    /* A decode step writes its record on the device (no host upload), except
+     * under graph replay, whose captured gather reads the uploaded record. */
+    const int device_record = count == 1 && !rt->graphs;
+    if (!device_record && lh_workspace_set_tokens(rt->ws, ids, rt->length, count, s)) {
         snprintf(error, capacity, "step parameters failed; reset required: %s", lh_last_error());
         return -1;
     }
@@ -855,7 +860,10 @@ static int execute(lunelette_metal *context, const int64_t *ids, size_t count, b
      * only to name the first one. */
     *rt->h_nonfinite = 0;
     int failed = hipEventRecord(rt->started, s) != hipSuccess ||
-        (count == 1 && rt->graphs ? graph_step(rt, path, s) : launch_step(rt, count, path, s)) ||
+        (device_record &&
+            lh_workspace_set_decode(rt->ws, rt->d_embedding, ids[0], rt->length, rt->d_x, s)) ||
+        (count == 1 && rt->graphs ? graph_step(rt, path, s) :
+            launch_step(rt, count, path, !device_record, s)) ||
         hipEventRecord(rt->finished, s) != hipSuccess;
     hipError_t status = hipStreamSynchronize(s);
     if (failed || status != hipSuccess) {
