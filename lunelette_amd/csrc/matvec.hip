@@ -6,9 +6,11 @@
 // across all its chunks, and the 64 lane sums reduce by one fixed tree. The
 // per-tensor scale multiplies the row total once.
 //
-// One wave owns whole rows, so there is no LDS and no barrier: a workgroup is
-// four independent waves. The RMSNorm prologue (qkv, gate/up, head) is
-// recomputed per wave from the 12 KiB input row in L2.
+// One wave owns whole rows. The workgroup stages the input row once in LDS;
+// where a norm precedes the projection (q|k|v, gate/up, head) the workgroup
+// applies the canonical RMSNorm there before any dot. The q|k|v and gate/up
+// kernels split each output pair (RoPE halves, gate and up) over two waves
+// and join the two dots through LDS.
 #include "lh_device.h"
 #include "lh_internal.h"
 
@@ -196,6 +198,66 @@ __device__ __forceinline__ void stage_commit(const float4 (&xv)[NCH], const floa
     }
 }
 
+// Norm-prologue staging of a 3072-wide row for a T-thread workgroup. Thread
+// tid loads the 8-byte units h = tid + T*u of the row and of gamma (unit h is
+// columns 2h, 2h+1, half h&1 of 16-byte word h/2), so every thread count that
+// divides 1536 needs no guards. norm_commit stores the units in the LDS layout
+// above; wave 0 forms the canonical r from LDS; every thread then writes
+// gamma * (x * r) over its own units. Three barriers; the last one publishes the
+// normalized row (and anything else the workgroup stored before it).
+template <int T>
+__device__ __forceinline__ void norm_load(const float* row, const float* gamma,
+    float2 (&xv)[1536 / T], float2 (&gv)[1536 / T])
+{
+    static_assert(1536 % T == 0, "thread count must divide the row's 8-byte units");
+    const uint32_t tid = threadIdx.x;
+#pragma unroll
+    for (int u = 0; u < 1536 / T; u++) {
+        xv[u] = reinterpret_cast<const float2*>(row)[tid + T * u];
+        gv[u] = reinterpret_cast<const float2*>(gamma)[tid + T * u];
+    }
+}
+
+__device__ __forceinline__ float2* staged_unit(float4* xl, uint32_t h)
+{
+    const uint32_t w = h >> 1;
+    return reinterpret_cast<float2*>(xl + staged_word(w >> 8, w & 255)) + (h & 1);
+}
+
+template <int T>
+__device__ __forceinline__ void norm_commit(const float2 (&xv)[1536 / T],
+    const float2 (&gv)[1536 / T], float4* xl, float* r_s)
+{
+    const uint32_t tid = threadIdx.x, lane = tid & 63;
+#pragma unroll
+    for (int u = 0; u < 1536 / T; u++) {
+        *staged_unit(xl, tid + T * u) = xv[u];
+    }
+    __syncthreads();
+    if ((tid >> 6) == 0) {
+        float acc = 0.0f;
+#pragma unroll 2
+        for (int w = 0; w < 12; w++) {
+            const float4 v = xl[w * 64 + lane];
+            acc = __builtin_fmaf(v.x, v.x, acc);
+            acc = __builtin_fmaf(v.y, v.y, acc);
+            acc = __builtin_fmaf(v.z, v.z, acc);
+            acc = __builtin_fmaf(v.w, v.w, acc);
+        }
+        const float ss = wave_lane0(wave_tree64(acc));
+        if (lane == 0) {
+            *r_s = 1.0f / __builtin_sqrtf(ss / (float)LH_HIDDEN + 1e-5f);
+        }
+    }
+    __syncthreads();
+    const float r = *r_s;
+#pragma unroll
+    for (int u = 0; u < 1536 / T; u++) {
+        *staged_unit(xl, tid + T * u) = make_float2(gv[u].x * (xv[u].x * r), gv[u].y * (xv[u].y * r));
+    }
+    __syncthreads();
+}
+
 // Issue the lane's loads for R rows (row-major, NCH*1024 columns) before any
 // other memory traffic of the wave, so weight latency overlaps the input-row
 // loads and the RMSNorm prologue.
@@ -335,9 +397,13 @@ k_rows_generic(const void* __restrict__ W, float scale, const float* __restrict_
 // ---------------------------------------------------------------------------
 // RMSNorm -> q|k|v -> RoPE (+ query factor on Q) -> Q scratch and KV append
 // (src/metal_encode.m:129-153). The 48 heads (32 q, 8 k, 8 v) hold 64 RoPE
-// pairs each, rows head*128 + i and + 64; wave g (of 1024) owns the pairs
-// P = 3g, 3g+1, 3g+2 (head P/64, i = P%64), so every SIMD gets six rows.
-// grid (1024/4, count), block 256.
+// pairs each, rows head*128 + i and + 64. A workgroup owns the six pairs
+// P = 6b .. 6b+5 (head P/64, i = P%64): waves 0 and 1 dot the three lower rows
+// (i) of pairs 6b+3k .. +2, waves 2 and 3 the matching upper rows (i + 64), and
+// the scaled dots meet in LDS, where threads 0..5 rotate one pair each.
+// The row loads of all four waves are issued before any weight load (the
+// first barrier), so the RMSNorm prologue is not queued behind weight misses.
+// grid (512, count), block 256.
 template <bool LUT>
 __global__ void __launch_bounds__(256)
 k_qkv_rope(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restrict__ gamma,
@@ -345,97 +411,116 @@ k_qkv_rope(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restr
     float* __restrict__ qout, float* __restrict__ kcache, float* __restrict__ vcache,
     uint32_t capacity)
 {
+    constexpr int T = 256;
     __shared__ float lut_s[LUT ? 256 : 1];
+    __shared__ float4 xin_s[3 * 4 * 64];
+    __shared__ float prod[2][6];
+    __shared__ float r_s;
     if constexpr (LUT) {
-        fill_lut(lut_s);
-        __syncthreads();
+        fill_lut(lut_s);  // published by the barriers below, before any dot
     }
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
     const uint32_t t = blockIdx.y;
-    const uint32_t g = blockIdx.x * 4 + wave;
-    uint32_t heads[3], is[3], rr[6];
+    const bool upper = wave >= 2;
+    const uint32_t k0 = 3 * (wave & 1);
+    const uint32_t base = blockIdx.x * 6;
+    float2 xv[1536 / T], gv[1536 / T];
+    norm_load<T>(xin + (size_t)t * LH_HIDDEN, gamma, xv, gv);
+    __syncthreads();
+    uint32_t rr[3];
 #pragma unroll
     for (int j = 0; j < 3; j++) {
-        const uint32_t pair = 3 * g + j;
-        heads[j] = pair >> 6;
-        is[j] = pair & 63;
-        rr[j] = heads[j] * 128 + is[j];
-        rr[3 + j] = rr[j] + 64;
+        const uint32_t pair = base + k0 + j;
+        rr[j] = (pair >> 6) * 128 + (pair & 63) + (upper ? 64 : 0);
     }
-    __shared__ float4 xin_s[3 * 4 * 64], gam_s[3 * 4 * 64];
-    float4 xv[3], gv[3];
-    stage_load<3, true>(xin + (size_t)t * LH_HIDDEN, gamma, xv, gv);
-    WVec<K_FP8> wv[6][3];
-    issue_rows<K_FP8, 3, 6>(Wqkv, rr, wv);
-    stage_commit<3, true>(xv, gv, xin_s, gam_s);
-    float dots[6];
-    dot_rows<K_FP8, LUT, 3, 6>(wv, xin_s, lut_s, dots);
-    const lh_token_params* tp = &params->tokens[t];
-    const uint32_t position = params->length + t;
+    WVec<K_FP8> wv[3][3];
+    issue_rows<K_FP8, 3, 3>(Wqkv, rr, wv);
+    norm_commit<T>(xv, gv, xin_s, &r_s);
+    float dots[3];
+    dot_rows<K_FP8, LUT, 3, 3>(wv, xin_s, lut_s, dots);
     if (lane == 0) {
 #pragma unroll
         for (int j = 0; j < 3; j++) {
-            const uint32_t head = heads[j], i = is[j];
+            const uint32_t head = (base + k0 + j) >> 6;
             const float scale = head < 32 ? scales.x : (head < 40 ? scales.y : scales.z);
-            const float lo = dots[j] * scale;
-            const float hi = dots[3 + j] * scale;
-            if (head < 40) {
-                // column i < 64 rotates with -x[i+64]; column i+64 with x[i].
-                float out_lo = lo * tp->cosine[i] + (-hi) * tp->sine[i];
-                float out_hi = hi * tp->cosine[i + 64] + lo * tp->sine[i + 64];
-                if (head < 32) {
-                    out_lo = out_lo * tp->qfactor;
-                    out_hi = out_hi * tp->qfactor;
-                    float* qh = qout + (size_t)t * LH_QUERY + head * 128;
-                    qh[i] = out_lo;
-                    qh[i + 64] = out_hi;
-                } else {
-                    float* kr = kcache + lh_kv_index(capacity, 0, head - 32, position);
-                    kr[i] = out_lo;
-                    kr[i + 64] = out_hi;
-                }
+            prod[upper][k0 + j] = dots[j] * scale;
+        }
+    }
+    __syncthreads();
+    if (tid < 6) {
+        const lh_token_params* tp = &params->tokens[t];
+        const uint32_t position = params->length + t;
+        const uint32_t pair = base + tid, head = pair >> 6, i = pair & 63;
+        const float lo = prod[0][tid];
+        const float hi = prod[1][tid];
+        if (head < 40) {
+            // column i < 64 rotates with -x[i+64]; column i+64 with x[i].
+            float out_lo = lo * tp->cosine[i] + (-hi) * tp->sine[i];
+            float out_hi = hi * tp->cosine[i + 64] + lo * tp->sine[i + 64];
+            if (head < 32) {
+                out_lo = out_lo * tp->qfactor;
+                out_hi = out_hi * tp->qfactor;
+                float* qh = qout + (size_t)t * LH_QUERY + head * 128;
+                qh[i] = out_lo;
+                qh[i + 64] = out_hi;
             } else {
-                float* vr = vcache + lh_kv_index(capacity, 0, head - 40, position);
-                vr[i] = lo;
-                vr[i + 64] = hi;
+                float* kr = kcache + lh_kv_index(capacity, 0, head - 32, position);
+                kr[i] = out_lo;
+                kr[i + 64] = out_hi;
             }
+        } else {
+            float* vr = vcache + lh_kv_index(capacity, 0, head - 40, position);
+            vr[i] = lo;
+            vr[i + 64] = hi;
         }
     }
 }
 
 // RMSNorm -> gate and up rows -> SiLU(gate)*up (src/metal_encode.m:162-171).
-// Wave g owns inner rows 3g .. 3g+2 (gate and up). grid (9216/12, count).
+// A workgroup of eight waves owns inner rows 12b .. 12b+11: waves 0..3 dot
+// three gate rows each, waves 4..7 the matching up rows, and the scaled dots
+// meet in LDS, where threads 0..11 form SiLU(gate)*up. The row loads of all
+// eight waves are issued before any weight load (the first barrier).
+// grid (9216/12, count), block 512.
 template <bool LUT>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(512)
 k_gateup_silu(const uint8_t* __restrict__ Wgate, const uint8_t* __restrict__ Wup, float2 scales,
     const float* __restrict__ gamma, const float* __restrict__ xin, float* __restrict__ gated)
 {
+    constexpr int T = 512;
     __shared__ float lut_s[LUT ? 256 : 1];
+    __shared__ float4 xin_s[3 * 4 * 64];
+    __shared__ float prod[2][12];
+    __shared__ float r_s;
     if constexpr (LUT) {
-        fill_lut(lut_s);
-        __syncthreads();
+        fill_lut(lut_s);  // published by the barriers below, before any dot
     }
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const uint32_t tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
     const uint32_t t = blockIdx.y;
-    const uint32_t row0 = (blockIdx.x * 4 + wave) * 3;
-    const uint32_t rr[3] = {row0, row0 + 1, row0 + 2};
-    __shared__ float4 xin_s[3 * 4 * 64], gam_s[3 * 4 * 64];
-    float4 xv[3], gv[3];
-    stage_load<3, true>(xin + (size_t)t * LH_HIDDEN, gamma, xv, gv);
-    WVec<K_FP8> wg[3][3], wu[3][3];
-    issue_rows<K_FP8, 3, 3>(Wgate, rr, wg);
-    issue_rows<K_FP8, 3, 3>(Wup, rr, wu);
-    stage_commit<3, true>(xv, gv, xin_s, gam_s);
-    float g[3], u[3];
-    dot_rows<K_FP8, LUT, 3, 3>(wg, xin_s, lut_s, g);
-    dot_rows<K_FP8, LUT, 3, 3>(wu, xin_s, lut_s, u);
+    const bool up = wave >= 4;
+    const uint32_t k0 = 3 * (wave & 3);
+    const uint32_t base = blockIdx.x * 12;
+    float2 xv[1536 / T], gv[1536 / T];
+    norm_load<T>(xin + (size_t)t * LH_HIDDEN, gamma, xv, gv);
+    __syncthreads();
+    const uint32_t rr[3] = {base + k0, base + k0 + 1, base + k0 + 2};
+    WVec<K_FP8> wv[3][3];
+    issue_rows<K_FP8, 3, 3>(up ? Wup : Wgate, rr, wv);
+    norm_commit<T>(xv, gv, xin_s, &r_s);
+    float dots[3];
+    dot_rows<K_FP8, LUT, 3, 3>(wv, xin_s, lut_s, dots);
     if (lane == 0) {
+        const float scale = up ? scales.y : scales.x;
 #pragma unroll
         for (int r = 0; r < 3; r++) {
-            const float gv = g[r] * scales.x;
-            const float uv = u[r] * scales.y;
-            gated[(size_t)t * LH_INNER + row0 + r] = silu(gv) * uv;
+            prod[up][k0 + r] = dots[r] * scale;
         }
+    }
+    __syncthreads();
+    if (tid < 12) {
+        gated[(size_t)t * LH_INNER + base + tid] = silu(prod[0][tid]) * prod[1][tid];
     }
 }
 
@@ -595,7 +680,7 @@ extern "C" int lh_launch_qkv_rope(int lookup, const uint8_t* Wqkv, float sq, flo
     const float* gamma, const float* x, const lh_step_params* params, uint32_t count,
     float* q, float* kcache_layer, float* vcache_layer, uint32_t capacity, hipStream_t s)
 {
-    dim3 grid(48 * 64 / 3 / 4, count);
+    dim3 grid(48 * 64 / 6, count);
     float3 scales = make_float3(sq, sk, sv);
     if (lookup) {
         hipLaunchKernelGGL(k_qkv_rope<true>, grid, dim3(256), 0, s, Wqkv, scales, gamma, x, params,
@@ -614,9 +699,9 @@ extern "C" int lh_launch_gateup_silu(int lookup, const uint8_t* Wgate, const uin
     dim3 grid(LH_INNER / 12, count);
     float2 scales = make_float2(sg, su);
     if (lookup) {
-        hipLaunchKernelGGL(k_gateup_silu<true>, grid, dim3(256), 0, s, Wgate, Wup, scales, gamma, x, gated);
+        hipLaunchKernelGGL(k_gateup_silu<true>, grid, dim3(512), 0, s, Wgate, Wup, scales, gamma, x, gated);
     } else {
-        hipLaunchKernelGGL(k_gateup_silu<false>, grid, dim3(256), 0, s, Wgate, Wup, scales, gamma, x, gated);
+        hipLaunchKernelGGL(k_gateup_silu<false>, grid, dim3(512), 0, s, Wgate, Wup, scales, gamma, x, gated);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
