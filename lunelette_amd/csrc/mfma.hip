@@ -3,26 +3,35 @@
 // src/metal_encode.m:94-110, src/metal_mps.m:26-111).
 //
 // P[s][m][n] = sum over the split's columns k of X[m][k] * dec(W[n][k]), FP32.
-// - X (FP32 activations) is pre-split by k_split into hi + mid + lo BF16 planes
-//   so that X == hi + mid + lo exactly; W stays FP8 in HBM and is decoded to
-//   BF16 exactly (v_cvt_scalef32_pk_bf16_fp8, unit scale: every E4M3FN value
-//   has at most 4 significant bits). Every MFMA product is exact; the three
-//   plane products accumulate in FP32.
-// - k_gemm: a 256-thread workgroup owns 64 tokens x 256 weight rows of one K
+// - X (FP32 activations) reaches the GEMM as planes of 16-bit values, in one
+//   of two formats. Three BF16 planes: X == hi + mid + lo exactly (k_split,
+//   and the attention output for the o projection). Two FP16 planes of the
+//   row scaled by a power of two: X * 2^e == h + l to about 22 significant
+//   bits, with 2^e bringing the row's largest magnitude into [2^14, 2^15) so
+//   that nothing overflows (the gate|up and down inputs, whose producers see
+//   whole token rows); the consumer multiplies the summed
+//   partials by 2^-e, exactly. W stays FP8 in HBM and is decoded exactly to
+//   BF16 or FP16 (v_cvt_scalef32_pk_{bf16,f16}_fp8, unit scale: every E4M3FN
+//   value has at most 4 significant bits and fits either type). The plane
+//   products accumulate in FP32.
+// - k_gemm_bf16 / k_gemm_f16: a 256-thread workgroup owns 64 tokens x 256 weight rows of one K
 //   split; each wave owns 64 weight rows and all 64 tokens (4 x 4 MFMA
-//   tiles). Per 64-column stage the activation tile (64 tokens x 3 planes,
-//   24 KB) goes to LDS by direct loads (global_load_lds_dwordx4) in
-//   fragment-major order, so each v_mfma_f32_16x16x32_bf16 A operand is one
-//   conflict-free 16-byte LDS read, shared by the four waves; each wave
+//   tiles). Per 64-column stage the activation tile (64 tokens x P planes,
+//   8P KB) goes to LDS by direct loads (global_load_lds_dwordx4) in
+//   fragment-major order, so each v_mfma_f32_16x16x32_{bf16,f16} A operand is
+//   one conflict-free 16-byte LDS read, shared by the four waves; each wave
 //   streams its weight rows straight into registers (16 FP8 codes per lane
 //   and row fragment) and converts them there. The next stage's loads are
 //   in flight (two LDS buffers, two weight register sets) while the current
-//   stage's 96 MFMAs per wave run. Lane group g = lane/16 supplies columns
+//   stage's 32P MFMAs per wave run. Lane group g = lane/16 supplies columns
 //   16g .. 16g+15 of the stage to both operands (a K permutation shared by
 //   A and B, so the sum is unchanged) as two 8-column k-slices. Two
-//   workgroups share a CU (48 KB LDS and <= 256 registers each). Measured
-//   alternatives: weights through LDS as well (slower on gate|up, equal
-//   elsewhere); a third stage in flight (spills at two workgroups per CU).
+//   workgroups share a CU (<= 48 KB LDS and <= 256 registers each). Two FP16
+//   planes do two thirds of the MFMA work of three BF16 planes (gate|up at
+//   256 tokens: 85 against 104 us, the same error against an FP64 product).
+//   Measured alternatives: weights through LDS as well (slower on gate|up,
+//   equal elsewhere); a third stage in flight (spills at two workgroups per
+//   CU); two BF16 planes (16 significant bits, outside the tolerance).
 // - Workgroup ids deal the (weight tile, split) columns round-robin to the 8
 //   XCDs and run a column's token tiles back to back on one XCD, so the
 //   weight tile is read from HBM once per XCD and from L2 after that.
@@ -42,16 +51,77 @@
 namespace lh {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
-constexpr int NSPLIT = 3;                 // BF16 planes per activation
 constexpr uint32_t GM = 64;               // tokens per workgroup tile
 constexpr uint32_t GN = 256;              // weight rows per workgroup tile (4 waves x 64)
 constexpr uint32_t BK = 64;               // columns per pipeline stage
-constexpr uint32_t A_FRAGS = 4 * 3 * 2;   // 1 KB activation fragments per stage
 constexpr uint32_t SPLIT_ROWS = 128;      // token stride granule of the split planes
 constexpr uint32_t MAX_N = 2 * LH_INNER;  // widest GEMM: gate|up
+
+// Activation plane formats of k_gemm: three exact BF16 planes (hi + mid + lo),
+// or two FP16 planes of a row scaled by 2^e (h + l, about 22 significant bits).
+enum { PLANES_BF16 = 3, PLANES_F16 = 2 };
+
+// 2^e as a float, e in [-126, 127].
+__device__ __forceinline__ float exp2i(int e)
+{
+    return __uint_as_float((uint32_t)(e + 127) << 23);
+}
+
+// Scale exponent of a row whose largest magnitude is m: m * 2^e lies in
+// [2^14, 2^15), inside FP16's normal range, so neither plane overflows. 0 for
+// m = 0 or nonfinite m; clamped to [-126, 126] (subnormal m gives 126).
+__device__ __forceinline__ int row_exponent(float m)
+{
+    const uint32_t field = (__float_as_uint(m) >> 23) & 0xffu;
+    if (!(m > 0.0f) || field == 0xffu) {
+        return 0;
+    }
+    if (field == 0) {
+        return 126;
+    }
+    const int e = 141 - (int)field;   // m = f * 2^(field - 126), f in [0.5, 1)
+    return e < -126 ? -126 : (e > 126 ? 126 : e);
+}
+
+// Two-plane FP16 form of an (already scaled) value: h = f16(v), l = f16(v - h);
+// v - h is exact in FP32, so h + l carries about 22 significant bits.
+__device__ __forceinline__ uint32_t f16_hi(float v, float& rest)
+{
+    const _Float16 h = (_Float16)v;
+    rest = v - (float)h;
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ uint32_t f16_bits(float v)
+{
+    return __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+// Four consecutive scaled values into the two FP16 planes of xs (plane stride
+// `plane` elements), one 8-byte store per plane; `at` is a multiple of 4.
+__device__ __forceinline__ void store_f16x2_4(uint16_t* xs, size_t plane, size_t at, float4 v)
+{
+    float ra, rb, rc, rd;
+    const uint32_t a = f16_hi(v.x, ra), b = f16_hi(v.y, rb), c = f16_hi(v.z, rc),
+                   d = f16_hi(v.w, rd);
+    *reinterpret_cast<uint2*>(xs + at) = make_uint2(a | (b << 16), c | (d << 16));
+    *reinterpret_cast<uint2*>(xs + plane + at) = make_uint2(
+        f16_bits(ra) | (f16_bits(rb) << 16), f16_bits(rc) | (f16_bits(rd) << 16));
+}
+
+__device__ __forceinline__ float4 scale4(float4 v, float s)
+{
+    return make_float4(v.x * s, v.y * s, v.z * s, v.w * s);
+}
+
+__device__ __forceinline__ float absmax4(float4 v)
+{
+    return fmaxf(fmaxf(fabsf(v.x), fabsf(v.y)), fmaxf(fabsf(v.z), fabsf(v.w)));
+}
 
 // Sum of S split-K partials in split order ((p0 + p1) + p2) + ..., all loads
 // issued before the first add. p points at split 0; stride4 is the split
@@ -71,6 +141,29 @@ __device__ __forceinline__ float4 sum_splits(const float4* __restrict__ p, size_
         acc.y = acc.y + v[s].y;
         acc.z = acc.z + v[s].z;
         acc.w = acc.w + v[s].w;
+    }
+    return acc;
+}
+
+// sum_splits with split s's partial first multiplied by sc[s] (powers of two,
+// so each product is exact and the sum is the unscaled one).
+template <int S>
+__device__ __forceinline__ float4 sum_splits_scaled(const float4* __restrict__ p, size_t stride4,
+    const float* __restrict__ sc)
+{
+    float4 v[S];
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        v[s] = p[s * stride4];
+    }
+    float4 acc = scale4(v[0], sc[0]);
+#pragma unroll
+    for (int s = 1; s < S; s++) {
+        const float4 w = scale4(v[s], sc[s]);
+        acc.x = acc.x + w.x;
+        acc.y = acc.y + w.y;
+        acc.z = acc.z + w.z;
+        acc.w = acc.w + w.w;
     }
     return acc;
 }
@@ -98,27 +191,32 @@ k_split(const float* __restrict__ x, uint16_t* __restrict__ xs, uint32_t width,
 // projections, src/metal_encode.m:160,175), written back; then the canonical
 // RMSNorm of the (updated) row, y = gamma * (x * r) with ss by the row-dot
 // schedule (w = x) and r = 1/sqrt(ss/n + 1e-5), the same normalized values the
-// decode kernels compute, split into the hi/mid/lo planes of xs for the next
-// GEMM. S = 0 only normalizes (the first layer's input norm). grid (count),
-// block 768: thread i owns columns 4i .. 4i+3.
-template <int S>
+// decode kernels compute, written as the next GEMM's input planes: with F16,
+// scaled by the row's power of two 2^e and split into two FP16 planes, with
+// out_scale[t] = 2^-e to undo it on the GEMM's output; otherwise the three
+// exact BF16 planes (out_scale unused). The partials carry their own
+// scales per split, in_scale[t][s] (nullable; the down projection's). S = 0
+// only normalizes (the first layer's input norm). grid (count), block 768:
+// thread i owns columns 4i .. 4i+3.
+template <int S, bool F16>
 __global__ void __launch_bounds__(768)
 k_residual_norm_split(const float* __restrict__ partial, size_t split_stride, float scale,
-    float* __restrict__ x, const float* __restrict__ gamma, uint16_t* __restrict__ xs,
-    uint32_t stride_tokens)
+    const float* __restrict__ in_scale, float* __restrict__ x, const float* __restrict__ gamma,
+    uint16_t* __restrict__ xs, float* __restrict__ out_scale, uint32_t stride_tokens)
 {
     // Row in the [chunk][quad][lane] 16-byte-word layout: lane l's 16 values
     // of chunk c (columns c*1024 + 16l .. +15) are words (4c + q)*64 + l.
     __shared__ float4 row_l[LH_HIDDEN / 4];
     __shared__ float r_s;
+    __shared__ float wmax[LH_HIDDEN / 4 / 64];
     const uint32_t t = blockIdx.x, tid = threadIdx.x;
     float4* xr = reinterpret_cast<float4*>(x + (size_t)t * LH_HIDDEN);
     const float4 g = reinterpret_cast<const float4*>(gamma)[tid];
     float4 v = xr[tid];
     if constexpr (S > 0) {
-        const float4 acc = sum_splits<S>(
-            reinterpret_cast<const float4*>(partial + (size_t)t * LH_HIDDEN) + tid,
-            split_stride / 4);
+        const float4* pt = reinterpret_cast<const float4*>(partial + (size_t)t * LH_HIDDEN) + tid;
+        const float4 acc = in_scale ? sum_splits_scaled<S>(pt, split_stride / 4, in_scale + t * S)
+                                    : sum_splits<S>(pt, split_stride / 4);
         v.x = v.x + acc.x * scale;
         v.y = v.y + acc.y * scale;
         v.z = v.z + acc.z * scale;
@@ -145,36 +243,71 @@ k_residual_norm_split(const float* __restrict__ partial, size_t split_stride, fl
     }
     __syncthreads();
     const float r = r_s;
-    store_split4(xs, (size_t)stride_tokens * LH_HIDDEN, (size_t)t * LH_HIDDEN + 4 * tid,
-        make_float4(g.x * (v.x * r), g.y * (v.y * r), g.z * (v.z * r), g.w * (v.w * r)));
+    const float4 y = make_float4(g.x * (v.x * r), g.y * (v.y * r), g.z * (v.z * r), g.w * (v.w * r));
+    if constexpr (!F16) {
+        store_split4(xs, (size_t)stride_tokens * LH_HIDDEN, (size_t)t * LH_HIDDEN + 4 * tid, y);
+        return;
+    }
+    const float m = wave_max64(absmax4(y));
+    if ((tid & 63) == 0) {
+        wmax[tid >> 6] = m;
+    }
+    __syncthreads();
+    float mr = wmax[0];
+#pragma unroll
+    for (int i = 1; i < LH_HIDDEN / 4 / 64; i++) {
+        mr = fmaxf(mr, wmax[i]);
+    }
+    const int e = row_exponent(mr);
+    if (tid == 0) {
+        out_scale[t] = exp2i(-e);
+    }
+    store_f16x2_4(xs, (size_t)stride_tokens * LH_HIDDEN, (size_t)t * LH_HIDDEN + 4 * tid,
+        scale4(y, exp2i(e)));
 }
 
 // Down-projection input: SiLU(s_g * gate) * (s_u * up) (src/metal_encode.m:
 // 162-171) from the gate|up GEMM partials P[s][m][0..18432) (gate rows first),
-// summed in split order, split into BF16 planes. grid (count, 5), block 256:
-// thread j < 1152 of the row takes inner columns 8j .. 8j+7.
+// summed in split order and multiplied by their row scale in_scale[t] (a power
+// of two, exact). Each of the down projection's DOWN_SPLITS K ranges (576
+// columns) gets its own power of two 2^e (its largest magnitude into
+// [2^14, 2^15)) before the split into two FP16 planes; out_scale[t][g] = 2^-e,
+// which the down projection's consumers apply to that split's partial. grid
+// (count, DOWN_SPLITS), block 192: thread j < 144 owns columns 576g + 4j .. +3.
+constexpr uint32_t DOWN_SPLITS = 16;
+constexpr uint32_t GROUP4 = LH_INNER / DOWN_SPLITS / 4;   // float4 columns per group: 144
+
 template <int S>
-__global__ void __launch_bounds__(256)
+__global__ void __launch_bounds__(192)
 k_split_silu(const float* __restrict__ partial, size_t split_stride, float2 scales,
-    uint16_t* __restrict__ xs, uint32_t stride_tokens)
+    const float* __restrict__ in_scale, uint16_t* __restrict__ xs,
+    float* __restrict__ out_scale, uint32_t stride_tokens)
 {
-    const uint32_t t = blockIdx.x, j = blockIdx.y * 256 + threadIdx.x;
-    if (8 * j >= LH_INNER) {
-        return;
-    }
-    const float4* row = reinterpret_cast<const float4*>(partial + (size_t)t * MAX_N) + 2 * j;
+    __shared__ float wmax[3];
+    const uint32_t t = blockIdx.x, grp = blockIdx.y, j = threadIdx.x;
+    const bool active = j < GROUP4;
+    // Idle lanes load (and discard) the group's last column: no branch around loads.
+    const uint32_t c4 = grp * GROUP4 + (active ? j : GROUP4 - 1);
+    const float4* row = reinterpret_cast<const float4*>(partial + (size_t)t * MAX_N) + c4;
     const size_t s4 = split_stride / 4;
-    const float4 g0 = sum_splits<S>(row, s4), g1 = sum_splits<S>(row + 1, s4);
-    const float4 u0 = sum_splits<S>(row + LH_INNER / 4, s4);
-    const float4 u1 = sum_splits<S>(row + LH_INNER / 4 + 1, s4);
-    const float sg = scales.x, su = scales.y;
-    const size_t plane = (size_t)stride_tokens * LH_INNER, at = (size_t)t * LH_INNER + 8 * j;
-    store_split4(xs, plane, at,
-        make_float4(silu(g0.x * sg) * (u0.x * su), silu(g0.y * sg) * (u0.y * su),
-            silu(g0.z * sg) * (u0.z * su), silu(g0.w * sg) * (u0.w * su)));
-    store_split4(xs, plane, at + 4,
-        make_float4(silu(g1.x * sg) * (u1.x * su), silu(g1.y * sg) * (u1.y * su),
-            silu(g1.z * sg) * (u1.z * su), silu(g1.w * sg) * (u1.w * su)));
+    const float ts = in_scale[t], sg = scales.x, su = scales.y;
+    const float4 g = scale4(sum_splits<S>(row, s4), ts);
+    const float4 u = scale4(sum_splits<S>(row + LH_INNER / 4, s4), ts);
+    const float4 y = make_float4(silu(g.x * sg) * (u.x * su), silu(g.y * sg) * (u.y * su),
+        silu(g.z * sg) * (u.z * su), silu(g.w * sg) * (u.w * su));
+    const float m = wave_max64(active ? absmax4(y) : 0.0f);
+    if ((j & 63) == 0) {
+        wmax[j >> 6] = m;
+    }
+    __syncthreads();
+    const int e = row_exponent(fmaxf(wmax[0], fmaxf(wmax[1], wmax[2])));
+    if (j == 0) {
+        out_scale[t * DOWN_SPLITS + grp] = exp2i(-e);
+    }
+    if (active) {
+        store_f16x2_4(xs, (size_t)stride_tokens * LH_INNER, (size_t)t * LH_INNER + 4 * c4,
+            scale4(y, exp2i(e)));
+    }
 }
 
 // q|k|v epilogue (src/metal_encode.m:129-153): partials P[s][m][0..6144)
@@ -230,8 +363,9 @@ k_qkv_epilogue(const float* __restrict__ partial, size_t split_stride, float3 sc
     }
 }
 
-// FP8 -> BF16 weight fragments: the 16 codes of u (row bytes 16g .. 16g+15
-// of the step) give the two 8-column k-slices h = 0 (bytes 0..7) and h = 1.
+// FP8 -> BF16 (or FP16) weight fragments, exact either way: the 16 codes of
+// u (row bytes 16g .. 16g+15 of the step) give the two 8-column k-slices
+// h = 0 (bytes 0..7) and h = 1.
 __device__ __forceinline__ void fp8x16_to_bf16x8x2(u32x4 u, bf16x8& lo, bf16x8& hi)
 {
     u32x4 a, b;
@@ -247,17 +381,38 @@ __device__ __forceinline__ void fp8x16_to_bf16x8x2(u32x4 u, bf16x8& lo, bf16x8& 
     hi = __builtin_bit_cast(bf16x8, b);
 }
 
-// grid: n_tiles * m_tiles * splits workgroups of 256 threads, two resident per
-// CU; (n_tiles * splits) a multiple of 8. W0 holds rows [0, boundary), W1
+__device__ __forceinline__ void fp8x16_to_f16x8x2(u32x4 u, f16x8& lo, f16x8& hi)
+{
+    u32x4 a, b;
+    a.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(u.x, 1.0f, false));
+    a.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(u.x, 1.0f, true));
+    a.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(u.y, 1.0f, false));
+    a.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(u.y, 1.0f, true));
+    b.x = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(u.z, 1.0f, false));
+    b.y = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(u.z, 1.0f, true));
+    b.z = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(u.w, 1.0f, false));
+    b.w = __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(u.w, 1.0f, true));
+    lo = __builtin_bit_cast(f16x8, a);
+    hi = __builtin_bit_cast(f16x8, b);
+}
+
+// P activation planes (PLANES_BF16 or PLANES_F16) of the same layout
+// xs[p][m][k]. grid: n_tiles * m_tiles * splits workgroups of 256 threads, two
+// resident per CU; (n_tiles * splits) a multiple of 8. W0 holds rows [0, boundary), W1
 // rows [boundary, N) (gate|up as two tensors); boundary a multiple of 256.
 // out: P[s][m][n] with split stride stride_tokens * N; token rows >= count
 // are not written (their activation rows, < m_tiles * 64 <= stride_tokens,
 // are read).
-__global__ void __launch_bounds__(256, 2)
-k_gemm(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint32_t boundary,
-    uint32_t N, uint32_t K, const uint16_t* __restrict__ xs, uint32_t stride_tokens,
-    uint32_t count, uint32_t m_tiles, uint32_t splits, float* __restrict__ out)
+template <int P>
+__device__ __forceinline__ void gemm_tile(const uint8_t* __restrict__ W0,
+    const uint8_t* __restrict__ W1, uint32_t boundary, uint32_t N, uint32_t K,
+    const uint16_t* __restrict__ xs, uint32_t stride_tokens, uint32_t count, uint32_t m_tiles,
+    uint32_t splits, float* __restrict__ out)
 {
+    static_assert(P == PLANES_BF16 || P == PLANES_F16, "plane format");
+    using V = typename std::conditional<P == PLANES_BF16, bf16x8, f16x8>::type;
+    constexpr uint32_t A_FRAGS = 4 * P * 2;   // 1 KB activation fragments per stage
+    constexpr uint32_t PW = A_FRAGS / 4;      // fragments each wave loads
     __shared__ __attribute__((aligned(1024))) uint8_t As0[A_FRAGS * 1024];
     __shared__ __attribute__((aligned(1024))) uint8_t As1[A_FRAGS * 1024];
     // (weight tile, split) columns are dealt round-robin to the 8 XCDs; each
@@ -273,17 +428,18 @@ k_gemm(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint32_t 
     const uint8_t* Wt = n0 < boundary ? W0 + (size_t)n0 * K : W1 + (size_t)(n0 - boundary) * K;
     const uint8_t* wrow = Wt + (size_t)l16 * K + k0 + 16 * g;
     const size_t plane = (size_t)stride_tokens * K;
-    // This wave's six A fragments of each stage: f = 6*wave + i, f = (mf*3 + p)*2 + h.
-    const uint16_t* asrc[6];
+    // This wave's PW A fragments of each stage: f = PW*wave + i,
+    // f = (mf*P + p)*2 + h.
+    const uint16_t* asrc[PW];
 #pragma unroll
-    for (int i = 0; i < 6; i++) {
-        const uint32_t f = 6 * wave + i, mf = f / 6, p = (f / 2) % 3, h = f % 2;
+    for (int i = 0; i < (int)PW; i++) {
+        const uint32_t f = PW * wave + i, mf = f / (2 * P), p = (f / 2) % P, h = f % 2;
         asrc[i] = xs + p * plane + (size_t)(m0 + 16 * mf + l16) * K + k0 + 16 * g + 8 * h;
     }
     auto load_a = [&](uint32_t dk, uint8_t* buf) {
 #pragma unroll
-        for (int i = 0; i < 6; i++) {
-            __builtin_amdgcn_global_load_lds(asrc[i] + dk, buf + (6 * wave + i) * 1024, 16, 0, 0);
+        for (int i = 0; i < (int)PW; i++) {
+            __builtin_amdgcn_global_load_lds(asrc[i] + dk, buf + (PW * wave + i) * 1024, 16, 0, 0);
         }
     };
     u32x4 wr[4];
@@ -304,24 +460,29 @@ k_gemm(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint32_t 
     // One stage: A fragments (mf, p, h) read from LDS one (p, h) group of four
     // ahead of its MFMAs; each fragment feeds the four weight fragments.
     auto compute = [&](const uint8_t* buf, const u32x4 (&w)[4]) {
-        bf16x8 b[4][2];
+        V b[4][2];
 #pragma unroll
         for (int nf = 0; nf < 4; nf++) {
-            fp8x16_to_bf16x8x2(w[nf], b[nf][0], b[nf][1]);
+            if constexpr (P == PLANES_BF16) {
+                fp8x16_to_bf16x8x2(w[nf], b[nf][0], b[nf][1]);
+            } else {
+                fp8x16_to_f16x8x2(w[nf], b[nf][0], b[nf][1]);
+            }
         }
-        bf16x8 ac[4], an[4];
-        auto read_group = [&](int j, bf16x8 (&dst)[4]) {
-            const int h = j / 3, p = 2 - j % 3;
+        V ac[4], an[4];
+        // Groups j: k-slice h = j / P, planes from the smallest (p = P - 1) up.
+        auto read_group = [&](int j, V (&dst)[4]) {
+            const int h = j / P, p = (P - 1) - j % P;
 #pragma unroll
             for (int mf = 0; mf < 4; mf++) {
-                dst[mf] = __builtin_bit_cast(bf16x8, *reinterpret_cast<const u32x4*>(
-                    buf + ((mf * 3 + p) * 2 + h) * 1024 + 16 * lane));
+                dst[mf] = __builtin_bit_cast(V, *reinterpret_cast<const u32x4*>(
+                    buf + ((mf * P + p) * 2 + h) * 1024 + 16 * lane));
             }
         };
         read_group(0, ac);
 #pragma unroll
-        for (int j = 0; j < 6; j++) {
-            if (j < 5) {
+        for (int j = 0; j < 2 * P; j++) {
+            if (j < 2 * P - 1) {
                 read_group(j + 1, an);
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -329,8 +490,13 @@ k_gemm(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint32_t 
             for (int mf = 0; mf < 4; mf++) {
 #pragma unroll
                 for (int nf = 0; nf < 4; nf++) {
-                    acc[mf][nf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac[mf], b[nf][j / 3],
-                        acc[mf][nf], 0, 0, 0);
+                    if constexpr (P == PLANES_BF16) {
+                        acc[mf][nf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac[mf],
+                            b[nf][j / P], acc[mf][nf], 0, 0, 0);
+                    } else {
+                        acc[mf][nf] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac[mf],
+                            b[nf][j / P], acc[mf][nf], 0, 0, 0);
+                    }
                 }
             }
             __builtin_amdgcn_sched_barrier(0);
@@ -374,7 +540,7 @@ k_gemm(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint32_t 
         }
         compute(As1, wc);
     }
-    // D layout of v_mfma_f32_16x16x32_bf16: lane l holds rows 4*(l/16) + r,
+    // D layout of v_mfma_f32_16x16x32_{bf16,f16}: lane l holds rows 4*(l/16) + r,
     // column l%16 of each 16x16 tile.
     float* o = out + (size_t)s * stride_tokens * N;
 #pragma unroll
@@ -392,21 +558,43 @@ k_gemm(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint32_t 
     }
 }
 
+// The two plane formats as kernels (a kernel template's host stub would have
+// to instantiate the FP16 body on the host).
+__global__ void __launch_bounds__(256, 2)
+k_gemm_bf16(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint32_t boundary,
+    uint32_t N, uint32_t K, const uint16_t* __restrict__ xs, uint32_t stride_tokens,
+    uint32_t count, uint32_t m_tiles, uint32_t splits, float* __restrict__ out)
+{
+    gemm_tile<PLANES_BF16>(W0, W1, boundary, N, K, xs, stride_tokens, count, m_tiles, splits, out);
+}
+
+__global__ void __launch_bounds__(256, 2)
+k_gemm_f16(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint32_t boundary,
+    uint32_t N, uint32_t K, const uint16_t* __restrict__ xs, uint32_t stride_tokens,
+    uint32_t count, uint32_t m_tiles, uint32_t splits, float* __restrict__ out)
+{
+    gemm_tile<PLANES_F16>(W0, W1, boundary, N, K, xs, stride_tokens, count, m_tiles, splits, out);
+}
+
 // x[i] = x[i] + scale * (((p0 + p1) + p2) + ...) (deterministic split-K
 // combine with the residual add, src/metal_encode.m:160,175); without the
 // residual, x[i] = scale * (...). Partials P[s][i] with split stride
-// split_stride; i runs over count * rows in float4 units. grid
+// split_stride, split s of token m first times in_scale[m][s] when given; i
+// runs over count * rows in float4 units (rows4 = rows / 4 per token). grid
 // ceil(count * rows / 1024), block 256.
 template <int S>
 __global__ void __launch_bounds__(256)
 k_combine_residual(const float* __restrict__ partial, size_t split_stride, size_t n4, float scale,
-    float* __restrict__ x, int residual)
+    const float* __restrict__ in_scale, uint32_t rows4, float* __restrict__ x, int residual)
 {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n4) {
         return;
     }
-    const float4 acc = sum_splits<S>(reinterpret_cast<const float4*>(partial) + i, split_stride / 4);
+    const float4* pi = reinterpret_cast<const float4*>(partial) + i;
+    const float4 acc = in_scale
+        ? sum_splits_scaled<S>(pi, split_stride / 4, in_scale + (i / rows4) * S)
+        : sum_splits<S>(pi, split_stride / 4);
     float4* xr = reinterpret_cast<float4*>(x) + i;
     float4 v = make_float4(acc.x * scale, acc.y * scale, acc.z * scale, acc.w * scale);
     if (residual) {
@@ -443,13 +631,32 @@ static size_t partial_floats(uint32_t B)
     return (size_t)4 * B * MAX_N;
 }
 
+// Bytes of the activation planes: three BF16 (or two FP16) planes of up to
+// 9216 columns per token. The scales of the FP16 planes follow them: one per
+// token for the gate|up input, DOWN_SPLITS per token for the down input.
+static size_t plane_bytes(size_t B)
+{
+    return 3 * B * LH_INNER * sizeof(uint16_t);
+}
+
+static float* token_scales(const lh_workspace* ws)
+{
+    return reinterpret_cast<float*>(reinterpret_cast<char*>(ws->d_split) +
+        plane_bytes(padded_block(ws)));
+}
+
+static float* group_scales(const lh_workspace* ws)
+{
+    return token_scales(ws) + padded_block(ws);
+}
+
 extern "C" int lh_mfma_prepare(lh_workspace* ws)
 {
     if (ws->d_split && ws->d_gemm) {
         return 0;
     }
     const size_t B = padded_block(ws);
-    const size_t split_bytes = 3 * B * LH_INNER * sizeof(uint16_t);
+    const size_t split_bytes = plane_bytes(B) + (1 + DOWN_SPLITS) * B * sizeof(float);
     const size_t gemm_bytes = partial_floats((uint32_t)B) * sizeof(float);
     if (hipMalloc((void**)&ws->d_split, split_bytes) != hipSuccess ||
         hipMalloc((void**)&ws->d_gemm, gemm_bytes) != hipSuccess) {
@@ -469,8 +676,9 @@ extern "C" int lh_mfma_prepare(lh_workspace* ws)
 
 // Calls f(std::integral_constant<int, S>) for the split count S, which the
 // elementwise kernels take as a template argument so that every partial load
-// issues before the first add. S = 0 (no partials) only where ZERO is set.
-template <bool ZERO = false, typename F>
+// issues before the first add. S = 0 (no partials) only where ZERO is set;
+// counts above MAXS are rejected (and not instantiated).
+template <bool ZERO = false, int MAXS = 16, typename F>
 static int with_splits(uint32_t splits, const char* what, F&& f)
 {
     switch (splits) {
@@ -484,8 +692,20 @@ static int with_splits(uint32_t splits, const char* what, F&& f)
     case 1: f(std::integral_constant<int, 1>{}); break;
     case 2: f(std::integral_constant<int, 2>{}); break;
     case 4: f(std::integral_constant<int, 4>{}); break;
-    case 8: f(std::integral_constant<int, 8>{}); break;
-    case 16: f(std::integral_constant<int, 16>{}); break;
+    case 8:
+        if constexpr (MAXS >= 8) {
+            f(std::integral_constant<int, 8>{});
+            break;
+        }
+        lh_set_error("%s: unsupported split count %u", what, splits);
+        return -1;
+    case 16:
+        if constexpr (MAXS >= 16) {
+            f(std::integral_constant<int, 16>{});
+            break;
+        }
+        lh_set_error("%s: unsupported split count %u", what, splits);
+        return -1;
     default:
         lh_set_error("%s: unsupported split count %u", what, splits);
         return -1;
@@ -501,21 +721,33 @@ static int split_rows(const float* x, uint16_t* xs, uint32_t width, uint32_t cou
     return launched_ok("split");
 }
 
-// x = x + scale * sum of `splits` partials (0: x unchanged), then the RMSNorm
-// of x with gamma split into xs; rows of 3072.
+// x = x + scale * sum of `splits` partials, split s times in_scale[t][s] when
+// given (0 splits: x unchanged), then
+// the RMSNorm of x with gamma as the next GEMM's input planes in xs: two FP16
+// planes with their row scales in out_scale, or (out_scale NULL) three BF16
+// planes; rows of 3072.
 static int residual_norm_split(const float* partial, uint32_t splits, uint32_t stride,
-    float scale, float* x, const float* gamma, uint16_t* xs, uint32_t count, hipStream_t s)
+    float scale, const float* in_scale, float* x, const float* gamma, uint16_t* xs,
+    float* out_scale, uint32_t count, hipStream_t s)
 {
     return with_splits<true>(splits, "residual norm split", [&](auto S) {
-        hipLaunchKernelGGL(k_residual_norm_split<decltype(S)::value>, dim3(count), dim3(768), 0, s,
-            partial, (size_t)stride * LH_HIDDEN, scale, x, gamma, xs, stride);
+        if (out_scale) {
+            hipLaunchKernelGGL((k_residual_norm_split<decltype(S)::value, true>), dim3(count),
+                dim3(768), 0, s, partial, (size_t)stride * LH_HIDDEN, scale, in_scale, x, gamma,
+                xs, out_scale, stride);
+        } else {
+            hipLaunchKernelGGL((k_residual_norm_split<decltype(S)::value, false>), dim3(count),
+                dim3(768), 0, s, partial, (size_t)stride * LH_HIDDEN, scale, in_scale, x, gamma,
+                xs, out_scale, stride);
+        }
     });
 }
 
-// P[s][m][n] for n < N over `splits` equal K ranges. N and boundary multiples
-// of 256, K a multiple of 64*splits, (N/256 * splits) a multiple of 8.
-static int gemm(const uint8_t* W0, const uint8_t* W1, uint32_t boundary, uint32_t N, uint32_t K,
-    const uint16_t* xs, uint32_t stride, uint32_t count, uint32_t splits, float* out,
+// P[s][m][n] for n < N over `splits` equal K ranges from `planes` activation
+// planes (PLANES_BF16 or PLANES_F16). N and boundary multiples of 256, K a
+// multiple of 64*splits, (N/256 * splits) a multiple of 8.
+static int gemm(int planes, const uint8_t* W0, const uint8_t* W1, uint32_t boundary, uint32_t N,
+    uint32_t K, const uint16_t* xs, uint32_t stride, uint32_t count, uint32_t splits, float* out,
     hipStream_t s)
 {
     const uint32_t n_tiles = N / GN;
@@ -526,19 +758,24 @@ static int gemm(const uint8_t* W0, const uint8_t* W1, uint32_t boundary, uint32_
         lh_set_error("gemm: unsupported shape N=%u K=%u splits=%u", N, K, splits);
         return -1;
     }
-    hipLaunchKernelGGL(k_gemm, dim3(n_tiles * m_tiles * splits), dim3(256), 0, s, W0,
-        W1 ? W1 : W0, boundary, N, K, xs, stride, count, m_tiles, splits, out);
+    if (planes == PLANES_BF16) {
+        hipLaunchKernelGGL(k_gemm_bf16, dim3(n_tiles * m_tiles * splits), dim3(256), 0, s,
+            W0, W1 ? W1 : W0, boundary, N, K, xs, stride, count, m_tiles, splits, out);
+    } else {
+        hipLaunchKernelGGL(k_gemm_f16, dim3(n_tiles * m_tiles * splits), dim3(256), 0, s,
+            W0, W1 ? W1 : W0, boundary, N, K, xs, stride, count, m_tiles, splits, out);
+    }
     return launched_ok("gemm");
 }
 
 static int combine(const float* partial, uint32_t splits, uint32_t rows, uint32_t count,
-    uint32_t stride, float scale, float* x, int residual, hipStream_t s)
+    uint32_t stride, float scale, const float* in_scale, float* x, int residual, hipStream_t s)
 {
     const size_t n4 = (size_t)count * rows / 4;
     return with_splits(splits, "split-K combine", [&](auto S) {
         hipLaunchKernelGGL(k_combine_residual<decltype(S)::value>,
             dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, partial,
-            (size_t)stride * rows, n4, scale, x, residual);
+            (size_t)stride * rows, n4, scale, in_scale, rows / 4, x, residual);
     });
 }
 
@@ -564,17 +801,23 @@ extern "C" int lh_fp8_gemm(lh_workspace* ws, const uint8_t* d_w, float scale, co
     const uint32_t stages = (uint32_t)cols / BK;
     const uint32_t splits = stages % 16 == 0 ? 16 : (stages % 8 == 0 ? 8 : 4);
     if (split_rows(d_x, ws->d_split, (uint32_t)cols, n, B, s) ||
-        gemm(d_w, NULL, (uint32_t)rows, (uint32_t)rows, (uint32_t)cols, ws->d_split, B, n,
-            splits, ws->d_gemm, s)) {
+        gemm(PLANES_BF16, d_w, NULL, (uint32_t)rows, (uint32_t)rows, (uint32_t)cols, ws->d_split,
+            B, n, splits, ws->d_gemm, s)) {
         return -1;
     }
-    return combine(ws->d_gemm, splits, (uint32_t)rows, n, B, scale, d_y, 0, s);
+    return combine(ws->d_gemm, splits, (uint32_t)rows, n, B, scale, NULL, d_y, 0, s);
 }
 
 // One layer over ws->count tokens. input_split: ws->d_split already holds the
-// BF16 split of input_norm(x) (the previous layer's last kernel wrote it);
-// next_norm: the last kernel also writes the split of next_norm(x) for the
-// following layer (NULL: plain residual combine).
+// BF16 planes of input_norm(x) (the previous layer's last kernel wrote them);
+// next_norm: the last kernel also writes them for the following layer (NULL:
+// plain residual combine). The gate|up and down inputs travel as two FP16
+// planes with power-of-two scales (per token for gate|up, per token and K split
+// for down). The q|k|v input stays
+// in three exact BF16 planes: its error reaches the attention scores, which
+// the softmax amplifies (at scores of a few hundred, two FP16 planes put the
+// config-3 layer at 1.2e-3 of the row maximum, over the 1e-3 tolerance), and
+// so does the attention output, which no single workgroup sees whole.
 extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, float* d_keys,
     float* d_values, lh_workspace* ws, int input_split, const float* next_norm, hipStream_t s)
 {
@@ -589,14 +832,16 @@ extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, floa
     const uint32_t B = padded_block(ws);
     float* P = ws->d_gemm;
     uint16_t* xs = ws->d_split;
+    float* scale_a = token_scales(ws);
+    float* scale_b = group_scales(ws);
     // K splits (measured at 256 tokens): gate|up 4 (the partial buffer's
     // limit), q|k|v 8, o 8, down 16.
     // q|k|v: 6144 rows, 3072 columns; scales, RoPE and the KV append in the
     // epilogue.
     const uint32_t sq = 8;
     if ((!input_split &&
-            residual_norm_split(NULL, 0, B, 1.0f, d_x, w->input_norm, xs, n, s)) ||
-        gemm(w->qkv, NULL, LH_QKV_ROWS, LH_QKV_ROWS, LH_HIDDEN, xs, B, n, sq, P, s) ||
+            residual_norm_split(NULL, 0, B, 1.0f, NULL, d_x, w->input_norm, xs, NULL, n, s)) ||
+        gemm(PLANES_BF16, w->qkv, NULL, LH_QKV_ROWS, LH_QKV_ROWS, LH_HIDDEN, xs, B, n, sq, P, s) ||
         with_splits(sq, "qkv epilogue", [&](auto S) {
             hipLaunchKernelGGL(k_qkv_epilogue<decltype(S)::value>, dim3(n, 3), dim3(256), 0, s,
                 P, (size_t)B * LH_QKV_ROWS, make_float3(w->scale[0], w->scale[1], w->scale[2]),
@@ -604,32 +849,34 @@ extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, floa
         })) {
         return -1;
     }
-    // Attention writes the o projection's input split; o: 3072 rows, 4096
-    // columns; residual, post-norm and the gate|up split after it.
+    // Attention writes the o projection's input as BF16 planes; o: 3072 rows,
+    // 4096 columns; residual, post-norm and the gate|up input after it.
     const uint32_t so = 8;
     if (lh_launch_attention_mfma(ws->d_q, d_keys, d_values, ws->d_params, (uint32_t)ws->length,
             n, C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_attn, xs, B, s) ||
         launched_ok("attention") ||
-        gemm(w->o, NULL, LH_HIDDEN, LH_HIDDEN, LH_QUERY, xs, B, n, so, P, s) ||
-        residual_norm_split(P, so, B, w->scale[3], d_x, w->post_norm, xs, n, s)) {
+        gemm(PLANES_BF16, w->o, NULL, LH_HIDDEN, LH_HIDDEN, LH_QUERY, xs, B, n, so, P, s) ||
+        residual_norm_split(P, so, B, w->scale[3], NULL, d_x, w->post_norm, xs, scale_a, n, s)) {
         return -1;
     }
-    // gate|up: 18432 rows, 3072 columns; SiLU(gate)*up in the down
-    // projection's split.
+    // gate|up: 18432 rows, 3072 columns; SiLU(gate)*up as the down
+    // projection's input.
     const uint32_t sg = 4;
-    if (gemm(w->gate, w->up, LH_INNER, MAX_N, LH_HIDDEN, xs, B, n, sg, P, s) ||
-        with_splits(sg, "silu split", [&](auto S) {
-            hipLaunchKernelGGL(k_split_silu<decltype(S)::value>, dim3(n, 5), dim3(256), 0, s, P,
-                (size_t)B * MAX_N, make_float2(w->scale[4], w->scale[5]), xs, B);
+    if (gemm(PLANES_F16, w->gate, w->up, LH_INNER, MAX_N, LH_HIDDEN, xs, B, n, sg, P, s) ||
+        with_splits<false, 4>(sg, "silu split", [&](auto S) {
+            hipLaunchKernelGGL(k_split_silu<decltype(S)::value>, dim3(n, DOWN_SPLITS), dim3(192),
+                0, s, P, (size_t)B * MAX_N, make_float2(w->scale[4], w->scale[5]), scale_a, xs,
+                scale_b, B);
         })) {
         return -1;
     }
     // down: 3072 rows, 9216 columns, residual (and the next layer's input
-    // split).
-    const uint32_t sd = 16;
-    if (gemm(w->down, NULL, LH_HIDDEN, LH_HIDDEN, LH_INNER, xs, B, n, sd, P, s)) {
+    // planes).
+    const uint32_t sd = DOWN_SPLITS;   // also the granule of the down input's scales
+    if (gemm(PLANES_F16, w->down, NULL, LH_HIDDEN, LH_HIDDEN, LH_INNER, xs, B, n, sd, P, s)) {
         return -1;
     }
-    return next_norm ? residual_norm_split(P, sd, B, w->scale[6], d_x, next_norm, xs, n, s)
-                     : combine(P, sd, LH_HIDDEN, n, B, w->scale[6], d_x, 1, s);
+    return next_norm
+        ? residual_norm_split(P, sd, B, w->scale[6], scale_b, d_x, next_norm, xs, NULL, n, s)
+        : combine(P, sd, LH_HIDDEN, n, B, w->scale[6], scale_b, d_x, 1, s);
 }
