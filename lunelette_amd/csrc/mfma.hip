@@ -14,8 +14,8 @@
 //   BF16 or FP16 (v_cvt_scalef32_pk_{bf16,f16}_fp8, unit scale: every E4M3FN
 //   value has at most 4 significant bits and fits either type). The plane
 //   products accumulate in FP32.
-// - k_gemm_bf16 / k_gemm_f16: a 256-thread workgroup owns 64 tokens x 256 weight rows of one K
-//   split; each wave owns 64 weight rows and all 64 tokens (4 x 4 MFMA
+// - k_gemm_bf16 / k_gemm_f16: a 256-thread workgroup owns 64 tokens x 256
+//   weight rows of one K split; each wave owns 64 weight rows and all 64 tokens (4 x 4 MFMA
 //   tiles). Per 64-column stage the activation tile (64 tokens x P planes,
 //   8P KB) goes to LDS by direct loads (global_load_lds_dwordx4) in
 //   fragment-major order, so each v_mfma_f32_16x16x32_{bf16,f16} A operand is
@@ -61,7 +61,7 @@ constexpr uint32_t BK = 64;               // columns per pipeline stage
 constexpr uint32_t SPLIT_ROWS = 128;      // token stride granule of the split planes
 constexpr uint32_t MAX_N = 2 * LH_INNER;  // widest GEMM: gate|up
 
-// Activation plane formats of k_gemm: three exact BF16 planes (hi + mid + lo),
+// Activation plane formats of the GEMM: three exact BF16 planes (hi + mid + lo),
 // or two FP16 planes of a row scaled by 2^e (h + l, about 22 significant bits).
 enum { PLANES_BF16 = 3, PLANES_F16 = 2 };
 
