@@ -15,8 +15,8 @@
 //   value has at most 4 significant bits and fits either type). The plane
 //   products accumulate in FP32.
 // - k_gemm_bf16 / k_gemm_f16: a 256-thread workgroup owns 64 tokens x 256
-//   weight rows of one K split; each wave owns 64 weight rows and all 64 tokens (4 x 4 MFMA
-//   tiles). Per 64-column stage the activation tile (64 tokens x P planes,
+//   weight rows of one K split; each wave owns 64 weight rows and all 64
+//   tokens (4 x 4 MFMA tiles). Per 64-column stage the activation tile (64 tokens x P planes,
 //   8P KB) goes to LDS by direct loads (global_load_lds_dwordx4) in
 //   fragment-major order, so each v_mfma_f32_16x16x32_{bf16,f16} A operand is
 //   one conflict-free 16-byte LDS read, shared by the four waves; each wave
