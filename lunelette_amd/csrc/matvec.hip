@@ -133,69 +133,33 @@ __device__ __forceinline__ void fill_lut(float* lut)
 // words: lane l's 16 values of chunk c (columns c*1024 + 16l .. +15) are the
 // words (4c + q)*64 + l, q = 0..3, so a wave reads a chunk with four
 // conflict-free 16-byte loads. Staging is split around the weight loads:
-// stage_load issues the row (and gamma) loads first, since vector loads retire
-// in issue order; stage_commit writes LDS and, with gamma, has wave 0 apply the
-// canonical RMSNorm in place: ss by the row-dot schedule with w = x,
-// r = 1/sqrt(ss/n + 1e-5), x = gamma * (x * r).
+// stage_load issues the row loads first, since vector loads retire in issue
+// order; stage_commit writes LDS.
 __device__ __forceinline__ uint32_t staged_word(int i, uint32_t tid)
 {
     // float4 index tid + 256*i of the row is chunk i, lane tid/4, quad tid%4
     return (4 * i + (tid & 3)) * 64 + (tid >> 2);
 }
 
-template <int NCH, bool NORM>
-__device__ __forceinline__ void stage_load(const float* row, const float* gamma, float4 (&xv)[NCH],
-    float4 (&gv)[NCH])
+template <int NCH>
+__device__ __forceinline__ void stage_load(const float* row, float4 (&xv)[NCH])
 {
     const uint32_t tid = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < NCH; i++) {
         xv[i] = reinterpret_cast<const float4*>(row)[tid + 256 * i];
     }
-    if constexpr (NORM) {
-#pragma unroll
-        for (int i = 0; i < NCH; i++) {
-            gv[i] = reinterpret_cast<const float4*>(gamma)[tid + 256 * i];
-        }
-    }
 }
 
-template <int NCH, bool NORM>
-__device__ __forceinline__ void stage_commit(const float4 (&xv)[NCH], const float4 (&gv)[NCH],
-    float4* xl, float4* gl)
+template <int NCH>
+__device__ __forceinline__ void stage_commit(const float4 (&xv)[NCH], float4* xl)
 {
-    const uint32_t tid = threadIdx.x, lane = tid & 63;
+    const uint32_t tid = threadIdx.x;
 #pragma unroll
     for (int i = 0; i < NCH; i++) {
         xl[staged_word(i, tid)] = xv[i];
-        if constexpr (NORM) {
-            gl[staged_word(i, tid)] = gv[i];
-        }
     }
     __syncthreads();
-    if constexpr (NORM) {
-        if ((tid >> 6) == 0) {
-            float acc = 0.0f;
-#pragma unroll
-            for (int w = 0; w < NCH * 4; w++) {
-                const float4 v = xl[w * 64 + lane];
-                acc = __builtin_fmaf(v.x, v.x, acc);
-                acc = __builtin_fmaf(v.y, v.y, acc);
-                acc = __builtin_fmaf(v.z, v.z, acc);
-                acc = __builtin_fmaf(v.w, v.w, acc);
-            }
-            const float ss = wave_lane0(wave_tree64(acc));
-            const float r = 1.0f / __builtin_sqrtf(ss / (float)(NCH * LH_CHUNK) + 1e-5f);
-#pragma unroll
-            for (int w = 0; w < NCH * 4; w++) {
-                const float4 v = xl[w * 64 + lane];
-                const float4 g = gl[w * 64 + lane];
-                xl[w * 64 + lane] = make_float4(g.x * (v.x * r), g.y * (v.y * r),
-                    g.z * (v.z * r), g.w * (v.w * r));
-            }
-        }
-        __syncthreads();
-    }
 }
 
 // Norm-prologue staging of a 3072-wide row for a T-thread workgroup. Thread
@@ -328,8 +292,8 @@ k_rows(const void* __restrict__ W, float scale, const float* __restrict__ x, flo
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
     const uint32_t t = blockIdx.y;
     const uint32_t row0 = (blockIdx.x * 4 + wave) * R;
-    float4 xv[NCH], gv[NCH];
-    stage_load<NCH, false>(x + (size_t)t * NCH * LH_CHUNK, nullptr, xv, gv);
+    float4 xv[NCH];
+    stage_load<NCH>(x + (size_t)t * NCH * LH_CHUNK, xv);
     uint32_t rr[R];
 #pragma unroll
     for (int r = 0; r < R; r++) {
@@ -337,7 +301,7 @@ k_rows(const void* __restrict__ W, float scale, const float* __restrict__ x, flo
     }
     WVec<KIND> wv[R][NCH];
     issue_rows<KIND, NCH, R>(W, rr, wv);
-    stage_commit<NCH, false>(xv, gv, xin_s, nullptr);
+    stage_commit<NCH>(xv, xin_s);
     float dots[R];
     dot_rows<KIND, LUT, NCH, R>(wv, xin_s, lut_s, dots);
     if (lane == 0) {
@@ -525,22 +489,27 @@ k_gateup_silu(const uint8_t* __restrict__ Wgate, const uint8_t* __restrict__ Wup
 }
 
 // Final RMSNorm -> tied BF16 head (src/metal_encode.m:204-210); the embedding
-// stays BF16 in HBM and widens exactly in registers. grid (VOCAB/16). With
-// nonfinite set, a workgroup that writes an Inf or NaN logit stores 1 there
-// (the caller clears it first), so the host need not scan every logit.
-__global__ void __launch_bounds__(256)
+// stays BF16 in HBM and widens exactly in registers. Eight waves of four rows
+// per workgroup share one staging of the row (the row loads are issued before
+// any weight load). grid (VOCAB/32), block 512. With nonfinite set, a wave
+// that writes an Inf or NaN logit stores 1 there (the caller clears it
+// first), so the host need not scan every logit.
+__global__ void __launch_bounds__(512)
 k_head(const uint16_t* __restrict__ E, const float* __restrict__ gamma,
     const float* __restrict__ xrow, float* __restrict__ logits, uint32_t* __restrict__ nonfinite)
 {
+    constexpr int T = 512;
+    __shared__ float4 xin_s[3 * 4 * 64];
+    __shared__ float r_s;
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    const uint32_t row0 = (blockIdx.x * 4 + wave) * 4;
+    const uint32_t row0 = (blockIdx.x * 8 + wave) * 4;
     const uint32_t rr[4] = {row0, row0 + 1, row0 + 2, row0 + 3};
-    __shared__ float4 xin_s[3 * 4 * 64], gam_s[3 * 4 * 64];
-    float4 xv[3], gv[3];
-    stage_load<3, true>(xrow, gamma, xv, gv);
+    float2 xv[1536 / T], gv[1536 / T];
+    norm_load<T>(xrow, gamma, xv, gv);
+    __syncthreads();
     WVec<K_BF16> wv[4][3];
     issue_rows<K_BF16, 3, 4>(E, rr, wv);
-    stage_commit<3, true>(xv, gv, xin_s, gam_s);
+    norm_commit<T>(xv, gv, xin_s, &r_s);
     float dots[4];
     dot_rows<K_BF16, false, 3, 4>(wv, xin_s, nullptr, dots);
     if (lane == 0) {
@@ -709,7 +678,7 @@ extern "C" int lh_launch_gateup_silu(int lookup, const uint8_t* Wgate, const uin
 extern "C" int lh_launch_head(const uint16_t* E, const float* gamma, const float* xrow,
     float* logits, uint32_t* nonfinite, hipStream_t s)
 {
-    hipLaunchKernelGGL(k_head, dim3(LH_VOCAB / 16), dim3(256), 0, s, E, gamma, xrow, logits,
+    hipLaunchKernelGGL(k_head, dim3(LH_VOCAB / 32), dim3(512), 0, s, E, gamma, xrow, logits,
         nonfinite);
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
