@@ -15,6 +15,8 @@ The reference's own MPS path is pinned only by tolerance (tests/test_metal.m:
   values over 1..69 blocks, ragged token tiles and the causal sentinel of
   tests/test_metal.m:956-999.
 """
+import math
+
 import numpy as np
 import pytest
 
@@ -166,3 +168,27 @@ def test_attention_mfma_causal_sentinel(gpu):
                                        capacity)
     assert np.max(np.abs(got[:4096] - 1.0)) < 2e-4
     assert np.max(np.abs(got[4096:] - 8703.0 / 4352)) < 2e-4
+
+
+@pytest.mark.parametrize("shift", [14, -14])
+def test_mfma_layer_down_input_range(gpu, shift):
+    """gate and up scales times 2^shift put SiLU(gate)*up up to about 1e13
+    (far past FP16's 65504) or below about 1e-4 (mostly FP16 subnormals):
+    the down projection's two FP16 planes carry a power-of-two scale per token
+    and K split, so the layer stays within the config-3 tolerance of the
+    oracle."""
+    from test_gpu_layer import oracle_layer, run_layer
+    host = dict(syn.layer(SEED, 2))
+    for name in ("scale_gate", "scale_up"):
+        host[name] = math.ldexp(host[name], shift)   # exact: still BF16-exact and normal
+    length, count, capacity = 64, 128, 256
+    x = syn.normal_f32(SEED, 9201, count * 3072)
+    kpm = syn.normal_f32(SEED, 9202, length * 1024).reshape(length, 1024)
+    vpm = syn.normal_f32(SEED, 9203, length * 1024).reshape(length, 1024)
+    got = run_layer(gpu, host, x, kpm, vpm, length, count, capacity, lh.PATH_MFMA)
+    want = oracle_layer(host, x, kpm, vpm, length, count, capacity, MIRROR)
+    gx, wx = got[0].reshape(count, 3072), want[0].reshape(count, 3072)
+    assert np.isfinite(gx).all()
+    rowmax = np.max(np.abs(wx), axis=1, keepdims=True)
+    assert np.max(np.abs(gx - wx) / rowmax) < 1e-3
+    assert np.median(np.abs(gx - wx) / np.maximum(np.abs(wx), 1e-30)) < 1e-5
