@@ -331,7 +331,7 @@ def cpu_baseline(syn, seed, budget_s=20.0):
 def main():
     args = parse()
     if args.gpus != 1:
-        print("bench.py measures one MI355X: this build has no multi-GPU path "
+        print("bench.py measures one MI355X: the library has no multi-GPU path "
               "(--gpus %d requested)" % args.gpus, file=sys.stderr)
         sys.exit(2)
     import lunelette_amd as lh

@@ -2,7 +2,7 @@
  *
  * TEST INFRASTRUCTURE ONLY. Nothing in the product (lunelette_amd/, include/)
  * links, loads or calls this code. Only tests/, __graft_entry__.smoke() and the
- * cpu_baseline leg of bench.py use it, as the checker.
+ * cpu_baseline leg of bench.py use it, to check results against.
  *
  * Two schedules are restated for every reduction:
  *   - ORC_REF    ("ref-literal"): the reference's own arithmetic order where the
