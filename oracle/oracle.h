@@ -23,6 +23,9 @@
  *   greedy       -- tests/test_generation.c cases + oracle/_ref build
  *   matvec/norm/attention/rope/silu -- double-precision brute force and the
  *     reference's closed forms (all-ones dot == K, long causal sentinel).
+ *   layer/model composition -- an independent float64 restatement of
+ *     src/metal_encode.m:124-210 (tests/test_oracle_composition.py), with
+ *     planted composition mistakes (orc_model.c, ORC_PLANT) that must fail it.
  *   Apple simd_sum order, Metal precise exp/rsqrt/log: parity unpinned (no
  *   runnable Metal implementation exists; the ref-literal tree is our choice).
  */

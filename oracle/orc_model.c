@@ -8,6 +8,17 @@
 #include <stdlib.h>
 #include <string.h>
 
+/* Planted composition mistakes for the tests that show the independent float64
+ * restatement of the layer catches them (tests/test_oracle_composition.py
+ * builds this file with -DORC_PLANT=n; the shipped oracle has ORC_PLANT 0):
+ * 1 attention residual skipped, 2 post-norm fed x instead of x+o,
+ * 3 query factor on K instead of Q, 4 V rotated before caching,
+ * 5 head on row 0 instead of the last row, 6 K cached unrotated,
+ * 7 MLP residual added to the layer input instead of x+o. */
+#ifndef ORC_PLANT
+#define ORC_PLANT 0
+#endif
+
 static void widen(const uint16_t *src, float *dst, size_t n)
 {
     for (size_t i = 0; i < n; i++) {
@@ -45,8 +56,15 @@ void orc_layer_forward(int schedule, orc_model *model, size_t layer, float *x,
     orc_matvec(schedule, ORC_W_FP8, w->q, w->scale[0], xn, q, Q, H, count);
     orc_matvec(schedule, ORC_W_FP8, w->k, w->scale[1], xn, k, KV, H, count);
     orc_matvec(schedule, ORC_W_FP8, w->v, w->scale[2], xn, v, KV, H, count);
-    orc_rope(q, cosine, sine, factor, rq, Q, count);
-    orc_rope(k, cosine, sine, NULL, rk, KV, count);
+    orc_rope(q, cosine, sine, ORC_PLANT == 3 ? NULL : factor, rq, Q, count);
+    orc_rope(k, cosine, sine, ORC_PLANT == 3 ? factor : NULL, rk, KV, count);
+    if (ORC_PLANT == 4) {
+        memcpy(attn, v, count * KV * sizeof(float));
+        orc_rope(attn, cosine, sine, NULL, v, KV, count);
+    }
+    if (ORC_PLANT == 6) {
+        memcpy(rk, k, count * KV * sizeof(float));
+    }
     size_t cap = model->capacity;
     float *keys = model->keys + layer * ORC_KV_HEADS * cap * 128;
     float *values = model->values + layer * ORC_KV_HEADS * cap * 128;
@@ -60,17 +78,22 @@ void orc_layer_forward(int schedule, orc_model *model, size_t layer, float *x,
     }
     orc_attention(schedule, rq, keys, values, cap * 128, 128, length, count, attn);
     orc_matvec(schedule, ORC_W_FP8, w->o, w->scale[3], attn, o, H, Q, count);
-    for (size_t i = 0; i < count * H; i++) {
-        x[i] = x[i] + o[i];
+    float *before = ORC_PLANT == 2 || ORC_PLANT == 7 ? malloc(count * H * sizeof(float)) : NULL;
+    if (before) {
+        memcpy(before, x, count * H * sizeof(float));
     }
-    orc_rmsnorm(schedule, gamma_post, x, xn, H, count);
+    for (size_t i = 0; i < count * H; i++) {
+        x[i] = ORC_PLANT == 1 ? x[i] : x[i] + o[i];
+    }
+    orc_rmsnorm(schedule, gamma_post, ORC_PLANT == 2 ? before : x, xn, H, count);
     orc_matvec(schedule, ORC_W_FP8, w->gate, w->scale[4], xn, gate, I, H, count);
     orc_matvec(schedule, ORC_W_FP8, w->up, w->scale[5], xn, up, I, H, count);
     orc_silu_mul(schedule, gate, up, gate, count * I);
     orc_matvec(schedule, ORC_W_FP8, w->down, w->scale[6], gate, o, H, I, count);
     for (size_t i = 0; i < count * H; i++) {
-        x[i] = x[i] + o[i];
+        x[i] = (ORC_PLANT == 7 ? before[i] : x[i]) + o[i];
     }
+    free(before);
     free(xn); free(q); free(k); free(v); free(rq); free(rk); free(attn); free(o);
     free(gate); free(up); free(cosine); free(sine); free(factor);
 }
@@ -99,7 +122,8 @@ int orc_model_forward(int schedule, orc_model *model, const int64_t *ids,
     }
     float gamma[ORC_HIDDEN], final[ORC_HIDDEN];
     widen(model->final_norm, gamma, ORC_HIDDEN);
-    orc_rmsnorm(schedule, gamma, x + (count - 1) * ORC_HIDDEN, final, ORC_HIDDEN, 1);
+    size_t last = ORC_PLANT == 5 ? 0 : count - 1;
+    orc_rmsnorm(schedule, gamma, x + last * ORC_HIDDEN, final, ORC_HIDDEN, 1);
     orc_matvec(schedule, ORC_W_BF16, model->embedding, 1.0f, final, logits,
         ORC_VOCAB, ORC_HIDDEN, 1);
     free(x);

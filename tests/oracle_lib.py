@@ -45,30 +45,36 @@ def load():
     if _lib is None:
         if not os.path.exists(ORACLE):
             raise RuntimeError("oracle/liboracle.so is not built (make -C oracle)")
-        l = ctypes.CDLL(ORACLE)
-        i = ctypes.c_int
-        fp = ctypes.POINTER(c_f)
-        _p(l, "orc_fp8_decode", c_f, ctypes.c_uint8)
-        _p(l, "orc_bf16_widen", c_f, ctypes.c_uint16)
-        _p(l, "orc_bf16_round", ctypes.c_uint16, c_f)
-        _p(l, "orc_yarn", i, ctypes.c_uint32, fp, fp)
-        _p(l, "orc_query_factor", c_f, ctypes.c_uint32)
-        _p(l, "orc_select_greedy", i, c_void, c_size, ctypes.POINTER(ctypes.c_int64))
-        _p(l, "orc_expf", c_f, c_f)
-        _p(l, "orc_silu_ref", c_f, c_f)
-        _p(l, "orc_silu_mirror", c_f, c_f)
-        _p(l, "orc_matvec", None, i, i, c_void, c_f, c_void, c_void, c_size, c_size, c_size)
-        _p(l, "orc_rmsnorm", None, i, c_void, c_void, c_void, c_size, c_size)
-        _p(l, "orc_rope", None, c_void, c_void, c_void, c_void, c_void, c_size, c_size)
-        _p(l, "orc_silu_mul", None, i, c_void, c_void, c_void, c_size)
-        _p(l, "orc_attention", None, i, c_void, c_void, c_void, c_size, c_size, c_size, c_size,
-           c_void)
-        _p(l, "orc_layer_forward", None, i, ctypes.POINTER(Model), c_size, c_void, c_size, c_size)
-        _p(l, "orc_model_forward", i, i, ctypes.POINTER(Model), c_void, c_size, c_size, c_void)
-        _p(l, "orc_set_threads", None, i)
-        _p(l, "orc_get_threads", i)
-        _lib = l
+        _lib = load_path(ORACLE)
     return _lib
+
+
+def load_path(path):
+    """An oracle build at `path` (the shipped one, or a planted-mistake variant
+    a test compiled) with its prototypes declared."""
+    l = ctypes.CDLL(path)
+    i = ctypes.c_int
+    fp = ctypes.POINTER(c_f)
+    _p(l, "orc_fp8_decode", c_f, ctypes.c_uint8)
+    _p(l, "orc_bf16_widen", c_f, ctypes.c_uint16)
+    _p(l, "orc_bf16_round", ctypes.c_uint16, c_f)
+    _p(l, "orc_yarn", i, ctypes.c_uint32, fp, fp)
+    _p(l, "orc_query_factor", c_f, ctypes.c_uint32)
+    _p(l, "orc_select_greedy", i, c_void, c_size, ctypes.POINTER(ctypes.c_int64))
+    _p(l, "orc_expf", c_f, c_f)
+    _p(l, "orc_silu_ref", c_f, c_f)
+    _p(l, "orc_silu_mirror", c_f, c_f)
+    _p(l, "orc_matvec", None, i, i, c_void, c_f, c_void, c_void, c_size, c_size, c_size)
+    _p(l, "orc_rmsnorm", None, i, c_void, c_void, c_void, c_size, c_size)
+    _p(l, "orc_rope", None, c_void, c_void, c_void, c_void, c_void, c_size, c_size)
+    _p(l, "orc_silu_mul", None, i, c_void, c_void, c_void, c_size)
+    _p(l, "orc_attention", None, i, c_void, c_void, c_void, c_size, c_size, c_size, c_size,
+       c_void)
+    _p(l, "orc_layer_forward", None, i, ctypes.POINTER(Model), c_size, c_void, c_size, c_size)
+    _p(l, "orc_model_forward", i, i, ctypes.POINTER(Model), c_void, c_size, c_size, c_void)
+    _p(l, "orc_set_threads", None, i)
+    _p(l, "orc_get_threads", i)
+    return l
 
 
 def load_ref():
@@ -122,7 +128,8 @@ def yarn(position):
 class HostModel:
     """Oracle model over host arrays (keeps the arrays alive)."""
 
-    def __init__(self, embedding, final_norm, layers, capacity):
+    def __init__(self, embedding, final_norm, layers, capacity, lib=None):
+        self.lib = lib
         self.keep = [embedding, final_norm]
         self.keys = np.zeros(len(layers) * 8 * capacity * 128, dtype=np.float32)
         self.values = np.zeros_like(self.keys)
@@ -146,14 +153,14 @@ class HostModel:
     def forward(self, schedule, ids, length):
         ids = np.ascontiguousarray(ids, dtype=np.int64)
         logits = np.empty(131072, dtype=np.float32)
-        rc = load().orc_model_forward(schedule, ctypes.byref(self.model), ptr(ids), length,
+        rc = (self.lib or load()).orc_model_forward(schedule, ctypes.byref(self.model), ptr(ids), length,
                                       len(ids), ptr(logits))
         if rc:
             raise RuntimeError("oracle forward rejected")
         return logits
 
     def layer_forward(self, schedule, layer, x, length, count):
-        load().orc_layer_forward(schedule, ctypes.byref(self.model), layer, ptr(x), length, count)
+        (self.lib or load()).orc_layer_forward(schedule, ctypes.byref(self.model), layer, ptr(x), length, count)
 
     def kv(self, layer, kind, position, count):
         """[count][1024] rows in the reference's position-major layout."""
