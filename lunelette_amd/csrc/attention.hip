@@ -444,18 +444,25 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
     if (b_begin < b_end) {
         load_block(b_begin);
     }
+    // Rows past the tile's last visible position hold whatever an earlier
+    // sequence (or a failed step) left in the cache. Masked weights are 0, and
+    // 0 * Inf would be NaN in P.V, so those rows are staged as zeros.
+    const uint32_t visible = length + last;
     for (uint32_t b = b_begin; b < b_end; b++) {
         // Stage K (float4 rows, stride 132) and V (stride 129) of the block.
         __syncthreads();   // the previous block's tiles are consumed
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const uint32_t idx = tid + 256 * i, row = idx >> 5, c4 = idx & 31;
-            *reinterpret_cast<fa_floatx4*>(&Ks[row * FA_KS + 4 * c4]) = kr[i];
+            const bool live = b * LH_ATTN_BLOCK + row <= visible;
+            const fa_floatx4 zero = fa_floatx4{0.f, 0.f, 0.f, 0.f};
+            const fa_floatx4 kk = live ? kr[i] : zero, vv = live ? vr[i] : zero;
+            *reinterpret_cast<fa_floatx4*>(&Ks[row * FA_KS + 4 * c4]) = kk;
             float* vd = &Vs[row * FA_VS + 4 * c4];
-            vd[0] = vr[i].x;
-            vd[1] = vr[i].y;
-            vd[2] = vr[i].z;
-            vd[3] = vr[i].w;
+            vd[0] = vv.x;
+            vd[1] = vv.y;
+            vd[2] = vv.z;
+            vd[3] = vv.w;
         }
         __syncthreads();
         if (b + 1 < b_end) {

@@ -46,10 +46,11 @@ class DeviceLayer:
         self.weights = w
 
 
-def kv_to_device_layout(kpm, capacity):
-    """[n][1024] position-major -> [8][capacity][128] head-major."""
+def kv_to_device_layout(kpm, capacity, tail=0.0):
+    """[n][1024] position-major -> [8][capacity][128] head-major; rows past n
+    hold `tail`."""
     n = kpm.shape[0]
-    out = np.zeros((8, capacity, 128), np.float32)
+    out = np.full((8, capacity, 128), tail, np.float32)
     out[:, :n] = kpm.reshape(n, 8, 128).transpose(1, 0, 2)
     return out
 
@@ -59,9 +60,10 @@ def kv_from_device_layout(khm, position, count):
         count, 1024)
 
 
-def attention_on_device(gpu, entry, q, kpm, vpm, length, count, capacity):
+def attention_on_device(gpu, entry, q, kpm, vpm, length, count, capacity, tail=0.0):
     """Run an attention entry point (lh_attention or lh_attention_mfma) on
-    position-major q/K/V; returns [count][4096] and checks the output guard."""
+    position-major q/K/V (cache rows past them hold `tail`); returns
+    [count][4096] and checks the output guard."""
     ws = gpu.lh_workspace_create(capacity, count)
     assert ws, lh.last_error()
     try:
@@ -69,8 +71,8 @@ def attention_on_device(gpu, entry, q, kpm, vpm, length, count, capacity):
         lh.check(gpu.lh_workspace_set_tokens(ws, ids.ctypes.data_as(lh.c_int64_p), length, count,
                                              None))
         d_q = lh.DeviceBuffer.from_array(q)
-        keys = lh.DeviceBuffer.from_array(kv_to_device_layout(kpm, capacity))
-        values = lh.DeviceBuffer.from_array(kv_to_device_layout(vpm, capacity))
+        keys = lh.DeviceBuffer.from_array(kv_to_device_layout(kpm, capacity, tail))
+        values = lh.DeviceBuffer.from_array(kv_to_device_layout(vpm, capacity, tail))
         out = lh.DeviceBuffer(count * 4096 * 4 + 16)
         lh.check(gpu.lh_memset_device(out.ptr, 0x5a, out.nbytes))
         lh.check(entry(d_q.ptr, keys.ptr, values.ptr, ws, out.ptr, None))

@@ -192,3 +192,28 @@ def test_mfma_layer_down_input_range(gpu, shift):
     rowmax = np.max(np.abs(wx), axis=1, keepdims=True)
     assert np.max(np.abs(gx - wx) / rowmax) < 1e-3
     assert np.median(np.abs(gx - wx) / np.maximum(np.abs(wx), 1e-30)) < 1e-5
+
+
+@pytest.mark.parametrize("tail", [np.inf, np.nan], ids=["inf", "nan"])
+@pytest.mark.parametrize("length,count,capacity", [(60, 3, 256), (256, 37, 4352),
+                                                   (4000, 256, 4352)])
+def test_attention_ignores_stale_cache_rows(gpu, tail, length, count, capacity):
+    """Cache rows past length+count hold what an earlier sequence or a failed
+    step left there (reset only rewinds the length). Both attention kernels
+    must give the same result as over a clean cache: the precise kernel
+    bitwise, the matrix-core kernel within its tolerance of the oracle (a
+    masked weight of 0 times a stale Inf would be NaN)."""
+    rng = np.random.default_rng(length + 3 * count)
+    total = length + count
+    q = (rng.normal(size=count * 4096) * 3).astype(np.float32)
+    kpm = rng.normal(size=(total, 1024)).astype(np.float32)
+    vpm = rng.normal(size=(total, 1024)).astype(np.float32)
+    clean = gpu_util.attention_on_device(gpu, gpu.lh_attention, q, kpm, vpm, length, count,
+                                         capacity)
+    stale = gpu_util.attention_on_device(gpu, gpu.lh_attention, q, kpm, vpm, length, count,
+                                         capacity, tail=tail)
+    assert np.array_equal(clean.view(np.uint32), stale.view(np.uint32))
+    got = gpu_util.attention_on_device(gpu, gpu.lh_attention_mfma, q, kpm, vpm, length, count,
+                                       capacity, tail=tail)
+    assert np.all(np.isfinite(got))
+    assert np.max(np.abs(got - clean)) < 2e-4

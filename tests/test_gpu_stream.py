@@ -11,8 +11,8 @@ holds the CPU oracle's streams (tests/golden/make_stream_golden.py):
   two schedules select the same 1024 tokens for this seed, so the GPU stream
   equals the reference-literal one throughout);
 - the MPS path (matrix-core prefill, tolerance-equal logits) must select the
-  same first token, and reports how long its stream agrees (1024 of 1024 on
-  the MI355X for this fixture).
+  same 1024 tokens as well: its prefill logits differ from the oracle's by
+  rounding only, and decode runs the bit-exact decode kernels.
 """
 import json
 import os
@@ -71,9 +71,9 @@ def test_precise_stream_matches_oracle_mirror(gpu):
           "reference-literal oracle" % (len(tokens), len(tokens), ref_agree))
 
 
-def test_mps_stream_first_token_and_agreement(gpu):
+def test_mps_stream_matches_oracle(gpu):
     fx = fixture()
     tokens = run_stream(fx, lh.PREFILL_MPS)
-    assert tokens[0] == fx["tokens_mirror"][0]
     n = agreement(tokens, fx["tokens_mirror"])
     print("MPS stream: first %d/%d tokens equal the mirror oracle" % (n, len(tokens)))
+    assert n == len(fx["tokens_mirror"]) == len(tokens)
