@@ -5,17 +5,26 @@ Workload (the one the headline metric is quoted on): the full random-init
 tied BF16 131072-token head), context capacity 4352, block 256. A seeded
 512-token prompt is prefilled in two 256-token chunks (prefill + append), then
 greedy decode runs for --steps tokens; a step is one decode call (all layers,
-the head, the 512 KiB logit copy and host greedy selection). value = decode
-tokens/s; prefill tokens/s is reported beside it.
+the head, the 512 KiB of logits reaching host memory and host greedy
+selection). value = decode tokens/s; prefill tokens/s is reported beside it,
+and the selected ids are compared with the oracle's token fixture after the
+timed calls (tokens_match_fixture = how many agree).
 
-Also measured, with HIP events on the stream the kernels run on: each fused
-decode operator at position 4351 launched over 26
-distinct layer weight/KV copies (3.0 GB + 0.9 GB, far beyond the 256 MB
-Infinity Cache), giving the FP8 matvec HBM bandwidth; `roofline` reports the
-dominant kernel (norm + gate/up + SiLU). The CPU baseline times the oracle's
-reference-literal schedule on the host cores over a bounded decode sample.
+Also measured, with HIP events on the stream the kernels run on:
+- each fused decode operator at position 4351 launched over 26 distinct layer
+  weight/KV copies (3.0 GB + 0.9 GB, far beyond the 256 MB Infinity Cache),
+  giving the FP8 matvec HBM bandwidth; `roofline` reports the dominant kernel
+  (norm + gate/up + SiLU);
+- decode attention at 550, 4352 and 16000 cached positions;
+- one FP8 linear 9216x3072 and one prefill layer (256 tokens after 4096);
+- the long-context prefix-reuse workload at capacity 17920 (16384-token
+  prompt, 8 turns of restore + append 64 + decode 128), with its ids compared
+  with the oracle's long fixture;
+- the CPU baseline: the oracle's reference-literal schedule on the host cores
+  over a bounded decode sample, with the host share of threads and with one.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
+       [--no-operators] [--no-long]
 """
 import argparse
 import ctypes
@@ -33,6 +42,16 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBPS = 8000.0
 METRIC = "decode tok/s + 256-chunk prefill tok/s @4352 ctx; FP8 matvec % HBM peak"
 
+# FP8 weight elements per layer and projection.
+FP8_WEIGHTS = {"qkv": 6144 * 3072, "o": 3072 * 4096, "gate_up": 2 * 9216 * 3072,
+               "down": 3072 * 9216}
+# Matrix-core prefill: activation planes per projection and their format
+# (exact hi/mid/lo BF16 split, or two FP16 planes with a power-of-two scale,
+# about 22 significant bits); FP8 weights convert exactly; FP32 accumulation.
+PREFILL_PLANES = {"qkv": (3, "3 x bf16 (exact split of fp32)"),
+                  "o": (3, "3 x bf16 (exact split of fp32)"),
+                  "gate_up": (2, "2 x fp16 + per-token power-of-two scale (~22 bits)"),
+                  "down": (2, "2 x fp16 + per-(token, K split) power-of-two scale (~22 bits)")}
 # Algorithmic bytes per decode-step launch (weights + activations read/written).
 FP8_BYTES = {"qkv_rope": 6144 * 3072, "o_residual": 3072 * 4096,
              "gateup_silu": 2 * 9216 * 3072, "down_residual": 3072 * 9216}
@@ -71,8 +90,8 @@ def parse():
     p.add_argument("--no-cpu-baseline", action="store_true")
     p.add_argument("--no-operators", action="store_true")
     p.add_argument("--op-repeats", type=int, default=4)
-    p.add_argument("--long", action="store_true",
-                   help="also run the long-context prefix-reuse workload (about a minute)")
+    p.add_argument("--no-long", action="store_true",
+                   help="skip the long-context prefix-reuse workload (about 10 s)")
     return p.parse_args()
 
 
@@ -154,6 +173,52 @@ def time_operators(lh, syn, seed, repeats):
     return result
 
 
+def time_attention(lh, syn, seed, lengths=(550, 4352, 16000), copies=16, repeats=4):
+    """Decode attention (one query token, all 32 heads) over L cached
+    positions, L = length + 1, at capacity 16448, rotating `copies` distinct
+    KV caches (2.2 GB): HIP-event time per call and K+V read GB/s (8192 B per
+    position)."""
+    lib = lh.lib()
+    capacity = 16448
+    kv_elems = 8 * capacity * 128
+    kv = lh.DeviceBuffer(2 * copies * kv_elems * 4)
+    fill = syn.normal_f32(seed, 9300, kv_elems)
+    for i in range(2 * copies):
+        lh.check(lib.lh_memcpy_htod(kv.ptr + i * kv_elems * 4, fill.ctypes.data, fill.nbytes))
+    q = lh.DeviceBuffer.from_array(syn.normal_f32(seed, 9301, 4096))
+    out = lh.DeviceBuffer(4096 * 4)
+    stream = lib.lh_stream_create()
+    ws = lib.lh_workspace_create(capacity, 1)
+    start, stop = lib.lh_event_create(), lib.lh_event_create()
+    result = {}
+    for L in lengths:
+        ids = np.array([7], np.int64)
+        lh.check(lib.lh_workspace_set_tokens(ws, ids.ctypes.data_as(lh.c_int64_p), L - 1, 1,
+                                             stream))
+
+        def launch(i):
+            keys = kv.ptr + 2 * (i % copies) * kv_elems * 4
+            lh.check(lib.lh_attention(q.ptr, keys, keys + kv_elems * 4, ws, out.ptr, stream),
+                     "attention")
+        for i in range(copies):
+            launch(i)
+        n = copies * repeats
+        lh.check(lib.lh_event_record(start, stream))
+        for i in range(n):
+            launch(i)
+        lh.check(lib.lh_event_record(stop, stream))
+        ms = ctypes.c_float()
+        lh.check(lib.lh_event_elapsed_ms(start, stop, ctypes.byref(ms)))
+        us = ms.value * 1e3 / n
+        result["L%d" % L] = {"us": round(us, 3),
+                             "GBps": round(8192 * L / (us * 1e-6) / 1e9, 1)}
+    for e in (start, stop):
+        lib.lh_event_destroy(e)
+    lib.lh_workspace_destroy(ws)
+    lib.lh_stream_destroy(stream)
+    return result
+
+
 def fp8_linear(lh, syn, seed, copies=16, repeats=8):
     """One FP8 linear y = s*(W.x), W 9216x3072 (28.3 MB), s = 0.0125, x ~ N(0,1),
     over `copies` distinct weight copies (453 MB, beyond the 256 MB Infinity
@@ -193,8 +258,9 @@ def fp8_linear(lh, syn, seed, copies=16, repeats=8):
 def prefill_layer(lh, syn, seed, repeats=8):
     """One decoder layer in chunked-prefill mode on the matrix-core path: 256
     tokens after a 4096-token prefix (KV N(0,1)), capacity 4352. HIP-event time
-    per layer; GEMM 59.59 GFLOP (x3 BF16 planes on the MFMA units) and
-    attention 17.72 GFLOP."""
+    per layer. Algorithmic work: GEMM 59.59 GFLOP and attention 17.72 GFLOP.
+    The MFMA units run each projection once per activation plane
+    (PREFILL_PLANES), so the GEMMs issue 135.3 GFLOP of MFMA work."""
     lib = lh.lib()
     capacity, length, count = 4352, 4096, 256
     host = syn.layer(seed, 0)
@@ -236,20 +302,34 @@ def prefill_layer(lh, syn, seed, repeats=8):
             total += ms.value
     us = total * 1e3 / repeats
     gemm, attn = 59.59e9, 17.72e9
+    mfma_gemm = 2 * count * sum(n * PREFILL_PLANES[k][0] for k, n in FP8_WEIGHTS.items())
     for e in (start, stop):
         lib.lh_event_destroy(e)
     lib.lh_workspace_destroy(ws)
     lib.lh_stream_destroy(stream)
     return {"tokens": count, "prefix": length, "us": round(us, 1),
             "algorithmic_TFLOPs": round((gemm + attn) / (us * 1e-6) / 1e12, 1),
-            "gemm_bf16_mfma_util_lower_bound": round(3 * gemm / (us * 1e-6) / 2.5e15, 4)}
+            "gemm_mfma_GFLOP": round(mfma_gemm / 1e9, 2),
+            "gemm_mfma_util_lower_bound": round(mfma_gemm / (us * 1e-6) / 2.5e15, 4)}
+
+
+def fixture_tokens(name):
+    """Selected ids of a committed oracle token fixture, or None."""
+    path = os.path.join(ROOT, "tests", "golden", name)
+    try:
+        with open(path) as f:
+            return json.load(f)
+    except (OSError, ValueError):
+        return None
 
 
 def long_context(lh, syn, Runtime, seed, prefill_mode):
     """Prefix-reuse workload at the 17920 profile: a 16384-token seeded prompt
     prefilled in 256-token chunks (checkpoint after 15872 tokens), then 8
     turns that restore the 15872-token prefix, append 64 new random tokens
-    and greedily decode 128 tokens (KV length 15937..16064)."""
+    and greedily decode 128 tokens (KV length 15937..16064). The selected ids
+    are compared with the oracle's (tests/golden/long_c17920_26layer.json)
+    after the timed calls."""
     rt = Runtime(seed=seed, layers=26, context=17920, block=256, prefill=prefill_mode,
                  strategy=lh.COMPACT_FP8_ARITHMETIC)
     try:
@@ -272,20 +352,28 @@ def long_context(lh, syn, Runtime, seed, prefill_mode):
         prefill_s = time.perf_counter() - t
         turns, append_s, decode_s, decode_device = 8, 0.0, 0.0, 0.0
         decoded = 0
+        tokens = []
         for turn in range(turns):
             rt.restore(checkpoint, copy=False)
             t = time.perf_counter()
             rt.append(syn.tokens(seed, 100 + turn, 64), copy=False)
             append_s += time.perf_counter() - t
             token = rt.greedy()
+            tokens.append(token)
             t = time.perf_counter()
             for _ in range(128):
                 rt.decode(token, copy=False)
                 decode_device += rt.last_device_ms()
                 token = rt.greedy()
+                tokens.append(token)
                 decoded += 1
             decode_s += time.perf_counter() - t
         rt.destroy_checkpoint(checkpoint)
+        fx = fixture_tokens("long_c17920_26layer.json")
+        match = None
+        if fx is not None and fx["seed"] == seed:
+            want = [t for turn in fx["turns"] for t in turn["tokens"]]
+            match = next((i for i in range(len(want)) if tokens[i] != want[i]), len(want))
         return {"workload": "16384-token prompt in 256-token chunks at context 17920; 8 turns "
                             "restore a 15872-token prefix, append 64 tokens, decode 128",
                 "prefill_tok_s": round(len(prompt) / prefill_s, 1),
@@ -293,18 +381,35 @@ def long_context(lh, syn, Runtime, seed, prefill_mode):
                 "turn_append_ms": round(append_s * 1e3 / turns, 3),
                 "decode_tok_s": round(decoded / decode_s, 2),
                 "decode_device_ms_per_step": round(decode_device / decoded, 4),
-                "kv_length": [keep + 65, keep + 64 + 128]}
+                "kv_length": [keep + 65, keep + 64 + 128],
+                "tokens_sha256": hashlib.sha256(np.array(tokens, np.int64).tobytes()
+                                                ).hexdigest()[:16],
+                "tokens_match_fixture": match, "tokens": len(tokens)}
     finally:
         rt.close()
 
 
-def cpu_baseline(syn, seed, budget_s=20.0):
-    """Oracle reference-literal decode of the full model on the host cores."""
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
+
+
+def cpu_baseline(syn, seed, budget_s=10.0):
+    """Oracle reference-literal decode of the full model on the host cores
+    (the reference's own arithmetic, restated in C, since the reference has no
+    CPU forward pass): with all of this process's host share of threads
+    (OMP_NUM_THREADS, else the affinity set) and with one thread, each over at
+    most `budget_s` seconds of steps."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib
     o = oracle_lib.load()
-    threads = int(os.environ.get("OMP_NUM_THREADS", "0") or 0)
-    o.orc_set_threads(threads if threads > 0 else min(16, os.cpu_count() or 1))
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or len(os.sched_getaffinity(0))
     t0 = time.time()
     layers = [syn.layer(seed, i) for i in range(26)]
     model = oracle_lib.HostModel(syn.embedding(seed).reshape(-1), syn.final_norm(seed), layers,
@@ -314,22 +419,36 @@ def cpu_baseline(syn, seed, budget_s=20.0):
     model.keys[:] = fill_k
     model.values[:] = fill_k[::-1]
     log("cpu baseline: model ready in %.1fs" % (time.time() - t0))
-    steps, elapsed, token = 0, 0.0, 7
-    while elapsed < budget_s and steps < 16:
-        t = time.time()
-        logits = model.forward(oracle_lib.REF, [token], prefix + steps)
-        elapsed += time.time() - t
-        token = int(np.argmax(logits))
-        steps += 1
-    return {"value": steps / elapsed, "unit": "tok/s", "cores": int(o.orc_get_threads()),
+
+    def run(threads, max_steps):
+        o.orc_set_threads(threads)
+        steps, elapsed, token = 0, 0.0, 7
+        while elapsed < budget_s and steps < max_steps:
+            t = time.time()
+            logits = model.forward(oracle_lib.REF, [token], prefix + steps)
+            elapsed += time.time() - t
+            token = int(np.argmax(logits))
+            steps += 1
+        return steps, steps / elapsed
+
+    steps, many = run(share, 16)
+    steps1, one = run(1, 4)
+    return {"value": many, "unit": "tok/s", "cores": share,
             "kind": "port",
-            "sample": "%d greedy decode steps of the 26-layer model at L=%d..%d, oracle "
-                      "reference-literal schedule (Kahan per 32 lanes), KV prefix seeded "
-                      "N(0,1)" % (steps, prefix + 1, prefix + steps)}
+            "sample": "%d greedy decode steps of the 26-layer model at L=%d..%d on %d threads "
+                      "(OMP_PROC_BIND=%s), oracle reference-literal schedule (Kahan per 32 "
+                      "lanes), KV prefix seeded N(0,1); %d steps on 1 thread" % (
+                          steps, prefix + 1, prefix + steps, share,
+                          os.environ.get("OMP_PROC_BIND"), steps1),
+            "value_1thread": one, "host_cpus": len(os.sched_getaffinity(0)),
+            "cpu_model": cpu_model()}
 
 
 def main():
     args = parse()
+    # Thread placement for the CPU baseline's OpenMP runtime (read when the
+    # oracle library loads).
+    os.environ.setdefault("OMP_PROC_BIND", "close")
     if args.gpus != 1:
         print("bench.py measures one MI355X: the library has no multi-GPU path "
               "(--gpus %d requested)" % args.gpus, file=sys.stderr)
@@ -408,6 +527,13 @@ def main():
         "tokens_sha256": hashlib.sha256(np.array(tokens, np.int64).tobytes()).hexdigest()[:16],
         "first_tokens": tokens[:8],
     }
+    fx = fixture_tokens("stream_c4352_26layer.json")
+    if fx is not None and fx["seed"] == args.seed:
+        want = fx["tokens_mirror"]
+        n = min(len(tokens), len(want))
+        out["tokens_match_fixture"] = next((i for i in range(n) if tokens[i] != want[i]), n)
+        out["tokens_compared"] = n
+    out["config"]["prefill_activations"] = {k: v[1] for k, v in PREFILL_PLANES.items()}
     if not args.no_operators:
         ops = time_operators(lh, syn, args.seed, args.op_repeats)
         fp8_us = sum(ops[k] for k in FP8_BYTES)
@@ -424,11 +550,13 @@ def main():
                            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": pmc_traffic(),
                            "bytes_per_launch": dom_bytes, "avg_us": round(ops[dom], 3)}
         log("operators (us): %s" % out["operators_us_at_pos4351"])
+        out["decode_attention"] = time_attention(lh, syn, args.seed)
+        log("decode attention: %s" % out["decode_attention"])
         out["fp8_linear_9216x3072"] = fp8_linear(lh, syn, args.seed)
         out["prefill_layer_256_after_4096"] = prefill_layer(lh, syn, args.seed)
         log("fp8 linear: %s" % out["fp8_linear_9216x3072"])
         log("prefill layer: %s" % out["prefill_layer_256_after_4096"])
-    if args.long:
+    if not args.no_long:
         out["long_context"] = long_context(lh, syn, Runtime, args.seed, prefill_mode)
         log("long context: %s" % out["long_context"])
     if not args.no_cpu_baseline:

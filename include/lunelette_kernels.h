@@ -176,19 +176,18 @@ int lh_st_inspect(const char *path, char *listing, size_t listing_capacity, char
 /* Bytes [offset, offset + bytes) of tensor `name`, bounds-checked. */
 int lh_st_read_tensor(const char *path, const char *name, uint64_t offset, void *out,
     size_t bytes, char *error, size_t capacity);
+/* FP8 admission of n codes under a per-tensor scale for a strategy
+ * (lunelette_metal_strategy), the check the runtime's upload applies to every
+ * FP8 tensor: the compact strategies follow lunelette_metal_weights_load_raw
+ * (src/metal_weights.c:174-231: positive, normal, BF16-exact scale; finite
+ * codes; normal nonzero products), RESIDENT_FP32 follows st_load_fp8
+ * (src/safetensors.c:521-548: positive finite scale; finite products).
+ * 0 admitted; -1 refused, with the first refused byte in the diagnostic. */
+int lh_fp8_admit(const uint8_t *codes, size_t n, float scale, int strategy, char *error,
+    size_t capacity);
 /* Container + tensor contract + scales of a model checkpoint; scales
  * [2 + 26*9] (slot order of src/metal_weights.h, 1 for non-FP8 slots) or NULL. */
 int lh_checkpoint_check(const char *path, float *scales, char *error, size_t capacity);
-
-/* ---- test seams (no counterpart in the reference ABI) ----
- * Host-forced failures equivalent to the reference's mocked command failures
- * (tests/test_metal.m:629-860), for state-machine tests on a live context:
- * what = 1 next execution fails before device work, 2 next execution yields a
- * nonfinite logit, 3 next checkpoint allocation fails. */
-struct lunelette_metal;
-int lunelette_metal_test_inject(struct lunelette_metal *context, int what);
-/* Overwrites one published host logit. */
-int lunelette_metal_test_set_logit(struct lunelette_metal *context, size_t index, float value);
 
 #ifdef __cplusplus
 }

@@ -34,10 +34,16 @@ typedef enum {
     LUNELETTE_METAL_PREFILL_CUSTOM = 1
 } lunelette_metal_prefill_mode;
 
-/* include/metal.h:24-28. RESIDENT_FP32 expands fl(dec*scale) to FP32 in HBM;
- * COMPACT_FP8_ARITHMETIC keeps FP8 codes and decodes in registers;
- * COMPACT_FP8_LOOKUP decodes through an unscaled 256-entry table. All three
- * give bitwise identical results. */
+/* include/metal.h:24-28. RESIDENT_FP32 stores the exact FP32 decode of every
+ * code in HBM; COMPACT_FP8_ARITHMETIC keeps FP8 codes and decodes in
+ * registers; COMPACT_FP8_LOOKUP decodes through an unscaled 256-entry table.
+ * All three multiply each row total by the per-tensor scale, so on weights
+ * every strategy admits they give bitwise identical results. Admission
+ * follows the reference per strategy: compact needs a positive, normal,
+ * BF16-exact scale, finite codes and normal nonzero products
+ * (src/metal_weights.c:174-231); resident needs a positive finite scale and
+ * finite products (st_load_fp8, src/safetensors.c:521-548), so subnormal
+ * scales and products load resident but not compact. */
 typedef enum {
     LUNELETTE_METAL_RESIDENT_FP32 = 0,
     LUNELETTE_METAL_COMPACT_FP8_ARITHMETIC = 1,

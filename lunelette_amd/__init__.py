@@ -15,6 +15,9 @@ import numpy as np
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIBRARY = os.path.join(_HERE, "liblunelette_hip.so")
+# The same objects plus the host-forced failure seams (csrc/lh_test_seams.h),
+# for the runtime's state-machine tests only.
+TEST_LIBRARY = os.path.join(_HERE, "liblunelette_hip_test.so")
 
 VOCAB = 131072
 HIDDEN = 3072
@@ -34,6 +37,7 @@ PATH_FUSED, PATH_LOOKUP, PATH_UNFUSED, PATH_RESIDENT, PATH_MFMA = range(5)
 OP_QKV_ROPE, OP_ATTENTION, OP_O_RESIDUAL, OP_GATEUP_SILU, OP_DOWN_RESIDUAL = range(5)
 
 _lib = None
+_test_lib = None
 
 c_size = ctypes.c_size_t
 c_void = ctypes.c_void_p
@@ -87,11 +91,34 @@ def _proto(lib, name, restype, *argtypes):
 def lib():
     """Load the built library (raises if it is missing)."""
     global _lib
-    if _lib is not None:
-        return _lib
-    if not os.path.exists(LIBRARY):
-        raise RuntimeError("liblunelette_hip.so is not built; run __graft_entry__.build()")
-    l = ctypes.CDLL(LIBRARY)
+    if _lib is None:
+        _lib = _load(LIBRARY)
+    return _lib
+
+
+def test_lib():
+    """Load the test build (the shipped library's objects plus the failure
+    seams of csrc/lh_test_seams.h); raises if it is missing."""
+    global _test_lib
+    if _test_lib is None:
+        l = _load(TEST_LIBRARY)
+        i, f = ctypes.c_int, ctypes.c_float
+        _proto(l, "lunelette_metal_test_inject", i, c_void, i)
+        _proto(l, "lunelette_metal_test_fail_after_layer", i, c_void, ctypes.c_uint32)
+        _proto(l, "lunelette_metal_test_set_epoch", i, c_void, ctypes.c_uint64)
+        _proto(l, "lunelette_metal_test_set_logit", i, c_void, c_size, f)
+        _proto(l, "lunelette_metal_test_fail_allocation", None, ctypes.c_uint)
+        _proto(l, "lunelette_metal_test_allocations", ctypes.c_uint)
+        _proto(l, "lunelette_metal_test_live_allocations", ctypes.c_long)
+        _test_lib = l
+    return _test_lib
+
+
+def _load(path):
+    if not os.path.exists(path):
+        raise RuntimeError("%s is not built; run __graft_entry__.build()" %
+                           os.path.basename(path))
+    l = ctypes.CDLL(path)
     i, v, f = ctypes.c_int, None, ctypes.c_float
     _proto(l, "lh_last_error", ctypes.c_char_p)
     _proto(l, "lh_device_count", i)
@@ -146,6 +173,7 @@ def lib():
     _proto(l, "lh_st_read_tensor", i, ctypes.c_char_p, ctypes.c_char_p, ctypes.c_uint64,
            c_void, c_size, ctypes.c_char_p, c_size)
     _proto(l, "lh_checkpoint_check", i, ctypes.c_char_p, c_float_p, ctypes.c_char_p, c_size)
+    _proto(l, "lh_fp8_admit", i, c_void, c_size, f, i, ctypes.c_char_p, c_size)
     err = ctypes.c_char_p
     _proto(l, "lunelette_metal_create", c_void, ctypes.c_char_p, err, c_size)
     _proto(l, "lunelette_metal_create_with_options", c_void, ctypes.c_char_p,
@@ -167,8 +195,6 @@ def lib():
     _proto(l, "lunelette_metal_checkpoint_destroy", v, c_void)
     _proto(l, "lunelette_metal_last_device_ms", i, c_void, c_float_p)
     _proto(l, "lunelette_metal_read_kv", i, c_void, c_size, i, c_size, c_size, c_float_p)
-    _proto(l, "lunelette_metal_test_inject", i, c_void, i)
-    _proto(l, "lunelette_metal_test_set_logit", i, c_void, c_size, f)
     _proto(l, "lunelette_select_greedy", i, c_float_p, c_int64_p, err, c_size)
     _proto(l, "lunelette_generate_with_logits", i, LOGITS_FN, c_void, c_int64_p, c_size,
            ctypes.POINTER(GenerationConfig), ctypes.POINTER(GenerationResult), err, c_size)
@@ -178,7 +204,6 @@ def lib():
     declare_session(l)
     declare_artifacts(l)
     declare_tokenizer(l)
-    _lib = l
     return l
 
 

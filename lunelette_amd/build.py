@@ -1,9 +1,13 @@
 """Builds the gfx950 library lunelette_amd/liblunelette_hip.so in-tree.
 
 HIP sources are compiled by hipcc for gfx950 only; the C host runtime by gcc
-against the ROCm headers; everything links into one shared library whose C-ABI
-is declared in include/*.h. Also builds the CPU oracle (test infrastructure)
-and, when the reference checkout is present, oracle/_ref.
+against the ROCm headers; everything links into one shared library that
+exports exactly the C-ABI declared in include/*.h (a linker version script
+keeps every internal symbol local). The same objects plus test_seams.c link
+into liblunelette_hip_test.so, which also exports the host-forced failure
+seams of csrc/lh_test_seams.h for the runtime's state-machine tests. Also
+builds the CPU oracle (test infrastructure) and, when the reference checkout
+is present, oracle/_ref.
 """
 import concurrent.futures
 import glob
@@ -16,6 +20,8 @@ PKG = os.path.join(ROOT, "lunelette_amd")
 CSRC = os.path.join(PKG, "csrc")
 OBJ = os.path.join(PKG, "_build")
 LIB = os.path.join(PKG, "liblunelette_hip.so")
+TEST_LIB = os.path.join(PKG, "liblunelette_hip_test.so")
+TEST_ONLY = ("test_seams.c",)
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 HIPCC = os.path.join(ROCM, "bin", "hipcc")
 
@@ -74,15 +80,44 @@ def kernel_resources(src):
     return kernels
 
 
+def declared_functions(headers):
+    """Function names (lunelette_* / lh_*) declared in the given C headers."""
+    import re
+    names = set()
+    for header in headers:
+        with open(header) as f:
+            text = re.sub(r"/\*.*?\*/", "", f.read(), flags=re.S)
+        for m in re.finditer(r"\b((?:lunelette|lh)_[a-z0-9_]+)\s*\(", text):
+            names.add(m.group(1))
+    return sorted(names - {"lunelette_logits_fn"})
+
+
+def _version_script(path, names):
+    with open(path, "w") as f:
+        f.write("{\n  global:\n")
+        for name in names:
+            f.write("    %s;\n" % name)
+        f.write("  local: *;\n};\n")
+
+
+def _link(out, objects, names, script):
+    _version_script(script, names)
+    tmp = out + ".tmp"
+    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objects +
+         ["-Wl,--version-script=" + script, "-lpthread", "-lm"])
+    os.replace(tmp, out)
+
+
 def build_library(jobs=8):
     os.makedirs(OBJ, exist_ok=True)
     sources = sorted(glob.glob(os.path.join(CSRC, "*.hip")) + glob.glob(os.path.join(CSRC, "*.c")))
     with concurrent.futures.ThreadPoolExecutor(max_workers=jobs) as pool:
         objects = list(pool.map(_compile, sources))
-    tmp = LIB + ".tmp"
-    _run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objects +
-         ["-lpthread", "-lm"])
-    os.replace(tmp, LIB)
+    shipped = [o for o, src in zip(objects, sources) if os.path.basename(src) not in TEST_ONLY]
+    abi = declared_functions(glob.glob(os.path.join(ROOT, "include", "*.h")))
+    _link(LIB, shipped, abi, os.path.join(OBJ, "exports.map"))
+    seams = declared_functions([os.path.join(CSRC, "lh_test_seams.h")])
+    _link(TEST_LIB, objects, abi + seams, os.path.join(OBJ, "exports_test.map"))
     return LIB
 
 

@@ -31,6 +31,60 @@ static int ok(hipError_t status, const char *what)
     return 0;
 }
 
+lh_allocation_counter lh_allocations;
+
+static int forced_failure(void)
+{
+    lh_allocations.count++;
+    return lh_allocations.fail_at && lh_allocations.count == lh_allocations.fail_at;
+}
+
+hipError_t lh_dev_malloc(void **ptr, size_t bytes)
+{
+    *ptr = NULL;
+    if (forced_failure()) {
+        return hipErrorOutOfMemory;
+    }
+    hipError_t status = hipMalloc(ptr, bytes ? bytes : 16);
+    if (status == hipSuccess) {
+        lh_allocations.live++;
+    } else {
+        *ptr = NULL;
+    }
+    return status;
+}
+
+hipError_t lh_host_malloc(void **ptr, size_t bytes, unsigned flags)
+{
+    *ptr = NULL;
+    if (forced_failure()) {
+        return hipErrorOutOfMemory;
+    }
+    hipError_t status = hipHostMalloc(ptr, bytes ? bytes : 16, flags);
+    if (status == hipSuccess) {
+        lh_allocations.live++;
+    } else {
+        *ptr = NULL;
+    }
+    return status;
+}
+
+void lh_dev_free(void *ptr)
+{
+    if (ptr) {
+        (void)hipFree(ptr);
+        lh_allocations.live--;
+    }
+}
+
+void lh_host_free(void *ptr)
+{
+    if (ptr) {
+        (void)hipHostFree(ptr);
+        lh_allocations.live--;
+    }
+}
+
 int lh_device_count(void)
 {
     int n = 0;
@@ -40,28 +94,23 @@ int lh_device_count(void)
 void *lh_device_alloc(size_t bytes)
 {
     void *p = NULL;
-    return ok(hipMalloc(&p, bytes ? bytes : 16), "hipMalloc") ? NULL : p;
+    return ok(lh_dev_malloc(&p, bytes), "hipMalloc") ? NULL : p;
 }
 
 void lh_device_free(void *d_ptr)
 {
-    if (d_ptr) {
-        (void)hipFree(d_ptr);
-    }
+    lh_dev_free(d_ptr);
 }
 
 void *lh_host_alloc_pinned(size_t bytes)
 {
     void *p = NULL;
-    return ok(hipHostMalloc(&p, bytes ? bytes : 16, hipHostMallocDefault), "hipHostMalloc") ?
-        NULL : p;
+    return ok(lh_host_malloc(&p, bytes, hipHostMallocDefault), "hipHostMalloc") ? NULL : p;
 }
 
 void lh_host_free_pinned(void *ptr)
 {
-    if (ptr) {
-        (void)hipHostFree(ptr);
-    }
+    lh_host_free(ptr);
 }
 
 int lh_memcpy_htod(void *d_dst, const void *src, size_t bytes)

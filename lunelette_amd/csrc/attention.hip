@@ -281,9 +281,8 @@ extern "C" int lh_launch_step_embed(const uint16_t* E, const float* yarn, int32_
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
-// The kernels read the step length from params (device memory, so a captured
-// graph replays with new lengths); `length` here must equal params->length and
-// only sizes the block grid.
+// The kernels read the step length from params (device memory); `length`
+// here must equal params->length and only sizes the block grid.
 extern "C" int lh_launch_attention(const float* q, const float* kcache_layer,
     const float* vcache_layer, const lh_step_params* params, uint32_t length, uint32_t count,
     uint32_t capacity, float* PM, float* PT, float* PA, float* out, hipStream_t s)
@@ -301,11 +300,6 @@ extern "C" int lh_launch_attention(const float* q, const float* kcache_layer,
 extern "C" uint32_t lh_attention_blocks(uint32_t length, uint32_t count)
 {
     return (length + count + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
-}
-
-extern "C" const void* lh_attention_blocks_kernel(void)
-{
-    return reinterpret_cast<const void*>(&k_attn_blocks);
 }
 
 extern "C" int lh_launch_embed(const uint16_t* E, const lh_step_params* params, uint32_t count,

@@ -20,7 +20,7 @@ static int check(hipError_t status, const char *what)
 static int alloc_device(void **out, size_t bytes, uint64_t *total)
 {
     *out = NULL;
-    if (check(hipMalloc(out, bytes ? bytes : 16), "workspace allocation")) {
+    if (check(lh_dev_malloc(out, bytes), "workspace allocation")) {
         return -1;
     }
     *total += bytes;
@@ -43,7 +43,7 @@ lh_workspace *lh_workspace_create(size_t capacity, size_t block)
     ws->block = block;
     const size_t nbc = capacity / LH_ATTN_BLOCK;
     const size_t B = block;
-    if (check(hipHostMalloc((void **)&ws->h_params, sizeof(lh_step_params), hipHostMallocDefault),
+    if (check(lh_host_malloc((void **)&ws->h_params, sizeof(lh_step_params), hipHostMallocDefault),
             "workspace pinned parameters") ||
         alloc_device((void **)&ws->d_params, sizeof(lh_step_params), &ws->bytes) ||
         alloc_device((void **)&ws->d_q, B * LH_QUERY * sizeof(float), &ws->bytes) ||
@@ -74,13 +74,9 @@ void lh_workspace_destroy(lh_workspace *ws)
         ws->d_qraw, ws->d_kraw, ws->d_vraw, ws->d_PM, ws->d_PT, ws->d_PA,
         ws->d_split, ws->d_gemm, ws->d_yarn};
     for (size_t i = 0; i < sizeof device / sizeof device[0]; i++) {
-        if (device[i]) {
-            (void)hipFree(device[i]);
-        }
+        lh_dev_free(device[i]);
     }
-    if (ws->h_params) {
-        (void)hipHostFree(ws->h_params);
-    }
+    lh_host_free(ws->h_params);
     free(ws);
 }
 

@@ -37,9 +37,8 @@ int lh_launch_attention(const float *q, const float *kcache_layer, const float *
 int lh_launch_attention_mfma(const float *q, const float *kcache_layer, const float *vcache_layer,
     const lh_step_params *params, uint32_t length, uint32_t count, uint32_t capacity, float *PM,
     float *PT, float *PA, float *out, uint16_t *xs, uint32_t xs_tokens, hipStream_t s);
-/* Block-grid width of the attention kernel, and its function (graph updates). */
+/* Block-grid width of the attention kernel. */
 uint32_t lh_attention_blocks(uint32_t length, uint32_t count);
-const void *lh_attention_blocks_kernel(void);
 int lh_launch_embed(const uint16_t *E, const lh_step_params *params, uint32_t count, float *x,
     hipStream_t s);
 /* One decode token: writes params (length, count 1, id, qfactor, cos/sin of
@@ -60,6 +59,36 @@ int lh_launch_expf(const float *x, float *out, size_t n, hipStream_t s);
 
 /* Thread-local diagnostic shared by the C ABI layers. */
 void lh_set_error(const char *format, ...);
+
+/* Every device and pinned-host allocation of the library goes through these
+ * (host_util.c). They count allocations and frees, and fail the fail_at-th
+ * allocation after the counter was armed: the host-forced allocation failure
+ * of the reference's tests (tests/test_metal.m:888-954). Only the test-seam
+ * library (test_seams.c, not part of the shipped library) arms it. */
+hipError_t lh_dev_malloc(void **ptr, size_t bytes);
+hipError_t lh_host_malloc(void **ptr, size_t bytes, unsigned flags);
+void lh_dev_free(void *ptr);
+void lh_host_free(void *ptr);
+typedef struct {
+    unsigned fail_at;   /* 1-based index of the allocation to fail; 0 never */
+    unsigned count;     /* allocations since the counter was armed */
+    long live;          /* allocations not yet freed */
+} lh_allocation_counter;
+extern lh_allocation_counter lh_allocations;
+
+/* Host-forced execution faults of one runtime context (runtime.c), set only
+ * by the test-seam library: the analogue of the reference's mocked command
+ * failures (tests/test_metal.m:629-860). */
+enum {
+    LH_FAULT_BEFORE_DEVICE = 1,    /* next execution fails before any device work */
+    LH_FAULT_NONFINITE = 2,        /* next execution publishes an Inf logit */
+    LH_FAULT_CHECKPOINT_ALLOC = 3, /* next checkpoint allocation fails */
+    LH_FAULT_AFTER_LAYER = 4,      /* next execution fails after layer arg's kernels ran */
+    LH_FAULT_EPOCH = 5             /* checkpoint epoch counter set to arg */
+};
+struct lunelette_metal;
+int lh_runtime_fault(struct lunelette_metal *context, int kind, uint64_t arg);
+int lh_runtime_set_logit(struct lunelette_metal *context, size_t index, float value);
 
 #ifdef __cplusplus
 }

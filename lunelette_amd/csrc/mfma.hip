@@ -658,8 +658,8 @@ extern "C" int lh_mfma_prepare(lh_workspace* ws)
     const size_t B = padded_block(ws);
     const size_t split_bytes = plane_bytes(B) + (1 + DOWN_SPLITS) * B * sizeof(float);
     const size_t gemm_bytes = partial_floats((uint32_t)B) * sizeof(float);
-    if (hipMalloc((void**)&ws->d_split, split_bytes) != hipSuccess ||
-        hipMalloc((void**)&ws->d_gemm, gemm_bytes) != hipSuccess) {
+    if (lh_dev_malloc((void**)&ws->d_split, split_bytes) != hipSuccess ||
+        lh_dev_malloc((void**)&ws->d_gemm, gemm_bytes) != hipSuccess) {
         lh_set_error("MFMA workspace allocation failed");
         return -1;
     }

@@ -33,19 +33,6 @@ struct lunelette_metal_checkpoint {
     float logits[LH_VOCAB];
 };
 
-/* With graphs enabled, one-token steps replay a HIP graph per layer path:
- * embedding, every layer and the head captured once. Replays read ids, positions, rotations and the
- * context length from the device step record; only the attention block grid
- * changes, when the context crosses a 64-position boundary, and is updated in
- * place on the instantiated graph. */
-typedef struct {
-    hipGraph_t graph;
-    hipGraphExec_t exec;
-    hipGraphNode_t attention[LH_LAYERS];
-    uint32_t nodes;           /* attention block nodes found in the capture */
-    uint32_t blocks;          /* grid width the instantiated graph holds */
-} decode_graph;
-
 typedef struct lh_runtime {
     lunelette_metal_limits limits;
     lunelette_metal_prefill_mode prefill_mode;
@@ -71,9 +58,10 @@ typedef struct lh_runtime {
     bool valid, endpoint_logits_valid;
     uint64_t identity, checkpoint_epoch;
     lunelette_metal_checkpoint *active_checkpoint;
-    int inject;               /* test seam, see lunelette_metal_test_inject */
-    bool graphs;              /* replay one-token steps as HIP graphs */
-    decode_graph decode[5];   /* indexed by LH_PATH_* */
+    struct {                  /* host-forced faults (lh_runtime_fault) */
+        bool before_device, nonfinite, checkpoint_alloc;
+        uint32_t after_layer;     /* fail after layer after_layer - 1; 0 off */
+    } fault;
 } lh_runtime;
 
 struct lunelette_metal {
@@ -137,24 +125,10 @@ static void destroy_runtime(lh_runtime *rt)
     }
     void *device[] = {rt->d_weights, rt->d_embedding, rt->d_norms, rt->d_kv, rt->d_x};
     for (size_t i = 0; i < sizeof device / sizeof device[0]; i++) {
-        if (device[i]) {
-            (void)hipFree(device[i]);
-        }
+        lh_dev_free(device[i]);
     }
-    if (rt->h_logits) {
-        (void)hipHostFree(rt->h_logits);
-    }
-    if (rt->h_nonfinite) {
-        (void)hipHostFree((void *)rt->h_nonfinite);
-    }
-    for (size_t i = 0; i < sizeof rt->decode / sizeof rt->decode[0]; i++) {
-        if (rt->decode[i].exec) {
-            (void)hipGraphExecDestroy(rt->decode[i].exec);
-        }
-        if (rt->decode[i].graph) {
-            (void)hipGraphDestroy(rt->decode[i].graph);
-        }
-    }
+    lh_host_free(rt->h_logits);
+    lh_host_free((void *)rt->h_nonfinite);
     lh_workspace_destroy(rt->ws);
     if (rt->started) {
         (void)hipEventDestroy(rt->started);
@@ -179,14 +153,19 @@ static int hip_ok(hipError_t status, const char *what, char *error, size_t capac
     return 0;
 }
 
-/* Compact admission domain (src/metal_weights.c:174-231): the scale must be
- * positive, FP32-normal and BF16-exact; every code finite; every nonzero
- * reconstructed product normal. Builds the 256-entry allowed table. */
-static int fp8_admission_table(float scale, unsigned char allowed[256])
+/* FP8 admission, per strategy. Compact (src/metal_weights.c:174-231): the
+ * scale must be positive, FP32-normal and BF16-exact; every code finite; every
+ * nonzero reconstructed product normal. Resident (st_load_fp8,
+ * src/safetensors.c:521-548): the scale positive and finite; every product
+ * fl(dec * scale) finite, so NaN codes and overflow are refused while
+ * subnormal scales and products are accepted. Builds the 256-entry allowed
+ * table; -1 when the scale itself is refused. */
+static int fp8_admission_table(float scale, bool resident, unsigned char allowed[256])
 {
     uint32_t bits;
     memcpy(&bits, &scale, sizeof bits);
-    if (!(scale > 0) || !isnormal(scale) || (bits & 0xffffu)) {
+    if (resident ? !(scale > 0) || !isfinite(scale) :
+            !(scale > 0) || !isnormal(scale) || (bits & 0xffffu)) {
         return -1;
     }
     for (unsigned code = 0; code < 256; code++) {
@@ -197,7 +176,36 @@ static int fp8_admission_table(float scale, unsigned char allowed[256])
         }
         float magnitude = e == 0 ? ldexpf((float)f, -9) : ldexpf((float)(8 + f), (int)e - 10);
         float product = magnitude * scale;
-        allowed[code] = isfinite(product) && (magnitude == 0 || isnormal(product));
+        allowed[code] = isfinite(product) && (resident || magnitude == 0 || isnormal(product));
+    }
+    return 0;
+}
+
+int lh_fp8_admit(const uint8_t *codes, size_t n, float scale, int strategy, char *error,
+    size_t capacity)
+{
+    if (!codes || (strategy != LUNELETTE_METAL_RESIDENT_FP32 &&
+            strategy != LUNELETTE_METAL_COMPACT_FP8_ARITHMETIC &&
+            strategy != LUNELETTE_METAL_COMPACT_FP8_LOOKUP)) {
+        report(error, capacity, "%sadmission needs codes and a strategy", NULL);
+        return -1;
+    }
+    const bool resident = strategy == LUNELETTE_METAL_RESIDENT_FP32;
+    unsigned char allowed[256];
+    if (fp8_admission_table(scale, resident, allowed)) {
+        report(error, capacity, resident ? "%sscale must be positive and finite" :
+            "%sscale must be positive FP32-normal widened BF16", NULL);
+        return -1;
+    }
+    for (size_t i = 0; i < n; i++) {
+        if (!allowed[codes[i]]) {
+            if (error && capacity) {
+                snprintf(error, capacity, "byte %zu code 0x%02x: %s", i, codes[i], resident ?
+                    "NaN or overflowing reconstructed product" :
+                    "NaN or non-normal/overflow reconstructed product");
+            }
+            return -1;
+        }
     }
     return 0;
 }
@@ -298,15 +306,17 @@ static int source_read(weight_source *src, uint32_t slot, uint64_t offset, void 
 
 /* FP8 tensor `tensor` of n codes: admit, then store the codes (compact) or
  * their exact FP32 decode (resident); both strategies multiply the row total
- * by the per-tensor scale, so their results are bitwise identical. */
+ * by the per-tensor scale, so on what both admit their results are bitwise
+ * identical. */
 static int upload_fp8(uploader *up, weight_source *src, uint32_t tensor, float scale, size_t n,
     bool resident, void *dst, char *error, size_t capacity)
 {
     unsigned char allowed[256];
-    if (fp8_admission_table(scale, allowed)) {
+    if (fp8_admission_table(scale, resident, allowed)) {
         if (error && capacity) {
-            snprintf(error, capacity, "compact tensor %u: scale must be positive FP32-normal "
-                "widened BF16", tensor);
+            snprintf(error, capacity, resident ?
+                "resident tensor %u: scale must be positive and finite" :
+                "compact tensor %u: scale must be positive FP32-normal widened BF16", tensor);
         }
         return -1;
     }
@@ -331,9 +341,11 @@ static int upload_fp8(uploader *up, weight_source *src, uint32_t tensor, float s
         for (size_t i = 0; i < m; i++) {
             if (!allowed[dst_codes[i]]) {
                 if (error && capacity) {
-                    snprintf(error, capacity, "compact tensor %u byte %zu code 0x%02x: NaN or "
-                        "non-normal/overflow reconstructed product", tensor, offset + i,
-                        dst_codes[i]);
+                    snprintf(error, capacity, resident ?
+                        "resident tensor %u byte %zu code 0x%02x: NaN or overflowing "
+                        "reconstructed product" :
+                        "compact tensor %u byte %zu code 0x%02x: NaN or non-normal/overflow "
+                        "reconstructed product", tensor, offset + i, dst_codes[i]);
                 }
                 free(codes);
                 return -1;
@@ -408,11 +420,6 @@ static lunelette_metal *build_runtime(weight_source *src, uint32_t layers,
     rt->prefill_mode = selected.prefill;
     rt->strategy = selected.strategy;
     rt->layers = layers;
-    /* LUNELETTE_HIP_GRAPHS=1 replays one-token steps as a HIP graph (opt-in:
-     * on MI355X it measures level with kernel-by-kernel launches, and
-     * rocprofv3 kernel tracing of graph replays has crashed the host process). */
-    const char *graphs = getenv("LUNELETTE_HIP_GRAPHS");
-    rt->graphs = graphs && strcmp(graphs, "1") == 0;
     const bool resident = selected.strategy == LUNELETTE_METAL_RESIDENT_FP32;
     const size_t C = resolved.context, B = resolved.block;
     const uint64_t fp8_bytes = layer_fp8_bytes() * rt->layers;
@@ -439,20 +446,22 @@ static lunelette_metal *build_runtime(weight_source *src, uint32_t layers,
         snprintf(error, capacity, "workspace: %s", lh_last_error());
         goto failure;
     }
-    if (hip_ok(hipMalloc(&rt->d_weights, weight_bytes), "weight allocation", error, capacity) ||
-        hip_ok(hipMalloc((void **)&rt->d_embedding, embedding_bytes), "embedding allocation",
+    if (hip_ok(lh_dev_malloc(&rt->d_weights, weight_bytes), "weight allocation", error,
+            capacity) ||
+        hip_ok(lh_dev_malloc((void **)&rt->d_embedding, embedding_bytes), "embedding allocation",
             error, capacity) ||
-        hip_ok(hipMalloc((void **)&rt->d_norms, norm_bytes), "norm allocation", error, capacity) ||
-        hip_ok(hipMalloc((void **)&rt->d_kv, kv_bytes), "KV allocation", error, capacity) ||
-        hip_ok(hipMalloc((void **)&rt->d_x, B * LH_HIDDEN * sizeof(float)), "scratch allocation",
-            error, capacity) ||
+        hip_ok(lh_dev_malloc((void **)&rt->d_norms, norm_bytes), "norm allocation", error,
+            capacity) ||
+        hip_ok(lh_dev_malloc((void **)&rt->d_kv, kv_bytes), "KV allocation", error, capacity) ||
+        hip_ok(lh_dev_malloc((void **)&rt->d_x, B * LH_HIDDEN * sizeof(float)),
+            "scratch allocation", error, capacity) ||
         /* The head kernel writes the logits straight into coherent pinned
          * memory: no device-to-host copy after the step. */
-        hip_ok(hipHostMalloc((void **)&rt->h_logits, LH_VOCAB * sizeof(float),
+        hip_ok(lh_host_malloc((void **)&rt->h_logits, LH_VOCAB * sizeof(float),
             hipHostMallocMapped | hipHostMallocCoherent), "pinned logits", error, capacity) ||
         hip_ok(hipHostGetDevicePointer((void **)&rt->d_logits, rt->h_logits, 0),
             "mapped logits", error, capacity) ||
-        hip_ok(hipHostMalloc((void **)&rt->h_nonfinite, 64,
+        hip_ok(lh_host_malloc((void **)&rt->h_nonfinite, 64,
             hipHostMallocMapped | hipHostMallocCoherent), "pinned flag", error, capacity) ||
         hip_ok(hipHostGetDevicePointer((void **)&rt->d_nonfinite, (void *)rt->h_nonfinite, 0),
             "mapped flag", error, capacity)) {
@@ -468,8 +477,8 @@ static lunelette_metal *build_runtime(weight_source *src, uint32_t layers,
      * post_norm, gate, up, down}. */
     up.stream = rt->stream;
     for (int k = 0; k < 2; k++) {
-        if (hip_ok(hipHostMalloc(&up.stage[k], STAGE_BYTES, hipHostMallocDefault), "pinned staging",
-                error, capacity) ||
+        if (hip_ok(lh_host_malloc(&up.stage[k], STAGE_BYTES, hipHostMallocDefault),
+                "pinned staging", error, capacity) ||
             hip_ok(hipEventCreate(&up.done[k]), "staging event", error, capacity)) {
             goto failure;
         }
@@ -525,7 +534,7 @@ static lunelette_metal *build_runtime(weight_source *src, uint32_t layers,
         goto failure;
     }
     for (int k = 0; k < 2; k++) {
-        (void)hipHostFree(up.stage[k]);
+        lh_host_free(up.stage[k]);
         (void)hipEventDestroy(up.done[k]);
         up.stage[k] = NULL;
         up.done[k] = NULL;
@@ -558,9 +567,7 @@ failure:
             (void)hipEventSynchronize(up.done[k]);
             (void)hipEventDestroy(up.done[k]);
         }
-        if (up.stage[k]) {
-            (void)hipHostFree(up.stage[k]);
-        }
+        lh_host_free(up.stage[k]);
     }
     destroy_runtime(rt);
     return NULL;
@@ -721,94 +728,14 @@ static int launch_step(lh_runtime *rt, size_t count, int path, int embed, hipStr
         if (rc) {
             return -1;
         }
+        if (rt->fault.after_layer == l + 1) {
+            rt->fault.after_layer = 0;
+            lh_set_error("injected launch failure after layer %u", l);
+            return -1;
+        }
     }
     return lh_head_forward_checked(rt->d_embedding, rt->d_norms + 2ull * rt->layers * LH_HIDDEN,
         rt->d_x + (count - 1) * LH_HIDDEN, rt->d_logits, rt->d_nonfinite, s);
-}
-
-static int graph_fail(hipError_t status, const char *what)
-{
-    lh_set_error("decode graph %s: %s", what, hipGetErrorString(status));
-    return -1;
-}
-
-static int capture_step(lh_runtime *rt, decode_graph *g, int path, uint32_t blocks, hipStream_t s)
-{
-    hipError_t status = hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal);
-    if (status != hipSuccess) {
-        return graph_fail(status, "capture");
-    }
-    const int failed = launch_step(rt, 1, path, 1, s);
-    hipGraph_t graph = NULL;
-    status = hipStreamEndCapture(s, &graph);
-    if (failed || status != hipSuccess || !graph) {
-        if (graph) {
-            (void)hipGraphDestroy(graph);
-        }
-        return failed ? -1 : graph_fail(status, "capture end");
-    }
-    size_t count = 0;
-    hipGraphNode_t *nodes = NULL;
-    status = hipGraphGetNodes(graph, NULL, &count);
-    if (status == hipSuccess && count) {
-        nodes = malloc(count * sizeof *nodes);
-        status = nodes ? hipGraphGetNodes(graph, nodes, &count) : hipErrorOutOfMemory;
-    }
-    const void *kernel = lh_attention_blocks_kernel();
-    g->nodes = 0;
-    for (size_t i = 0; status == hipSuccess && i < count; i++) {
-        hipGraphNodeType type;
-        status = hipGraphNodeGetType(nodes[i], &type);
-        if (status != hipSuccess || type != hipGraphNodeTypeKernel) {
-            continue;
-        }
-        hipKernelNodeParams params;
-        status = hipGraphKernelNodeGetParams(nodes[i], &params);
-        if (status == hipSuccess && params.func == kernel && g->nodes < LH_LAYERS) {
-            g->attention[g->nodes++] = nodes[i];
-        }
-    }
-    free(nodes);
-    if (status == hipSuccess && g->nodes != rt->layers) {
-        status = hipErrorInvalidValue;
-    }
-    if (status == hipSuccess) {
-        status = hipGraphInstantiate(&g->exec, graph, NULL, NULL, 0);
-    }
-    if (status != hipSuccess) {
-        g->exec = NULL;
-        (void)hipGraphDestroy(graph);
-        return graph_fail(status, "instantiate");
-    }
-    g->graph = graph;
-    g->blocks = blocks;
-    return 0;
-}
-
-static int graph_step(lh_runtime *rt, int path, hipStream_t s)
-{
-    decode_graph *g = &rt->decode[path];
-    const uint32_t blocks = lh_attention_blocks((uint32_t)rt->length, 1);
-    if (!g->exec) {
-        if (capture_step(rt, g, path, blocks, s)) {
-            return -1;
-        }
-    } else if (g->blocks != blocks) {
-        for (uint32_t i = 0; i < g->nodes; i++) {
-            hipKernelNodeParams params;
-            hipError_t status = hipGraphKernelNodeGetParams(g->attention[i], &params);
-            if (status == hipSuccess) {
-                params.gridDim.x = blocks;
-                status = hipGraphExecKernelNodeSetParams(g->exec, g->attention[i], &params);
-            }
-            if (status != hipSuccess) {
-                return graph_fail(status, "update");
-            }
-        }
-        g->blocks = blocks;
-    }
-    hipError_t status = hipGraphLaunch(g->exec, s);
-    return status == hipSuccess ? 0 : graph_fail(status, "launch");
 }
 
 static int execute(lunelette_metal *context, const int64_t *ids, size_t count, bool prefill,
@@ -842,15 +769,14 @@ static int execute(lunelette_metal *context, const int64_t *ids, size_t count, b
     rt->active_checkpoint = NULL;
     rt->endpoint_logits_valid = false;
     rt->valid = false;
-    if (rt->inject == 1) {
-        rt->inject = 0;
+    if (rt->fault.before_device) {
+        rt->fault.before_device = false;
         snprintf(error, capacity, "execution failed; reset required: injected launch failure");
         return -1;
     }
     hipStream_t s = rt->stream;
-    /* A decode step writes its record on the device (no host upload), except
-     * under graph replay, whose captured gather reads the uploaded record. */
-    const int device_record = count == 1 && !rt->graphs;
+    /* A decode step writes its record on the device (no host upload). */
+    const int device_record = count == 1;
     if (!device_record && lh_workspace_set_tokens(rt->ws, ids, rt->length, count, s)) {
         snprintf(error, capacity, "step parameters failed; reset required: %s", lh_last_error());
         return -1;
@@ -862,8 +788,7 @@ static int execute(lunelette_metal *context, const int64_t *ids, size_t count, b
     int failed = hipEventRecord(rt->started, s) != hipSuccess ||
         (device_record &&
             lh_workspace_set_decode(rt->ws, rt->d_embedding, ids[0], rt->length, rt->d_x, s)) ||
-        (count == 1 && rt->graphs ? graph_step(rt, path, s) :
-            launch_step(rt, count, path, !device_record, s)) ||
+        launch_step(rt, count, path, !device_record, s) ||
         hipEventRecord(rt->finished, s) != hipSuccess;
     hipError_t status = hipStreamSynchronize(s);
     if (failed || status != hipSuccess) {
@@ -874,8 +799,8 @@ static int execute(lunelette_metal *context, const int64_t *ids, size_t count, b
     if (hipEventElapsedTime(&rt->last_ms, rt->started, rt->finished) != hipSuccess) {
         rt->last_ms = -1.0f;
     }
-    if (rt->inject == 2) {
-        rt->inject = 0;
+    if (rt->fault.nonfinite) {
+        rt->fault.nonfinite = false;
         rt->h_logits[LH_VOCAB - 1] = INFINITY;
         *rt->h_nonfinite = 1;
     }
@@ -934,8 +859,8 @@ int lunelette_metal_checkpoint_create(lunelette_metal *context,
         return -1;
     }
     lunelette_metal_checkpoint *saved = NULL;
-    if (rt->inject == 3) {
-        rt->inject = 0;
+    if (rt->fault.checkpoint_alloc) {
+        rt->fault.checkpoint_alloc = false;
     } else {
         saved = malloc(sizeof *saved);
     }
@@ -1019,21 +944,39 @@ int lunelette_metal_read_kv(const lunelette_metal *context, size_t layer, int ki
     return 0;
 }
 
-/* Test seam (no counterpart in the reference ABI; mirrors the reference's
- * host-forced failures in tests/test_metal.m:629-860): 1 = next execution
- * fails before device work, 2 = next execution yields a nonfinite logit,
- * 3 = next checkpoint allocation fails. */
-int lunelette_metal_test_inject(lunelette_metal *context, int what)
+/* Host-forced faults (lh_internal.h). Only the test-seam library calls these;
+ * the shipped library exports neither. */
+int lh_runtime_fault(lunelette_metal *context, int kind, uint64_t arg)
 {
-    if (!context || !context->rt || what < 0 || what > 3) {
+    lh_runtime *rt = context ? context->rt : NULL;
+    if (!rt) {
         return -1;
     }
-    context->rt->inject = what;
-    return 0;
+    switch (kind) {
+    case LH_FAULT_BEFORE_DEVICE:
+        rt->fault.before_device = true;
+        return 0;
+    case LH_FAULT_NONFINITE:
+        rt->fault.nonfinite = true;
+        return 0;
+    case LH_FAULT_CHECKPOINT_ALLOC:
+        rt->fault.checkpoint_alloc = true;
+        return 0;
+    case LH_FAULT_AFTER_LAYER:
+        if (arg >= rt->layers) {
+            return -1;
+        }
+        rt->fault.after_layer = (uint32_t)arg + 1;
+        return 0;
+    case LH_FAULT_EPOCH:
+        rt->checkpoint_epoch = arg;
+        return 0;
+    default:
+        return -1;
+    }
 }
 
-/* Test seam: overwrite the published host logits (checkpoint/NaN tests). */
-int lunelette_metal_test_set_logit(lunelette_metal *context, size_t index, float value)
+int lh_runtime_set_logit(lunelette_metal *context, size_t index, float value)
 {
     if (!context || !context->rt || index >= LH_VOCAB) {
         return -1;

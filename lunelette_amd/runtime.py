@@ -9,7 +9,7 @@ import ctypes
 import numpy as np
 
 from . import (COMPACT_FP8_ARITHMETIC, Limits, Memory, Options, PREFILL_MPS, SyntheticConfig,
-               VOCAB, c_float_p, c_int64_p, lib)
+               VOCAB, c_float_p, c_int64_p, lib, test_lib)
 
 
 class RuntimeError_(RuntimeError):
@@ -19,11 +19,12 @@ class RuntimeError_(RuntimeError):
 class Runtime:
     """A runtime context over the seeded synthetic model, or over the FP8
     safetensors checkpoint at `path` (lunelette_metal_create_configured; all
-    26 layers)."""
+    26 layers). seams=True creates it in the test build of the library, whose
+    host-forced failure seams the inject/fail_* methods drive."""
 
     def __init__(self, seed=1, layers=26, context=4352, block=256, prefill=PREFILL_MPS,
-                 strategy=COMPACT_FP8_ARITHMETIC, path=None):
-        self._lib = lib()
+                 strategy=COMPACT_FP8_ARITHMETIC, path=None, seams=False):
+        self._lib = test_lib() if seams else lib()
         self._err = ctypes.create_string_buffer(512)
         opts = Options(prefill, strategy)
         lim = Limits(context, block)
@@ -136,10 +137,25 @@ class Runtime:
         return out.reshape(count, 1024)
 
     def inject(self, what):
-        self._lib.lunelette_metal_test_inject(self.handle, what)
+        """Test build only: 1 fail before device work, 2 Inf logit, 3 checkpoint
+        allocation failure (next call)."""
+        if self._lib.lunelette_metal_test_inject(self.handle, what):
+            raise RuntimeError_("inject rejected")
+
+    def fail_after_layer(self, layer):
+        """Test build only: the next execution fails after `layer`'s kernels."""
+        if self._lib.lunelette_metal_test_fail_after_layer(self.handle, layer):
+            raise RuntimeError_("fail_after_layer rejected")
+
+    def set_epoch(self, epoch):
+        """Test build only: sets the checkpoint epoch counter."""
+        if self._lib.lunelette_metal_test_set_epoch(self.handle, epoch):
+            raise RuntimeError_("set_epoch rejected")
 
     def set_logit(self, index, value):
-        self._lib.lunelette_metal_test_set_logit(self.handle, index, value)
+        """Test build only: overwrites one published host logit."""
+        if self._lib.lunelette_metal_test_set_logit(self.handle, index, value):
+            raise RuntimeError_("set_logit rejected")
 
     @property
     def last_error(self):

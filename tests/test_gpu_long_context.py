@@ -1,0 +1,126 @@
+"""Long-context prefix reuse at the 17920 capacity profile on the GPU.
+
+The workload of the benchmark's long line: a 16384-token seeded prompt
+prefilled in 256-token chunks with a checkpoint at 15872, then turns that
+restore the 15872-token prefix, append 64 ids and decode greedily. The
+reference's own planner stops at 4352 (src/metal_plan.h:39-41) and its long
+schedules at 4352 (tests/long_context/long/schedule.py:11-47), so this profile
+is pinned by the oracle alone, through fixtures written offline by
+tests/golden/make_long_golden.py (device-mirror schedule):
+- matrix-core attention against the oracle at 8192- and 16128-token prefixes
+  with 64 and 256 query rows (the KV-split launches of 16 and 4 splits), to
+  the 2e-4 tolerance of the shorter cases;
+- a 2-layer model through every call of the workload (64 prompt chunks,
+  restore, append 64, 8 decodes): the precise path's logits equal the
+  fixture's bit for bit (SHA-256 per call); the matrix-core path's logits stay
+  within 1e-3 of each call's logit range of them and select the same ids;
+- the 26-layer benchmark workload (8 turns of append 64 + 128 decodes): the
+  precise path selects the fixture's 8 x 129 ids, and so does the matrix-core
+  path.
+"""
+import hashlib
+import json
+import os
+
+import numpy as np
+import pytest
+
+import lunelette_amd as lh
+from lunelette_amd import synthetic as syn
+from lunelette_amd.runtime import Runtime
+
+import gpu_util
+import oracle_lib
+from oracle_lib import MIRROR
+
+pytestmark = pytest.mark.gpu
+GOLDEN = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
+CONTEXT = 17920
+
+
+def fixture(name):
+    path = os.path.join(GOLDEN, name)
+    if not os.path.exists(path):
+        pytest.skip("fixture %s not generated (tests/golden/make_long_golden.py)" % name)
+    with open(path) as f:
+        return json.load(f)
+
+
+@pytest.mark.parametrize("length,count", [(8192, 64), (8192, 256), (16128, 64), (16128, 256)])
+def test_attention_mfma_long_prefix(gpu, length, count):
+    rng = np.random.default_rng(length + count)
+    total = length + count
+    q = (rng.normal(size=count * 4096) * 3).astype(np.float32)
+    kpm = rng.normal(size=(total, 1024)).astype(np.float32)
+    vpm = rng.normal(size=(total, 1024)).astype(np.float32)
+    got = gpu_util.attention_on_device(gpu, gpu.lh_attention_mfma, q, kpm, vpm, length, count,
+                                       CONTEXT)
+    want = oracle_lib.attention(MIRROR, q, kpm.reshape(-1), vpm.reshape(-1), 128, 1024, length,
+                                count)
+    assert np.all(np.isfinite(got))
+    assert np.max(np.abs(got - want)) < 2e-4
+
+
+def run_workload(fx, prefill_mode, turns):
+    """Yields (kind, logits) for every call of the fixture's workload."""
+    rt = Runtime(seed=fx["seed"], layers=fx["layers"], context=fx["context"], block=fx["block"],
+                 prefill=prefill_mode)
+    try:
+        prompt = syn.tokens(fx["seed"], 2, fx["prompt"])
+        assert [int(t) for t in prompt[:8]] == fx["prompt_first"]
+        checkpoint = None
+        for begin in range(0, fx["prompt"], fx["block"]):
+            ids = prompt[begin:begin + fx["block"]]
+            logits = rt.prefill(ids) if begin == 0 else rt.append(ids)
+            yield ("prefill" if begin == 0 else "append"), logits, rt
+            if begin + fx["block"] == fx["keep"]:
+                checkpoint = rt.checkpoint()
+        for turn in range(turns):
+            yield "restore", rt.restore(checkpoint), rt
+            ids = syn.tokens(fx["seed"], 100 + turn, fx["append"])
+            yield "append", rt.append(ids), rt
+            for _ in range(fx["decode"]):
+                yield "decode", rt.decode(rt.greedy()), rt
+        rt.destroy_checkpoint(checkpoint)
+    finally:
+        rt.close()
+
+
+def test_long_reuse_2layer_calls(gpu):
+    fx = fixture("long_c17920_2layer.json")
+    calls = fx["calls"]
+    precise = []
+    for i, (kind, logits, rt) in enumerate(run_workload(fx, lh.PREFILL_CUSTOM, 1)):
+        assert kind == calls[i]["kind"]
+        digest = hashlib.sha256(logits.tobytes()).hexdigest()
+        assert digest == calls[i]["sha256"], "precise path differs from the oracle at call %d" % i
+        assert rt.greedy() == calls[i]["token"]
+        precise.append(logits)
+    assert len(precise) == len(calls)
+    for i, (kind, logits, rt) in enumerate(run_workload(fx, lh.PREFILL_MPS, 1)):
+        want = precise[i]
+        span = float(want.max() - want.min())
+        assert np.max(np.abs(logits - want)) <= 1e-3 * span, "call %d (%s)" % (i, kind)
+        assert rt.greedy() == calls[i]["token"], "call %d (%s)" % (i, kind)
+
+
+def expected_stream(fx):
+    """Every id selected in the turns: the append's, then each decode's."""
+    return [t for turn in fx["turns"] for t in turn["tokens"]]
+
+
+@pytest.mark.parametrize("mode", [lh.PREFILL_CUSTOM, lh.PREFILL_MPS], ids=["precise", "mps"])
+def test_long_reuse_26layer_stream(gpu, mode):
+    fx = fixture("long_c17920_26layer.json")
+    got = []
+    in_turns = False
+    for kind, _, rt in run_workload(fx, mode, len(fx["turns"])):
+        in_turns = in_turns or kind == "restore"
+        if in_turns and kind in ("append", "decode"):
+            got.append(rt.greedy())
+    want = expected_stream(fx)
+    first = next((i for i in range(len(want)) if i >= len(got) or got[i] != want[i]), None)
+    print("long stream: %d/%d ids equal the oracle's" % (
+        len(want) if first is None else first, len(want)))
+    assert first is None, "first differing id at %d (top-2 gap there %.4g)" % (
+        first, [g for turn in fx["turns"] for g in turn["gaps"]][first])

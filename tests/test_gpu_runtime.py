@@ -9,7 +9,18 @@ Invariants from the reference's tests:
 - restore + append == fresh replay, bitwise (tests/long_context/long/schedule.py:33-44);
 - argument errors leave state untouched; execution/nonfinite failures
   invalidate until reset; checkpoint epochs/identity (tests/test_metal.m:629-860);
-- KV prefix, suffix and tail bytes after restore/rebranch (tests/test_metal.m).
+- KV prefix, suffix and tail bytes after restore/rebranch (tests/test_metal.m);
+- a step that fails after some layers wrote their KV rows invalidates the
+  sequence; after reset the same calls give bitwise the logits of a fresh
+  context (tests/test_metal.m:629-860, encoder failures at every index);
+- the N-th device or pinned allocation of create failing, for every N, returns
+  NULL with a diagnostic and frees everything it had allocated
+  (tests/test_metal.m:888-954);
+- checkpoint epoch exhaustion refuses a new handle and keeps the active one
+  (tests/test_metal.m:812-828).
+The failure cases run on the test build of the library
+(liblunelette_hip_test.so: the same objects plus the seams of
+lunelette_amd/csrc/lh_test_seams.h); every fault is forced from the host.
 """
 import math
 
@@ -44,6 +55,15 @@ def host_model():
 @pytest.fixture(scope="module")
 def rt(gpu):
     r = Runtime(seed=SEED, layers=LAYERS, context=256, block=256, prefill=lh.PREFILL_CUSTOM)
+    yield r
+    r.close()
+
+
+@pytest.fixture(scope="module")
+def rts(gpu):
+    """The same model on the test build, for host-forced failures."""
+    r = Runtime(seed=SEED, layers=LAYERS, context=256, block=256, prefill=lh.PREFILL_CUSTOM,
+                seams=True)
     yield r
     r.close()
 
@@ -150,7 +170,8 @@ def test_argument_errors_leave_state(rt):
     assert np.all(np.isfinite(logits))
 
 
-def test_execution_failure_invalidates_until_reset(rt):
+def test_execution_failure_invalidates_until_reset(rts):
+    rt = rts
     rt.reset()
     rt.prefill([1, 2])
     rt.inject(1)
@@ -168,7 +189,8 @@ def test_execution_failure_invalidates_until_reset(rt):
     rt.prefill([1])
 
 
-def test_checkpoint_semantics(rt):
+def test_checkpoint_semantics(rts):
+    rt = rts
     rt.reset()
     with pytest.raises(RuntimeError_):
         rt.checkpoint()  # no endpoint
@@ -256,25 +278,85 @@ def test_memory_and_limits(rt):
     assert mem["total_bytes"] == mem["weight_bytes"] + mem["scratch_bytes"] + mem["kv_bytes"]
 
 
-def test_graph_replay_equals_kernel_launches_across_blocks(gpu, monkeypatch):
-    """One-token steps replayed from a captured HIP graph (LUNELETTE_HIP_GRAPHS=1)
-    whose attention grid is updated at every 64-position boundary give bitwise
-    the logits and tokens of the same steps launched kernel by kernel."""
-    monkeypatch.setenv("LUNELETTE_HIP_GRAPHS", "1")
-    graphed = Runtime(seed=SEED, layers=LAYERS, context=256, block=256, prefill=lh.PREFILL_CUSTOM)
-    monkeypatch.setenv("LUNELETTE_HIP_GRAPHS", "0")
-    plain = Runtime(seed=SEED, layers=LAYERS, context=256, block=256, prefill=lh.PREFILL_CUSTOM)
+@pytest.mark.parametrize("mode", [lh.PREFILL_CUSTOM, lh.PREFILL_MPS], ids=["precise", "mps"])
+def test_failure_after_layer_then_reset_replays_bitwise(gpu, mode):
+    """Each layer writes its K/V rows before the next runs; a step failing after
+    layer 0 has written layer 0's rows for it. The sequence is invalid until
+    reset, a checkpoint taken before is dead, and after reset the same calls
+    give the logits of a fresh context bit for bit (the rows the failed step
+    wrote are rewritten before any read)."""
+    prompt = syn.tokens(SEED, 20, 40)
+    with Runtime(seed=SEED, layers=LAYERS, context=256, block=256, prefill=mode) as fresh:
+        want = [fresh.prefill(prompt), fresh.decode(7), fresh.append([8, 9, 10])]
+    with Runtime(seed=SEED, layers=LAYERS, context=256, block=256, prefill=mode,
+                 seams=True) as rt:
+        rt.fail_after_layer(0)
+        with pytest.raises(RuntimeError_, match="reset required"):
+            rt.prefill(prompt)
+        with pytest.raises(RuntimeError_):
+            rt.decode(7)  # invalid until reset
+        rt.reset()
+        assert np.array_equal(bits(rt.prefill(prompt)), bits(want[0]))
+        saved = rt.checkpoint()
+        rt.fail_after_layer(LAYERS - 1)
+        with pytest.raises(RuntimeError_, match="layer 1"):
+            rt.decode(7)
+        with pytest.raises(RuntimeError_):
+            rt.restore(saved)  # the failure invalidated the checkpoint
+        rt.destroy_checkpoint(saved)
+        rt.reset()
+        assert np.array_equal(bits(rt.prefill(prompt)), bits(want[0]))
+        rt.fail_after_layer(0)
+        with pytest.raises(RuntimeError_):
+            rt.append([8, 9, 10])
+        rt.reset()
+        assert np.array_equal(bits(rt.prefill(prompt)), bits(want[0]))
+        assert np.array_equal(bits(rt.decode(7)), bits(want[1]))
+        assert np.array_equal(bits(rt.append([8, 9, 10])), bits(want[2]))
+        with pytest.raises(RuntimeError_):
+            rt.fail_after_layer(LAYERS)  # no such layer
+
+
+@pytest.mark.parametrize("context,block", [(256, 256), (4352, 128)])
+def test_allocation_failure_at_every_index(gpu, context, block):
+    """The N-th device or pinned-host allocation of create fails, for every N
+    create makes: create returns NULL with a diagnostic, and every allocation
+    it had made is freed."""
+    seams = lh.test_lib()
+    seams.lunelette_metal_test_fail_allocation(0)
+    live = seams.lunelette_metal_test_live_allocations()
+    with Runtime(seed=SEED, layers=1, context=context, block=block, seams=True) as ok:
+        total = seams.lunelette_metal_test_allocations()
+        ok.prefill([1, 2])
+    assert seams.lunelette_metal_test_live_allocations() == live
+    assert total >= 20
     try:
-        ids = syn.tokens(SEED, 9, 60)
-        assert np.array_equal(bits(graphed.prefill(ids)), bits(plain.prefill(ids)))
-        token = graphed.greedy()
-        assert token == plain.greedy()
-        for _ in range(72):   # positions 60..131: block counts 1, 2, 3
-            a = graphed.decode(token)
-            b = plain.decode(token)
-            assert np.array_equal(bits(a), bits(b))
-            token = graphed.greedy()
-            assert token == plain.greedy()
+        for n in range(1, total + 1):
+            seams.lunelette_metal_test_fail_allocation(n)
+            with pytest.raises(RuntimeError_, match="create failed: .+"):
+                Runtime(seed=SEED, layers=1, context=context, block=block, seams=True)
+            assert seams.lunelette_metal_test_allocations() == n
+            assert seams.lunelette_metal_test_live_allocations() == live, n
     finally:
-        plain.close()
-        graphed.close()
+        seams.lunelette_metal_test_fail_allocation(0)
+    with Runtime(seed=SEED, layers=1, context=context, block=block, seams=True) as again:
+        again.prefill([1, 2])
+
+
+def test_checkpoint_epoch_exhaustion(gpu):
+    with Runtime(seed=SEED, layers=1, context=256, block=256, prefill=lh.PREFILL_CUSTOM,
+                 seams=True) as rt:
+        rt.prefill([1, 2, 3])
+        first = rt.checkpoint()   # epoch 1
+        saved = rt.restore(first)
+        rt.decode(4)
+        rt.set_epoch(2 ** 64 - 1)
+        with pytest.raises(RuntimeError_, match="epoch"):
+            rt.checkpoint()
+        rt.set_epoch(1)
+        assert np.array_equal(bits(rt.restore(first)), bits(saved))  # still the active one
+        second = rt.checkpoint()
+        with pytest.raises(RuntimeError_):
+            rt.restore(first)
+        rt.destroy_checkpoint(first)
+        rt.destroy_checkpoint(second)

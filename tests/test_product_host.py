@@ -40,6 +40,24 @@ def test_library_exports_every_declared_function(product):
     assert not missing, missing
 
 
+def exported(path):
+    import subprocess
+    out = subprocess.run(["nm", "-D", "--defined-only", path], stdout=subprocess.PIPE,
+                         text=True, check=True).stdout
+    return {line.split()[-1] for line in out.splitlines() if line.split()[1:2] == ["T"]}
+
+
+def test_shipped_library_exports_exactly_the_abi(product):
+    """The shipped library exports the functions of include/*.h and nothing
+    else: no internal launcher and no test seam. The test build exports the
+    same plus the seams of lunelette_amd/csrc/lh_test_seams.h."""
+    abi = declared_functions()
+    assert exported(lh.LIBRARY) == abi
+    seams = {n for n in exported(lh.TEST_LIBRARY) - abi}
+    assert seams and all(n.startswith("lunelette_metal_test_") for n in seams), seams
+    assert "lunelette_metal_test_inject" in seams
+
+
 def test_yarn_and_query_factor_match_oracle(product, oracle):
     fp = ctypes.POINTER(ctypes.c_float)
     c = np.empty(128, np.float32)
