@@ -1,62 +1,96 @@
-/* Chat framing of one turn (behaviour of the reference's src/chat.c:6-59):
- * BOS, [SYSTEM_PROMPT] system [/SYSTEM_PROMPT] when given, [INST] prompt
- * [/INST] unless raw. Texts are encoded as ordinary text; the output is
- * written only when the whole frame fits the 256-token context. */
+/* Chat framing of one turn, to the contract of the reference's include/chat.h:
+ * BOS, then [SYSTEM_PROMPT] system [/SYSTEM_PROMPT] when a system text is
+ * given, then [INST] prompt [/INST]; raw framing is BOS + prompt and takes no
+ * system text. Texts are encoded as ordinary text, so a literal control
+ * spelling inside them stays text.
+ *
+ * The frame is planned as a list of segments (a control id, or the encoding
+ * of one text), measured, and written to the caller's array only when it fits
+ * the 256-id context, so a failure leaves ids and count untouched. */
 #include "lunelette_chat.h"
 
 #include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
+typedef struct {
+    int64_t control;       /* id of a control segment, or -1 for text */
+    const char *text;      /* text to encode (control == -1) */
+    uint32_t *ids;         /* encoded text, owned */
+    size_t n;
+} segment;
+
+static void fail(char *error, size_t error_size, const char *message)
+{
+    if (error && error_size) {
+        snprintf(error, error_size, "%s", message);
+    }
+}
+
 int lunelette_chat_prompt(const lunelette_tokenizer *tokenizer, const char *prompt,
     const char *system, int raw, int64_t ids[LUNELETTE_CONTEXT_LIMIT], size_t *count,
     char *error, size_t error_size)
 {
-    if (!tokenizer || !prompt || !ids || !count || (raw && system)) {
-        if (error && error_size) {
-            snprintf(error, error_size, "Invalid prompt arguments (raw forbids system)");
-        }
+    if (!tokenizer || !prompt || !ids || !count) {
+        fail(error, error_size, "chat: tokenizer, prompt and output are required");
         return -1;
     }
-    uint32_t *user = NULL, *sys = NULL;
-    size_t user_n = 0, sys_n = 0;
-    int status = -1;
-    if (!lunelette_tokenizer_encode(tokenizer, (const unsigned char *)prompt, strlen(prompt),
-            &user, &user_n, error, error_size) ||
-        (system && !lunelette_tokenizer_encode(tokenizer, (const unsigned char *)system,
-            strlen(system), &sys, &sys_n, error, error_size))) {
-        goto done;
+    if (raw && system) {
+        fail(error, error_size, "chat: raw framing takes no system text");
+        return -1;
     }
-    const size_t framing = 1 + (raw ? 0 : 2) + (system ? 2 : 0);
-    const size_t total = framing + user_n + sys_n;
+    segment plan[7];
+    size_t segments = 0;
+    plan[segments++] = (segment){LUNELETTE_TOKEN_BOS, NULL, NULL, 0};
+    if (system) {
+        plan[segments++] = (segment){LUNELETTE_TOKEN_SYSTEM, NULL, NULL, 0};
+        plan[segments++] = (segment){-1, system, NULL, 0};
+        plan[segments++] = (segment){LUNELETTE_TOKEN_END_SYSTEM, NULL, NULL, 0};
+    }
+    if (!raw) {
+        plan[segments++] = (segment){LUNELETTE_TOKEN_INST, NULL, NULL, 0};
+    }
+    plan[segments++] = (segment){-1, prompt, NULL, 0};
+    if (!raw) {
+        plan[segments++] = (segment){LUNELETTE_TOKEN_END_INST, NULL, NULL, 0};
+    }
+
+    int status = -1;
+    size_t total = 0;
+    for (size_t i = 0; i < segments; i++) {
+        segment *s = &plan[i];
+        if (s->control >= 0) {
+            total += 1;
+            continue;
+        }
+        if (!lunelette_tokenizer_encode(tokenizer, (const unsigned char *)s->text,
+                strlen(s->text), &s->ids, &s->n, error, error_size)) {
+            goto release;
+        }
+        total += s->n;
+    }
     if (total > LUNELETTE_CONTEXT_LIMIT) {
         if (error && error_size) {
-            snprintf(error, error_size, "Prompt exceeds 256-token context (%zu tokens)", total);
+            snprintf(error, error_size, "chat: the framed turn needs %zu ids, over the 256-id "
+                "context", total);
         }
-        goto done;
+        goto release;
     }
-    size_t n = 0;
-    ids[n++] = LUNELETTE_TOKEN_BOS;
-    if (system) {
-        ids[n++] = LUNELETTE_TOKEN_SYSTEM;
-        for (size_t i = 0; i < sys_n; i++) {
-            ids[n++] = sys[i];
+    size_t at = 0;
+    for (size_t i = 0; i < segments; i++) {
+        if (plan[i].control >= 0) {
+            ids[at++] = plan[i].control;
+        } else {
+            for (size_t j = 0; j < plan[i].n; j++) {
+                ids[at++] = plan[i].ids[j];
+            }
         }
-        ids[n++] = LUNELETTE_TOKEN_END_SYSTEM;
     }
-    if (!raw) {
-        ids[n++] = LUNELETTE_TOKEN_INST;
-    }
-    for (size_t i = 0; i < user_n; i++) {
-        ids[n++] = user[i];
-    }
-    if (!raw) {
-        ids[n++] = LUNELETTE_TOKEN_END_INST;
-    }
-    *count = n;
+    *count = at;
     status = 0;
-done:
-    free(user);
-    free(sys);
+release:
+    for (size_t i = 0; i < segments; i++) {
+        free(plan[i].ids);
+    }
     return status;
 }

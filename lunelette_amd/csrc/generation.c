@@ -1,5 +1,5 @@
-/* Greedy selection and the full-prefix generation loop (contract of the
- * reference include/generation.h:38-71, behaviour of src/generation.c:8-136). */
+/* Greedy selection and the full-prefix generation loop, to the contract of
+ * the reference's include/generation.h:38-71. */
 #include "lunelette_generation.h"
 #include "lh_scan.h"
 
@@ -41,77 +41,114 @@ int lunelette_select_greedy(const float *logits, int64_t *token, char *error, si
     return 0;
 }
 
+/* Request checks of include/generation.h:47-71, all made before any callback
+ * (every prompt id, even for a zero budget). Returns the diagnostic of the
+ * first problem, or NULL; *at names a bad prompt position. */
+static const char *request_problem(lunelette_logits_fn next, const int64_t *prompt, size_t count,
+    size_t limit, const lunelette_generation_config *config,
+    const lunelette_generation_result *result, size_t *at)
+{
+    if (limit != LUNELETTE_CONTEXT_LIMIT && limit != LUNELETTE_LONG_CONTEXT_LIMIT) {
+        return "generation: context limit must be 256 or 4352";
+    }
+    if (!next || !prompt || !config || !result) {
+        return "generation: callback, prompt, config and result are required";
+    }
+    if (!count || count > limit) {
+        return "generation: prompt length must be 1..context limit";
+    }
+    if (config->max_new_tokens > LUNELETTE_GENERATION_LIMIT) {
+        return "generation: budget above 256 new tokens";
+    }
+    if (config->eos_token < 0 || config->eos_token >= LUNELETTE_VOCAB_SIZE) {
+        return "generation: EOS id outside the vocabulary";
+    }
+    for (size_t i = 0; i < count; i++) {
+        if (prompt[i] < 0 || prompt[i] >= LUNELETTE_VOCAB_SIZE) {
+            *at = i;
+            return "generation: prompt id at position %zu outside the vocabulary";
+        }
+    }
+    return NULL;
+}
+
+/* Stop rule after `produced` new tokens with the sequence `length` long:
+ * the last token being EOS wins over an exhausted budget, which wins over a
+ * full context (the prompt's own ids never count as EOS). -1: continue. */
+static int stop_rule(int64_t last, size_t produced, size_t length, size_t limit,
+    const lunelette_generation_config *config)
+{
+    if (produced && last == config->eos_token) {
+        return LUNELETTE_STOP_EOS;
+    }
+    if (produced == config->max_new_tokens) {
+        return LUNELETTE_STOP_LIMIT;
+    }
+    if (length == limit) {
+        return LUNELETTE_STOP_CONTEXT;
+    }
+    return -1;
+}
+
+/* The full prefix (prompt then generated ids) is handed to the callback on
+ * every step; the caller's result is written only after the last step
+ * succeeded, so a failure leaves it exactly as it was. */
 int lunelette_generate_with_logits_capacity(lunelette_logits_fn next, void *context,
     const int64_t *prompt, size_t count, size_t context_limit,
     const lunelette_generation_config *config, lunelette_generation_result *result,
     char *error, size_t capacity)
 {
-    say(error, capacity, context_limit == LUNELETTE_CONTEXT_LIMIT ?
-        "generation: require callback, prompt 1..256, config budget 0..256, valid EOS, result" :
-        "generation: require callback, context 256 or 4352, prompt within context, "
-        "config budget 0..256, valid EOS, result");
-    if (!next || !prompt || !config || !result || !count || count > context_limit ||
-        (context_limit != LUNELETTE_CONTEXT_LIMIT &&
-            context_limit != LUNELETTE_LONG_CONTEXT_LIMIT) ||
-        config->max_new_tokens > LUNELETTE_GENERATION_LIMIT || config->eos_token < 0 ||
-        config->eos_token >= LUNELETTE_VOCAB_SIZE) {
-        return -1;
-    }
-    for (size_t i = 0; i < count; i++) {
-        if (prompt[i] < 0 || prompt[i] >= LUNELETTE_VOCAB_SIZE) {
-            if (error && capacity) {
-                snprintf(error, capacity, "generation: invalid prompt token at %zu", i);
-            }
-            return -1;
-        }
-    }
-    int64_t *ids = malloc(context_limit * sizeof *ids);
-    float *logits = NULL;
-    if (!ids) {
-        say(error, capacity, "generation: prefix allocation failed");
-        return -1;
-    }
-    memcpy(ids, prompt, count * sizeof *ids);
-    if (config->max_new_tokens && count < context_limit) {
-        logits = malloc(LUNELETTE_VOCAB_SIZE * sizeof(float));
-        if (!logits) {
-            say(error, capacity, "generation: logits allocation failed");
-            free(ids);
-            return -1;
-        }
-    }
-    lunelette_generation_result pending;
-    memset(&pending, 0, sizeof pending);
-    pending.stop = LUNELETTE_STOP_LIMIT;
-    int status = 0;
-    while (pending.count < config->max_new_tokens) {
-        if (count == context_limit) {
-            pending.stop = LUNELETTE_STOP_CONTEXT;
-            break;
-        }
+    size_t at = 0;
+    const char *problem = request_problem(next, prompt, count, context_limit, config, result,
+        &at);
+    if (problem) {
         if (error && capacity) {
-            snprintf(error, capacity, "generation: logits callback failed at step %zu",
-                pending.count);
+            snprintf(error, capacity, problem, at);
         }
-        int64_t best;
-        if (next(context, ids, count, logits, error, capacity) ||
-            lunelette_select_greedy(logits, &best, error, capacity)) {
-            status = -1;
-            break;
-        }
-        ids[count++] = best;
-        pending.tokens[pending.count++] = best;
-        if (best == config->eos_token) {
-            pending.stop = LUNELETTE_STOP_EOS;
-            break;
-        }
-    }
-    free(ids);
-    free(logits);
-    if (status) {
         return -1;
     }
-    *result = pending;
+    lunelette_generation_result staged = {.count = 0, .stop = LUNELETTE_STOP_LIMIT};
+    size_t length = count;
+    int64_t last = -1;
+    int stop = stop_rule(last, 0, length, context_limit, config);
+    int64_t *prefix = NULL;
+    float *scratch = NULL;
+    if (stop < 0) {
+        prefix = malloc(context_limit * sizeof *prefix);
+        scratch = malloc(LUNELETTE_VOCAB_SIZE * sizeof *scratch);
+        if (!prefix || !scratch) {
+            say(error, capacity, "generation: scratch allocation failed");
+            free(prefix);
+            free(scratch);
+            return -1;
+        }
+        memcpy(prefix, prompt, count * sizeof *prefix);
+    }
+    while (stop < 0) {
+        if (error && capacity) {
+            error[0] = '\0';
+        }
+        if (next(context, prefix, length, scratch, error, capacity)) {
+            if (error && capacity && !error[0]) {
+                snprintf(error, capacity, "generation: the logits callback failed on new token "
+                    "%zu", staged.count);
+            }
+            break;
+        }
+        if (lunelette_select_greedy(scratch, &last, error, capacity)) {
+            break;
+        }
+        prefix[length++] = last;
+        staged.tokens[staged.count++] = last;
+        stop = stop_rule(last, staged.count, length, context_limit, config);
+    }
+    free(prefix);
+    free(scratch);
+    if (stop < 0) {
+        return -1;
+    }
+    staged.stop = (lunelette_stop_reason)stop;
+    *result = staged;
     if (error && capacity) {
         error[0] = '\0';
     }

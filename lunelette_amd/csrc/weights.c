@@ -306,70 +306,100 @@ static int parse_header(lh_st_file *f, const unsigned char *header, size_t lengt
 
 /* ---- data layout ---- */
 
-static int check_layout(const lh_st_file *f, uint64_t data_bytes)
+/* Byte size of a tensor from its dtype and shape: every dimension at most
+ * INT64_MAX, a zero dimension makes it empty, and neither the element count
+ * nor the byte count may overflow 64 bits. */
+static int tensor_bytes(const lh_st_tensor *t, uint64_t *bytes)
 {
-    size_t nonempty = 0;
-    for (size_t i = 0; i < f->count; i++) {
-        const lh_st_tensor *t = &f->tensors[i];
-        uint64_t elements = 1;
-        bool zero = false;
-        for (uint32_t k = 0; k < t->rank; k++) {
-            if (t->shape[k] > (uint64_t)INT64_MAX) {
-                return -1;
-            }
-            zero |= t->shape[k] == 0;
-        }
-        if (zero) {
-            elements = 0;
-        } else {
-            for (uint32_t k = 0; k < t->rank; k++) {
-                if (elements > UINT64_MAX / t->shape[k]) {
-                    return -1;
-                }
-                elements *= t->shape[k];
-            }
-        }
-        if (elements > UINT64_MAX / (uint64_t)t->dtype || t->end < t->begin ||
-            t->end > data_bytes || t->end - t->begin != elements * (uint64_t)t->dtype) {
+    uint64_t elements = 1;
+    bool empty = false;
+    for (uint32_t k = 0; k < t->rank; k++) {
+        if (t->shape[k] > (uint64_t)INT64_MAX) {
             return -1;
         }
-        nonempty += t->end > t->begin;
+        empty = empty || t->shape[k] == 0;
     }
-    /* Walk the data section from 0: exactly one non-empty tensor starts at
-     * every cursor position, and the last one ends at the section's end. */
-    uint64_t cursor = 0;
-    for (size_t step = 0; step < nonempty; step++) {
-        const lh_st_tensor *next = NULL;
-        for (size_t i = 0; i < f->count; i++) {
-            const lh_st_tensor *t = &f->tensors[i];
-            if (t->begin == cursor && t->end > cursor) {
-                if (next) {
-                    return -1;
-                }
-                next = t;
-            }
-        }
-        if (!next) {
+    for (uint32_t k = 0; k < t->rank && !empty; k++) {
+        if (elements > UINT64_MAX / t->shape[k]) {
             return -1;
         }
-        cursor = next->end;
+        elements *= t->shape[k];
     }
-    if (cursor != data_bytes) {
+    if (empty) {
+        elements = 0;
+    }
+    if (elements > UINT64_MAX / (uint64_t)t->dtype) {
         return -1;
     }
+    *bytes = elements * (uint64_t)t->dtype;
+    return 0;
+}
+
+static int by_begin(const void *a, const void *b)
+{
+    const lh_st_tensor *x = *(const lh_st_tensor *const *)a;
+    const lh_st_tensor *y = *(const lh_st_tensor *const *)b;
+    return x->begin < y->begin ? -1 : (x->begin > y->begin);
+}
+
+/* The data section must be tiled exactly by the non-empty tensors: sorted by
+ * offset, the first starts at 0, each starts where the previous ends (so two
+ * at one offset fail), and the last ends at the section's end. An empty
+ * tensor may sit at any tile boundary but not strictly inside a tile. Every
+ * tensor's byte range must match its dtype and shape and lie in the section. */
+static int check_layout(const lh_st_file *f, uint64_t data_bytes)
+{
+    const lh_st_tensor **tiles = malloc((f->count ? f->count : 1) * sizeof *tiles);
+    if (!tiles) {
+        return -1;
+    }
+    size_t n = 0;
+    int status = -1;
     for (size_t i = 0; i < f->count; i++) {
-        const lh_st_tensor *empty = &f->tensors[i];
-        if (empty->begin != empty->end) {
-            continue;
+        const lh_st_tensor *t = &f->tensors[i];
+        uint64_t bytes;
+        if (tensor_bytes(t, &bytes) || t->end < t->begin || t->end > data_bytes ||
+            t->end - t->begin != bytes) {
+            goto done;
         }
-        for (size_t k = 0; k < f->count; k++) {
-            const lh_st_tensor *t = &f->tensors[k];
-            if (t->begin < empty->begin && empty->begin < t->end) {
-                return -1;
-            }
+        if (bytes) {
+            tiles[n++] = t;
         }
     }
-    return 0;
+    qsort(tiles, n, sizeof *tiles, by_begin);
+    uint64_t expected = 0;
+    for (size_t i = 0; i < n; i++) {
+        if (tiles[i]->begin != expected) {
+            goto done;
+        }
+        expected = tiles[i]->end;
+    }
+    if (expected != data_bytes) {
+        goto done;
+    }
+    for (size_t i = 0; i < f->count; i++) {
+        const lh_st_tensor *t = &f->tensors[i];
+        if (t->begin != t->end || n == 0) {
+            continue;
+        }
+        /* Last tile starting at or before the empty tensor's offset. */
+        size_t lo = 0, hi = n;
+        while (hi - lo > 1) {
+            const size_t mid = lo + (hi - lo) / 2;
+            if (tiles[mid]->begin <= t->begin) {
+                lo = mid;
+            } else {
+                hi = mid;
+            }
+        }
+        if (tiles[lo]->begin < t->begin && t->begin < tiles[lo]->end) {
+            goto done;
+        }
+    }
+    status = 0;
+done:
+    free(tiles);
+    return status;
 }
 
 /* ---- container API ---- */
