@@ -308,3 +308,69 @@ def test_chat_framing(synthetic, libraries):
             assert t.chat_prompt("x" * 255)[0] == -1          # 258 ids do not fit
             assert t.chat_prompt(b"\xff")[0] == -1
             assert t.chat_prompt("u", b"\xff")[0] == -1
+
+
+REFERENCE_TABLE = "/root/reference/src/tokenizer_unicode.h"
+
+
+def shipped_classes():
+    import re as _re
+    text = open(os.path.join(ROOT, "lunelette_amd", "csrc", "lh_unicode_classes.h")).read()
+    table = bytearray(0x110000)
+    for a, b, m in _re.findall(r"\{0x([0-9a-f]+), 0x([0-9a-f]+), (\d+)\}", text):
+        table[int(a, 16):int(b, 16) + 1] = bytes([int(m)]) * (int(b, 16) - int(a, 16) + 1)
+    return table
+
+
+def test_class_table_matches_reference_table():
+    """Every code point has the class the reference tokenizer's generated
+    property table (Unicode 18.0.0) gives it, mapped onto the pattern's five
+    classes."""
+    if not os.path.exists(REFERENCE_TABLE):
+        pytest.skip("the reference checkout is not present")
+    import importlib.util
+    spec = importlib.util.spec_from_file_location(
+        "gen", os.path.join(ROOT, "lunelette_amd", "csrc", "gen_unicode_classes.py"))
+    gen = importlib.util.module_from_spec(spec)
+    spec.loader.exec_module(gen)
+    ranges, version = gen.reference_ranges(REFERENCE_TABLE)
+    assert "Unicode 18" in version
+    want = bytearray(0x110000)
+    for a, b, m in ranges:
+        want[a:b + 1] = bytes([gen.from_reference_mask(m)]) * (b - a + 1)
+    assert shipped_classes() == want
+
+
+# Code points whose class Unicode 18 assigns and the installed regex package's
+# older data does not (letters, numbers, marks), mixed with ASCII.
+UNICODE18 = ["\U0003d000", "\U0003d5a1", "\U00018e00", "\U00019191", "\U00012550",
+             "\U00012686"]
+
+
+def test_unicode18_text_matches_reference_tokenizer(tmp_path, libraries):
+    if len(libraries) < 2:
+        pytest.skip("oracle/_ref/libreftok.so not built")
+    table = shipped_classes()
+    assert all(table[ord(c)] for c in UNICODE18)
+    path = tmp_path / "rich18.json"
+    write_tekken(path, rich_ranks())
+    opened = [(name, Tokenizer(path, library)) for name, library in libraries]
+    alphabet = UNICODE18 + ["a", "Z", " ", "7", "\n", "é", "日", "!", "'s"]
+    rng = random.Random(18)
+    texts = ["".join(rng.choice(alphabet) for _ in range(rng.randrange(1, 30)))
+             for _ in range(2000)]
+    engine = regex.compile(PATTERN)
+    boundaries_differ = 0
+    for text in texts:
+        ids = [t.encode(text) for _, t in opened]
+        assert ids[0] == ids[1], repr(text)
+        ends, at = [], 0
+        for m in engine.finditer(text):
+            at += len(m.group().encode())
+            ends.append(at)
+        boundaries_differ += ends != split(text)
+    # The texts exercise the new assignments: the installed regex (older
+    # Unicode data) splits many of them differently.
+    assert boundaries_differ > 100
+    for _, t in opened:
+        t.close()
