@@ -28,10 +28,12 @@
  */
 #define _POSIX_C_SOURCE 200809L
 #include "lh_weights.h"
+#include "lunelette_weights.h"
 
 #include <limits.h>
 #include <math.h>
 #include <stdbool.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -758,4 +760,43 @@ int lh_checkpoint_check(const char *path, float *scales, char *error, size_t cap
     lh_weights_close(w);
     free(w);
     return rc;
+}
+
+/* include/lunelette_weights.h: the metadata handle of src/metal_weights.h for
+ * callers that validate a checkpoint without creating a runtime. */
+int lunelette_metal_weights_open(lunelette_metal_weights *weights, const char *path,
+    char *error, size_t capacity)
+{
+    char fallback[512];
+    if (!error || !capacity) {
+        error = fallback;
+        capacity = sizeof fallback;
+    }
+    if (!weights) {
+        snprintf(error, capacity, "checkpoint metadata needs a handle");
+        return -1;
+    }
+    weights->opened = NULL;
+    lh_weights *w = malloc(sizeof *w);
+    if (!w) {
+        snprintf(error, capacity, "checkpoint handle allocation failed");
+        return -1;
+    }
+    if (lh_weights_open(w, path, error, capacity)) {
+        free(w);
+        return -1;
+    }
+    weights->opened = w;
+    return 0;
+}
+
+void lunelette_metal_weights_close(lunelette_metal_weights *weights)
+{
+    if (weights && weights->opened) {
+        lh_weights_close(weights->opened);
+        free(weights->opened);
+    }
+    if (weights) {
+        weights->opened = NULL;
+    }
 }
