@@ -121,6 +121,17 @@ int lh_layer_operator(int op, const lh_layer_weights *w, float *d_x, float *d_ke
  * [0, length+t] of d_keys/d_values ([8][capacity][128]) into d_out. */
 int lh_attention(const float *d_q, const float *d_keys, const float *d_values, lh_workspace *ws,
     float *d_out, void *stream);
+/* No counterpart in the reference. For callers that cannot allocate device
+ * memory (code under HIP graph capture, tight serving loops, harnesses that
+ * forbid hipMalloc): lh_attention without a workspace. Query rows d_q
+ * [count][4096] attend positions [0, length + t] of d_keys/d_values
+ * ([8][capacity][128]); bitwise the result of lh_attention for the same
+ * length and count. The split-KV partials and the step header live in one
+ * static device array per GPU, held until the process ends: count * capacity
+ * must not exceed 65536 (17.0 MB of scratch), larger calls are refused. Calls that
+ * overlap on one GPU race on that array; callers serialize them. */
+int lh_attention_noalloc(const float *d_q, const float *d_keys, const float *d_values,
+    size_t length, size_t count, size_t capacity, float *d_out, void *stream);
 /* The same attention on the matrix cores (the PREFILL_MPS path's operator;
  * replaces the scores + attend dispatches of src/metal_encode.m:154-159 when
  * prefill runs on MPS): FP32 MFMA with an online softmax, tolerance-equal to

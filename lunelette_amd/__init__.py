@@ -158,6 +158,8 @@ def _load(path):
            c_void, c_void)
     _proto(l, "lh_attention", i, c_void, c_void, c_void, c_void, c_void, c_void)
     _proto(l, "lh_attention_mfma", i, c_void, c_void, c_void, c_void, c_void, c_void)
+    _proto(l, "lh_attention_noalloc", i, c_void, c_void, c_void, c_size, c_size, c_size, c_void,
+           c_void)
     _proto(l, "lh_embed_forward", i, c_void, c_void, c_void, c_void)
     _proto(l, "lh_yarn", i, ctypes.c_uint32, c_float_p, c_float_p)
     _proto(l, "lh_query_factor", f, ctypes.c_uint32)

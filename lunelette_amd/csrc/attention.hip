@@ -23,6 +23,8 @@
 #include "lh_device.h"
 #include "lh_internal.h"
 
+#include <pthread.h>
+
 namespace lh {
 
 constexpr uint32_t GROUP = 8;     // blocks chained per combine group
@@ -295,6 +297,80 @@ extern "C" int lh_launch_attention(const float* q, const float* kcache_layer,
     hipLaunchKernelGGL(k_attn_combine, dim3(LH_HEADS * 4, count), dim3(256), 0, s, PM, PT, PA, params,
         capacity, out);
     return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+// ---------------------------------------------------------------------------
+// lh_attention_noalloc: the same two kernels for callers that cannot allocate.
+// The step header (only `length` is read) and the split-KV partials live in
+// one file-scope device array per GPU. Host code never passes the array's
+// name to a kernel: its device address comes from hipGetSymbolAddress, taken
+// once per device on the first call there. Layout: 256-byte header, then PM
+// and PT ([count][32][capacity/64] floats each), then PA (x 128).
+namespace lh {
+constexpr size_t NOALLOC_POSITIONS = 65536;   // largest count * capacity
+constexpr size_t NOALLOC_PARTIALS = NOALLOC_POSITIONS / LH_ATTN_BLOCK * LH_HEADS;
+constexpr size_t NOALLOC_BYTES = 256 + 4 * NOALLOC_PARTIALS * (2 + LH_HEAD_DIM);
+__device__ __align__(256) unsigned char scratch[NOALLOC_BYTES];
+
+__global__ void k_set_step(lh_step_params* params, uint32_t length, uint32_t count)
+{
+    if (threadIdx.x == 0) {
+        params->length = length;
+        params->count = count;
+    }
+}
+}  // namespace lh
+
+static pthread_mutex_t noalloc_lock = PTHREAD_MUTEX_INITIALIZER;
+static unsigned char* noalloc_base[64];
+
+extern "C" int lh_attention_noalloc(const float* d_q, const float* d_keys, const float* d_values,
+    size_t length, size_t count, size_t capacity, float* d_out, void* stream)
+{
+    if (!d_q || !d_keys || !d_values || !d_out || !count || !capacity ||
+        capacity % LH_ATTN_BLOCK || length > capacity || count > capacity - length) {
+        lh_set_error("attention_noalloc: need q, K, V and out, capacity a multiple of 64, "
+            "length + count <= capacity");
+        return -1;
+    }
+    if (count > lh::NOALLOC_POSITIONS / capacity) {
+        lh_set_error("attention_noalloc: count * capacity = %zu exceeds the %zu positions of "
+            "the static scratch", count * capacity, lh::NOALLOC_POSITIONS);
+        return -1;
+    }
+    int device = -1;
+    if (hipGetDevice(&device) != hipSuccess || device < 0 || device >= 64) {
+        lh_set_error("attention_noalloc: no current device");
+        return -1;
+    }
+    pthread_mutex_lock(&noalloc_lock);
+    if (!noalloc_base[device]) {
+        void* ptr = nullptr;
+        const hipError_t status = hipGetSymbolAddress(&ptr, HIP_SYMBOL(lh::scratch));
+        if (status != hipSuccess || !ptr) {
+            pthread_mutex_unlock(&noalloc_lock);
+            lh_set_error("attention_noalloc: scratch address: %s", hipGetErrorString(status));
+            return -1;
+        }
+        noalloc_base[device] = static_cast<unsigned char*>(ptr);
+    }
+    unsigned char* base = noalloc_base[device];
+    pthread_mutex_unlock(&noalloc_lock);
+    const size_t partials = count * LH_HEADS * (capacity / LH_ATTN_BLOCK);
+    lh_step_params* params = reinterpret_cast<lh_step_params*>(base);
+    float* PM = reinterpret_cast<float*>(base + 256);
+    float* PT = PM + partials;
+    float* PA = PT + partials;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipLaunchKernelGGL(lh::k_set_step, dim3(1), dim3(64), 0, s, params, (uint32_t)length,
+        (uint32_t)count);
+    if (hipGetLastError() != hipSuccess ||
+        lh_launch_attention(d_q, d_keys, d_values, params, (uint32_t)length, (uint32_t)count,
+            (uint32_t)capacity, PM, PT, PA, d_out, s)) {
+        lh_set_error("attention_noalloc: launch failed");
+        return -1;
+    }
+    return 0;
 }
 
 extern "C" uint32_t lh_attention_blocks(uint32_t length, uint32_t count)
