@@ -277,9 +277,9 @@ __device__ __forceinline__ void dot_rows(const WVec<KIND> (&wv)[R][NCH], const f
 }
 
 // ---------------------------------------------------------------------------
-// Model-shape row dots: y[t][row] = (residual ? residual[t][row] + : ) s * dot.
+// Model-shape row dots: y[t][row] = (RES ? residual[t][row] + : ) s * dot.
 // Wave w of workgroup b owns rows R*(4b + w) .. +R. grid (rows/(4R), tokens).
-template <int KIND, bool LUT, int NCH, int R>
+template <int KIND, bool LUT, int NCH, int R, bool RES>
 __global__ void __launch_bounds__(256)
 k_rows(const void* __restrict__ W, float scale, const float* __restrict__ x, float* y,
     const float* residual, uint32_t rows)
@@ -302,14 +302,38 @@ k_rows(const void* __restrict__ W, float scale, const float* __restrict__ x, flo
     WVec<KIND> wv[R][NCH];
     issue_rows<KIND, NCH, R>(W, rr, wv);
     stage_commit<NCH>(xv, xin_s);
+    // The epilogue's residual values are requested now, after the row is
+    // staged, so they return behind the weights instead of costing a memory
+    // round trip after the dots. Written as assembly because the compiler
+    // sinks an ordinary load to its use; loads complete in issue order, so
+    // the compiler's own waits for the weights stay sufficient (they wait one
+    // load longer), and the values are read only after waiting for all loads.
+    float res[R];
+    if constexpr (RES) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            const float* p = residual + (size_t)t * rows + row0 + r;
+            asm volatile("global_load_dword %0, %1, off" : "=v"(res[r]) : "v"(p) : "memory");
+        }
+    }
     float dots[R];
     dot_rows<KIND, LUT, NCH, R>(wv, xin_s, lut_s, dots);
+    if constexpr (RES) {
+#pragma unroll
+        for (int r = 0; r < R; r++) {
+            asm volatile("s_waitcnt vmcnt(0)" : "+v"(res[r]) : : "memory");
+        }
+    }
+    float out[R];
+#pragma unroll
+    for (int r = 0; r < R; r++) {
+        const float v = dots[r] * scale;
+        out[r] = RES ? res[r] + v : v;
+    }
     if (lane == 0) {
 #pragma unroll
         for (int r = 0; r < R; r++) {
-            const size_t o = (size_t)t * rows + row0 + r;
-            const float v = dots[r] * scale;
-            y[o] = residual ? residual[o] + v : v;
+            y[(size_t)t * rows + row0 + r] = out[r];
         }
     }
 }
@@ -558,8 +582,13 @@ static int launch_rows(const void* W, float scale, const float* x, float* y, con
     uint32_t rows, uint32_t tokens, hipStream_t s)
 {
     dim3 grid(rows / (4 * R), tokens);
-    hipLaunchKernelGGL((k_rows<KIND, LUT, NCH, R>), grid, dim3(256), 0, s, W, scale, x, y,
-        residual, rows);
+    if (residual) {
+        hipLaunchKernelGGL((k_rows<KIND, LUT, NCH, R, true>), grid, dim3(256), 0, s, W, scale, x,
+            y, residual, rows);
+    } else {
+        hipLaunchKernelGGL((k_rows<KIND, LUT, NCH, R, false>), grid, dim3(256), 0, s, W, scale, x,
+            y, residual, rows);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
