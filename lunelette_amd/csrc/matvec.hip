@@ -276,6 +276,58 @@ __device__ __forceinline__ void dot_rows(const WVec<KIND> (&wv)[R][NCH], const f
     }
 }
 
+// A wave's run of RW rows (rows[j], any order) with DEPTH rows of loads in
+// flight: start() issues the first DEPTH rows; run() then, before each row's
+// dot, issues the row DEPTH ahead into the slot the previous dot freed, and
+// dots one row at a time in issue order. The compiler's waits follow issue
+// order, so each dot starts as soon as its own row has landed, and after the
+// last bytes arrive only one row's dot remains (where dot_rows over three rows
+// at once waits for the last of the three). Scheduling barriers keep each
+// row's loads between the dots around them: the scheduler otherwise hoists
+// later rows' loads above a dot, which pushes that dot's waits back to
+// vmcnt(0) and drains the wave's queue on every row.
+template <int KIND, int NCH, int RW, int DEPTH>
+struct RowStream {
+    static constexpr int SLOTS = DEPTH + 1;
+    WVec<KIND> wv[SLOTS][NCH];
+
+    __device__ __forceinline__ void issue(const void* W, uint32_t row, int slot)
+    {
+        const int lane = threadIdx.x & 63;
+#pragma unroll
+        for (int c = 0; c < NCH; c++) {
+            load_w<KIND>(wv[slot][c], W, row, NCH * LH_CHUNK, c * LH_CHUNK + lane * LH_LANE_COLS);
+        }
+    }
+
+    __device__ __forceinline__ void start(const void* W, const uint32_t (&rows)[RW])
+    {
+#pragma unroll
+        for (int j = 0; j < DEPTH && j < RW; j++) {
+            issue(W, rows[j], j % SLOTS);
+        }
+    }
+
+    // Unscaled canonical dots of the RW rows; lane 0 holds the totals.
+    template <bool LUT>
+    __device__ __forceinline__ void run(const void* W, const uint32_t (&rows)[RW],
+        const float4* xl, const float* lut, float (&dots)[RW])
+    {
+#pragma unroll
+        for (int j = 0; j < RW; j++) {
+            if (j + DEPTH < RW) {
+                issue(W, rows[j + DEPTH], (j + DEPTH) % SLOTS);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            float d[1];
+            dot_rows<KIND, LUT, NCH, 1>(
+                *reinterpret_cast<const WVec<KIND>(*)[1][NCH]>(&wv[j % SLOTS]), xl, lut, d);
+            dots[j] = d[0];
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+};
+
 // ---------------------------------------------------------------------------
 // Model-shape row dots: y[t][row] = (RES ? residual[t][row] + : ) s * dot.
 // Wave w of workgroup b owns rows R*(4b + w) .. +R. grid (rows/(4R), tokens).
@@ -466,49 +518,57 @@ k_qkv_rope(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restr
 }
 
 // RMSNorm -> gate and up rows -> SiLU(gate)*up (src/metal_encode.m:162-171).
-// A workgroup of eight waves owns inner rows 12b .. 12b+11: waves 0..3 dot
-// three gate rows each, waves 4..7 the matching up rows, and the scaled dots
-// meet in LDS, where threads 0..11 form SiLU(gate)*up. The row loads of all
-// eight waves are issued before any weight load (the first barrier).
-// grid (9216/12, count), block 512.
+// A workgroup of eight waves owns inner rows 36b .. 36b+35, so the model's
+// 9216 rows fill the 256 CUs with one workgroup each and the input row is
+// staged and normalized once per CU: waves 0..3 dot nine gate rows each,
+// waves 4..7 the matching up rows, each as a RowStream with three rows in
+// flight. The scaled dots meet in LDS, where threads 0..35 form
+// SiLU(gate)*up. grid (9216/36, count), block 512.
+constexpr int GATEUP_ROWS = 9;  // rows per wave
+constexpr int GATEUP_DEPTH = 3; // rows of loads in flight per wave
+
 template <bool LUT>
 __global__ void __launch_bounds__(512)
 k_gateup_silu(const uint8_t* __restrict__ Wgate, const uint8_t* __restrict__ Wup, float2 scales,
     const float* __restrict__ gamma, const float* __restrict__ xin, float* __restrict__ gated)
 {
     constexpr int T = 512;
+    constexpr int NR = 4 * GATEUP_ROWS;
     __shared__ float lut_s[LUT ? 256 : 1];
     __shared__ float4 xin_s[3 * 4 * 64];
-    __shared__ float prod[2][12];
+    __shared__ float prod[2][NR];
     __shared__ float r_s;
     if constexpr (LUT) {
-        fill_lut(lut_s);  // published by the barriers below, before any dot
+        fill_lut(lut_s);  // published by the norm's barriers, before any dot
     }
     const uint32_t tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const uint32_t t = blockIdx.y;
     const bool up = wave >= 4;
-    const uint32_t k0 = 3 * (wave & 3);
-    const uint32_t base = blockIdx.x * 12;
+    const uint32_t k0 = GATEUP_ROWS * (wave & 3);
+    const uint8_t* W = up ? Wup : Wgate;
+    uint32_t rr[GATEUP_ROWS];
+#pragma unroll
+    for (int r = 0; r < GATEUP_ROWS; r++) {
+        rr[r] = blockIdx.x * NR + k0 + r;
+    }
     float2 xv[1536 / T], gv[1536 / T];
     norm_load<T>(xin + (size_t)t * LH_HIDDEN, gamma, xv, gv);
-    __syncthreads();
-    const uint32_t rr[3] = {base + k0, base + k0 + 1, base + k0 + 2};
-    WVec<K_FP8> wv[3][3];
-    issue_rows<K_FP8, 3, 3>(up ? Wup : Wgate, rr, wv);
+    RowStream<K_FP8, 3, GATEUP_ROWS, GATEUP_DEPTH> stream;
+    stream.start(W, rr);
     norm_commit<T>(xv, gv, xin_s, &r_s);
-    float dots[3];
-    dot_rows<K_FP8, LUT, 3, 3>(wv, xin_s, lut_s, dots);
+    float dots[GATEUP_ROWS];
+    stream.template run<LUT>(W, rr, xin_s, lut_s, dots);
     if (lane == 0) {
         const float scale = up ? scales.y : scales.x;
 #pragma unroll
-        for (int r = 0; r < 3; r++) {
+        for (int r = 0; r < GATEUP_ROWS; r++) {
             prod[up][k0 + r] = dots[r] * scale;
         }
     }
     __syncthreads();
-    if (tid < 12) {
-        gated[(size_t)t * LH_INNER + base + tid] = silu(prod[0][tid]) * prod[1][tid];
+    if (tid < NR) {
+        gated[(size_t)t * LH_INNER + blockIdx.x * NR + tid] = silu(prod[0][tid]) * prod[1][tid];
     }
 }
 
@@ -694,7 +754,8 @@ extern "C" int lh_launch_gateup_silu(int lookup, const uint8_t* Wgate, const uin
     float sg, float su, const float* gamma, const float* x, uint32_t count, float* gated,
     hipStream_t s)
 {
-    dim3 grid(LH_INNER / 12, count);
+    static_assert(LH_INNER % (4 * GATEUP_ROWS) == 0, "gate/up rows per workgroup");
+    dim3 grid(LH_INNER / (4 * GATEUP_ROWS), count);
     float2 scales = make_float2(sg, su);
     if (lookup) {
         hipLaunchKernelGGL(k_gateup_silu<true>, grid, dim3(512), 0, s, Wgate, Wup, scales, gamma, x, gated);
