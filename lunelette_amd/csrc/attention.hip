@@ -90,10 +90,7 @@ k_attn_blocks(const float* __restrict__ q, const float* __restrict__ kcache,
     }
 #pragma unroll
     for (int hh = 0; hh < 4; hh++) {
-        // (c0 + c1) + (c2 + c3); IEEE addition is commutative, so every lane of
-        // the quad ends with the same bits.
-        float v = c[hh] + __shfl_xor(c[hh], 1, 64);
-        v = v + __shfl_xor(v, 2, 64);
+        const float v = quad_sum(c[hh]);  // (c0 + c1) + (c2 + c3)
         if (quarter == 0 && p < valid) {
             S[hh][p] = v * LH_SCORE_SCALE;
         }

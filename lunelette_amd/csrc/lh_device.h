@@ -71,12 +71,34 @@ __device__ __forceinline__ float wave_lane0(float v)
     return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(v)));
 }
 
+// Maximum over the 64 lanes, returned in every lane: the halving tree above
+// with fmaxf, then lane 0's value broadcast. The maximum does not depend on
+// the pairing (NaN lanes are ignored unless all are NaN); only the sign of a
+// zero maximum may differ from another pairing, and every use subtracts it.
 __device__ __forceinline__ float wave_max64(float v)
 {
-    for (int s = 32; s >= 1; s >>= 1) {
-        v = fmaxf(v, __shfl_xor(v, s, 64));
-    }
-    return v;
+    const uint32_t u = __float_as_uint(v);
+    const auto p32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+    v = fmaxf(v, __uint_as_float(p32[1]));
+    const uint32_t w = __float_as_uint(v);
+    const auto p16 = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+    v = fmaxf(v, __uint_as_float(p16[1]));
+    v = fmaxf(v, dpp_row_shl(v, 8));
+    v = fmaxf(v, dpp_row_shl(v, 4));
+    v = fmaxf(v, dpp_row_shl(v, 2));
+    v = fmaxf(v, dpp_row_shl(v, 1));
+    return wave_lane0(v);
+}
+
+// (c0 + c1) + (c2 + c3) over the four lanes of each aligned quad, in every
+// lane of the quad (IEEE addition is commutative, so lane q's c_q + c_(q^1)
+// has the bits of lane 0's c0 + c1): two DPP quad permutations.
+__device__ __forceinline__ float quad_sum(float c)
+{
+    const float v = c + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(c), 0xB1, 0xf, 0xf,
+        false));  // quad_perm [1,0,3,2]
+    return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xf, 0xf,
+        false));  // quad_perm [2,3,0,1]
 }
 
 // exp(x): Cody & Waite additive range reduction (Cody, Waite, "Software
