@@ -166,11 +166,44 @@ def time_operators(lh, syn, seed, repeats):
         ms = ctypes.c_float()
         lh.check(lib.lh_event_elapsed_ms(start, stop, ctypes.byref(ms)))
         result[name] = ms.value * 1e3 / n  # microseconds per launch
+    # Pure-read floors: the same weight bytes (q|k|v, o, gate and up together,
+    # down) streamed by lh_read_floor from the same rotating copies, the best
+    # grid and loads-in-flight that divide the size.
+    spans = {"qkv_rope": (first["qkv"], qkv.nbytes), "o_residual": (first["o"], host["o"].nbytes),
+             "gateup_silu": (first["gate"], host["gate"].nbytes + host["up"].nbytes),
+             "down_residual": (first["down"], host["down"].nbytes)}
+    assert first["up"] == first["gate"] + host["gate"].nbytes
+    sink = lh.DeviceBuffer(16384 * 4)
+    floors = {}
+    for name, (base, nbytes) in spans.items():
+        best = None
+        for grid in (256, 384, 512, 576, 768, 1024, 1152, 1536, 1728, 2048, 2304, 3072):
+            for unroll in (1, 2, 4, 8):
+                if nbytes % (grid * 4 * 64 * 16 * unroll):
+                    continue
+                def launch(i):
+                    lh.check(lib.lh_read_floor(base + (i % copies) * per_layer, nbytes, grid,
+                                               unroll, sink.ptr, stream), "read floor")
+                for i in range(copies):
+                    launch(i)
+                n = copies * repeats
+                lh.check(lib.lh_event_record(start, stream))
+                for i in range(n):
+                    launch(i)
+                lh.check(lib.lh_event_record(stop, stream))
+                ms = ctypes.c_float()
+                lh.check(lib.lh_event_elapsed_ms(start, stop, ctypes.byref(ms)))
+                us = ms.value * 1e3 / n
+                if best is None or us < best[0]:
+                    best = (us, grid, unroll)
+        floors[name] = {"floor_us": round(best[0], 3), "grid": best[1], "unroll": best[2],
+                        "kernel_us": round(result[name], 3),
+                        "ratio": round(result[name] / best[0], 3)}
     lib.lh_event_destroy(start)
     lib.lh_event_destroy(stop)
     lib.lh_workspace_destroy(ws)
     lib.lh_stream_destroy(stream)
-    return result
+    return result, floors
 
 
 def time_attention(lh, syn, seed, lengths=(550, 4352, 16000), copies=16, repeats=4):
@@ -535,7 +568,7 @@ def main():
         out["tokens_compared"] = n
     out["config"]["prefill_activations"] = {k: v[1] for k, v in PREFILL_PLANES.items()}
     if not args.no_operators:
-        ops = time_operators(lh, syn, args.seed, args.op_repeats)
+        ops, floors = time_operators(lh, syn, args.seed, args.op_repeats)
         fp8_us = sum(ops[k] for k in FP8_BYTES)
         fp8_gbps = sum(FP8_BYTES.values()) / (fp8_us * 1e-6) / 1e9
         dom = "gateup_silu"
@@ -543,13 +576,15 @@ def main():
         achieved = dom_bytes / (ops[dom] * 1e-6) / 1e9
         out["operators_us_at_pos4351"] = {k: round(v, 3) for k, v in ops.items()}
         out["fp8_matvec"] = {"GBps": round(fp8_gbps, 1), "frac_hbm": round(fp8_gbps / HBM_PEAK_GBPS, 4),
-                             "bytes_per_layer": sum(FP8_BYTES.values())}
+                             "bytes_per_layer": sum(FP8_BYTES.values()),
+                             "read_floors": floors}
         out["roofline"] = {"bound": "hbm", "kernel": "k_gateup_silu (RMSNorm + gate/up FP8 "
                            "row dots + SiLU*up)", "achieved": round(achieved, 1),
                            "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": pmc_traffic(),
                            "bytes_per_launch": dom_bytes, "avg_us": round(ops[dom], 3)}
         log("operators (us): %s" % out["operators_us_at_pos4351"])
+        log("read floors: %s" % floors)
         out["decode_attention"] = time_attention(lh, syn, args.seed)
         log("decode attention: %s" % out["decode_attention"])
         out["fp8_linear_9216x3072"] = fp8_linear(lh, syn, args.seed)

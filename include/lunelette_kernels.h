@@ -65,6 +65,14 @@ int lh_rope(const float *d_x, const float *d_cos, const float *d_sin, const floa
     float *d_out, size_t width, size_t tokens, void *stream);
 /* E4M3FN decode of n codes (hardware conversion used by the kernels). */
 int lh_fp8_decode(const uint8_t *d_codes, float *d_out, size_t n, void *stream);
+/* Streaming-read measurement (no counterpart in the reference): reads `bytes`
+ * from d_src with 16-byte non-temporal loads in `grid` workgroups of four
+ * waves, `unroll` loads (1, 2, 4 or 8) in flight per lane, folded so that no
+ * load is dead; d_sink (grid*4 words) is written only for an improbable fold
+ * value. bytes must be a multiple of grid*4*64*16*unroll. bench.py times it
+ * over the decode weight shapes as each kernel's pure-read floor. */
+int lh_read_floor(const void *d_src, size_t bytes, unsigned grid, unsigned unroll,
+    unsigned *d_sink, void *stream);
 /* Device exp and SiLU used by the kernels (bitwise checks against the oracle). */
 int lh_expf(const float *d_x, float *d_out, size_t n, void *stream);
 

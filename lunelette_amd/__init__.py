@@ -143,6 +143,7 @@ def _load(path):
     _proto(l, "lh_bf16_matvec", i, c_void, c_void, c_void, c_size, c_size, c_size, c_void)
     _proto(l, "lh_rmsnorm", i, c_void, c_void, c_void, c_size, c_size, c_void)
     _proto(l, "lh_element", i, i, c_void, c_void, c_void, c_size, c_void)
+    _proto(l, "lh_read_floor", i, c_void, c_size, ctypes.c_uint, ctypes.c_uint, c_void, c_void)
     _proto(l, "lh_rope", i, c_void, c_void, c_void, c_void, c_void, c_size, c_size, c_void)
     _proto(l, "lh_fp8_decode", i, c_void, c_void, c_size, c_void)
     _proto(l, "lh_expf", i, c_void, c_void, c_size, c_void)

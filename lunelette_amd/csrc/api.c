@@ -256,6 +256,21 @@ int lh_element(int mode, const float *d_first, const float *d_second, float *d_o
         "element");
 }
 
+int lh_read_floor(const void *d_src, size_t bytes, unsigned grid, unsigned unroll,
+    unsigned *d_sink, void *stream)
+{
+    const size_t unit = (size_t)grid * 4 * 64 * 16 * unroll;
+    if (!d_src || !d_sink || !grid || grid > 65536 ||
+        (unroll != 1 && unroll != 2 && unroll != 4 && unroll != 8) || !bytes ||
+        bytes % unit) {
+        lh_set_error("read_floor: pointers, grid 1..65536, unroll 1/2/4/8 and bytes a multiple "
+            "of grid*4*64*16*unroll required");
+        return -1;
+    }
+    return launched(lh_launch_read_floor(d_src, bytes, grid, unroll, d_sink,
+        (hipStream_t)stream), "read floor");
+}
+
 int lh_rope(const float *d_x, const float *d_cos, const float *d_sin, const float *d_qfactor,
     float *d_out, size_t width, size_t tokens, void *stream)
 {

@@ -55,6 +55,9 @@ int lh_launch_rope_append(const float *q_raw, const float *k_raw, const float *v
     const lh_step_params *params, uint32_t count, float *q, float *kcache_layer,
     float *vcache_layer, uint32_t capacity, hipStream_t s);
 int lh_launch_fp8_decode(const uint8_t *codes, float *out, size_t n, hipStream_t s);
+/* Streaming read of bytes (a multiple of grid*4*64*16*unroll; unroll 1, 2, 4, 8). */
+int lh_launch_read_floor(const void *src, size_t bytes, uint32_t grid, uint32_t unroll,
+    uint32_t *sink, hipStream_t s);
 int lh_launch_expf(const float *x, float *out, size_t n, hipStream_t s);
 
 /* Thread-local diagnostic shared by the C ABI layers. */

@@ -351,15 +351,27 @@ k_rows(const void* __restrict__ W, float scale, const float* __restrict__ x, flo
     for (int r = 0; r < R; r++) {
         rr[r] = row0 + r;
     }
-    WVec<KIND> wv[R][NCH];
-    issue_rows<KIND, NCH, R>(W, rr, wv);
+    // FP8 rows stream with one row of loads in flight ahead of the row being
+    // dotted (RowStream); with all R rows requested at once the model's o
+    // and down projections ran 6% and 8% slower. Other kinds keep every row
+    // in flight.
+    constexpr bool STREAM = KIND == K_FP8 && R > 1;
+    RowStream<KIND, NCH, R, 1> stream;
+    WVec<KIND> wv[STREAM ? 1 : R][NCH];
+    if constexpr (STREAM) {
+        stream.start(W, rr);
+    } else {
+        issue_rows<KIND, NCH, R>(W, rr, wv);
+    }
     stage_commit<NCH>(xv, xin_s);
     // The epilogue's residual values are requested now, after the row is
     // staged, so they return behind the weights instead of costing a memory
     // round trip after the dots. Written as assembly because the compiler
-    // sinks an ordinary load to its use; loads complete in issue order, so
-    // the compiler's own waits for the weights stay sufficient (they wait one
-    // load longer), and the values are read only after waiting for all loads.
+    // sinks an ordinary load to its use. Loads complete in issue order, so
+    // the compiler's own waits for the weights, which do not count these,
+    // stay sufficient: for a row issued before them they wait longer, for a
+    // row issued after them exactly. The values are read only after waiting
+    // for all loads.
     float res[R];
     if constexpr (RES) {
 #pragma unroll
@@ -369,7 +381,11 @@ k_rows(const void* __restrict__ W, float scale, const float* __restrict__ x, flo
         }
     }
     float dots[R];
-    dot_rows<KIND, LUT, NCH, R>(wv, xin_s, lut_s, dots);
+    if constexpr (STREAM) {
+        stream.template run<LUT>(W, rr, xin_s, lut_s, dots);
+    } else {
+        dot_rows<KIND, LUT, NCH, R>(wv, xin_s, lut_s, dots);
+    }
     if constexpr (RES) {
 #pragma unroll
         for (int r = 0; r < R; r++) {

@@ -18,6 +18,38 @@ __global__ void k_element(int mode, const float* __restrict__ a, const float* __
     out[i] = mode == 0 ? v + b[i] : (mode == 1 ? silu(v) : v * b[i]);
 }
 
+// Streaming-read measurement: `words` 16-byte words from src, wave w reading
+// the contiguous range [w, w+1) * words / waves with U non-temporal loads in
+// flight per lane, folded by XOR so that no load is dead; a lane writes sink
+// only if its fold equals a value chosen so that it practically never does.
+typedef uint32_t rf_u32x4 __attribute__((ext_vector_type(4)));
+
+template <int U>
+__global__ void __launch_bounds__(256)
+k_read_floor(const rf_u32x4* __restrict__ src, size_t words, uint32_t* __restrict__ sink)
+{
+    const size_t waves = (size_t)gridDim.x * 4;
+    const size_t wave = (size_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    const uint32_t lane = threadIdx.x & 63;
+    const size_t per_wave = words / waves;   // a multiple of 64 * U
+    const rf_u32x4* p = src + wave * per_wave + lane;
+    uint32_t acc = 0;
+    for (size_t i = 0; i < per_wave; i += 64 * U) {
+        rf_u32x4 v[U];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            v[u] = __builtin_nontemporal_load(p + i + 64 * u);
+        }
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+        }
+    }
+    if (acc == 0x9e3779b9u) {
+        sink[wave] = acc;
+    }
+}
+
 // SiLU(gate)*up in one pass.
 __global__ void k_silu_mul(const float* __restrict__ gate, const float* __restrict__ up,
     float* __restrict__ out, size_t n)
@@ -144,5 +176,20 @@ extern "C" int lh_launch_fp8_decode(const uint8_t* codes, float* out, size_t n, 
 extern "C" int lh_launch_expf(const float* x, float* out, size_t n, hipStream_t s)
 {
     hipLaunchKernelGGL(k_expf, grid_for(n), dim3(256), 0, s, x, out, n);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+extern "C" int lh_launch_read_floor(const void* src, size_t bytes, uint32_t grid, uint32_t unroll,
+    uint32_t* sink, hipStream_t s)
+{
+    const rf_u32x4* w = static_cast<const rf_u32x4*>(src);
+    const size_t words = bytes / 16;
+    switch (unroll) {
+    case 1: hipLaunchKernelGGL(k_read_floor<1>, dim3(grid), dim3(256), 0, s, w, words, sink); break;
+    case 2: hipLaunchKernelGGL(k_read_floor<2>, dim3(grid), dim3(256), 0, s, w, words, sink); break;
+    case 4: hipLaunchKernelGGL(k_read_floor<4>, dim3(grid), dim3(256), 0, s, w, words, sink); break;
+    case 8: hipLaunchKernelGGL(k_read_floor<8>, dim3(grid), dim3(256), 0, s, w, words, sink); break;
+    default: return -1;
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

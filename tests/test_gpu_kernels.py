@@ -202,3 +202,19 @@ def test_head_nonfinite_flag(gpu):
         assert int(flag.download(np.uint32)[0]) == want, name
         assert np.isfinite(b).all() == (want == 0), name
         del emb
+
+
+def test_read_floor_runs_and_validates(gpu):
+    """The streaming-read measurement kernel bench.py times as the decode
+    kernels' floor: it accepts sizes that the grid and loads-in-flight divide,
+    refuses others, and leaves its sink alone for ordinary data."""
+    nbytes = 256 * 4 * 64 * 16 * 8 * 3
+    src = lh.DeviceBuffer.from_array(np.zeros(nbytes // 4, np.float32))
+    sink = lh.DeviceBuffer.from_array(np.zeros(16384, np.uint32))
+    for grid, unroll in ((256, 1), (256, 8), (768, 2), (1536, 4)):
+        lh.check(gpu.lh_read_floor(src.ptr, nbytes, grid, unroll, sink.ptr, None))
+    lh.check(gpu.lh_device_synchronize())
+    assert not sink.download(np.uint32).any()
+    for grid, unroll, size in ((256, 3, nbytes), (0, 1, nbytes), (256, 1, nbytes - 16),
+                               (4096, 8, nbytes)):
+        assert gpu.lh_read_floor(src.ptr, size, grid, unroll, sink.ptr, None) == -1
