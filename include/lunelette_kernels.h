@@ -107,9 +107,15 @@ enum {
     LH_PATH_MFMA = 4      /* multi-token: MFMA GEMM projections */
 };
 
+/* KV cache of one layer (capacity a multiple of 64): d_values is
+ * [8][capacity][128] FP32 rows; d_keys holds the same [8][capacity][128]
+ * values with each 64-position tile's 16-byte words permuted: dims
+ * 32q + 4i .. 32q + 4i + 3 of the tile's position p (0..63) sit at word
+ * ((p / 16) * 8 + i) * 64 + (p % 16) * 4 + q of the tile. */
+
 /* One decoder layer (src/metal_encode.m:124-187) over d_x [count][3072] in
  * place, at positions [length, length+count) set by lh_workspace_set_tokens;
- * K/V rows are appended into d_keys/d_values ([8][capacity][128]). */
+ * K/V rows are appended into d_keys/d_values (layout above). */
 int lh_layer_forward(const lh_layer_weights *w, float *d_x, float *d_keys, float *d_values,
     lh_workspace *ws, int path, void *stream);
 /* One operator of the decode-schedule layer (the analogue of
@@ -126,14 +132,14 @@ int lh_layer_operator(int op, const lh_layer_weights *w, float *d_x, float *d_ke
     float *d_values, lh_workspace *ws, void *stream);
 /* Causal GQA attention (src/metal_kernels.metal:80-132 scores + attend) of
  * the workspace's count query rows d_q [count][4096] over positions
- * [0, length+t] of d_keys/d_values ([8][capacity][128]) into d_out. */
+ * [0, length+t] of d_keys/d_values (layout above) into d_out. */
 int lh_attention(const float *d_q, const float *d_keys, const float *d_values, lh_workspace *ws,
     float *d_out, void *stream);
 /* No counterpart in the reference. For callers that cannot allocate device
  * memory (code under HIP graph capture, tight serving loops, harnesses that
  * forbid hipMalloc): lh_attention without a workspace. Query rows d_q
  * [count][4096] attend positions [0, length + t] of d_keys/d_values
- * ([8][capacity][128]); bitwise the result of lh_attention for the same
+ * (layout above); bitwise the result of lh_attention for the same
  * length and count. The split-KV partials and the step header live in one
  * static device array per GPU, held until the process ends: count * capacity
  * must not exceed 65536 (17.0 MB of scratch), larger calls are refused. Calls that

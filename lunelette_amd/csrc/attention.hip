@@ -14,8 +14,9 @@
 //   left to right; out[d] = A[d] / T.
 //
 // KV layout [kv_head][capacity][128] per layer: a block's K or V tile is one
-// contiguous 32 KiB read. K goes straight to registers (lane = position,
-// quarter of the head dimension), V is staged in LDS for the P.V chains, so a
+// contiguous 32 KiB read (K's words permuted inside the tile, lh_ktile_word).
+// K goes straight to registers (lane = position, quarter of the head
+// dimension), V is staged in LDS for the P.V chains, so a
 // workgroup holds 35 KiB of LDS and four fit on a CU. Rows at or past
 // length+t+1 never enter arithmetic. The combine runs as its own kernel: the
 // kernel boundary publishes the partials device-wide, where an in-kernel
@@ -47,13 +48,14 @@ k_attn_blocks(const float* __restrict__ q, const float* __restrict__ kcache,
     // ceil((length + count) / 64) blocks of a capacity that is a multiple of
     // 64, so all 64 rows are in bounds; rows past the valid count are never
     // used in arithmetic.
-    // K: wave w covers positions 16w..16w+15; lane = 4 * (position - 16w) + quarter.
+    // K: wave w covers positions 16w..16w+15; lane = 4 * (position - 16w) +
+    // quarter, and the tile's word order (lh_ktile_word) makes each of the
+    // eight loads one contiguous 1 KiB read.
     const uint32_t p = 16 * wave + (lane >> 2), quarter = lane & 3;
     float4 k[8];
-    const float4* krow = kb + (size_t)p * (LH_HEAD_DIM / 4) + 8 * quarter;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        k[i] = krow[i];
+        k[i] = kb[(wave * 8 + i) * 64 + lane];
     }
     float4 vr[8];
 #pragma unroll
@@ -521,10 +523,16 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             const uint32_t idx = tid + 256 * i, row = idx >> 5, c4 = idx & 31;
+            // K word idx = tid + 256 i of the tile (lh_ktile_word order) holds
+            // position (idx >> 9) * 16 + (idx & 63) / 4 = 16 (i / 2) + lane / 4,
+            // dims 32 (idx & 3) + 4 ((idx >> 6) & 7) = 32 (lane % 4) + 4 (wave + 4 (i % 2)).
+            const uint32_t krow = 16 * (i >> 1) + (lane >> 2);
+            const uint32_t kc4 = 8 * (lane & 3) + wave + 4 * (i & 1);
             const bool live = b * LH_ATTN_BLOCK + row <= visible;
+            const bool klive = b * LH_ATTN_BLOCK + krow <= visible;
             const fa_floatx4 zero = fa_floatx4{0.f, 0.f, 0.f, 0.f};
-            const fa_floatx4 kk = live ? kr[i] : zero, vv = live ? vr[i] : zero;
-            *reinterpret_cast<fa_floatx4*>(&Ks[row * FA_KS + 4 * c4]) = kk;
+            const fa_floatx4 kk = klive ? kr[i] : zero, vv = live ? vr[i] : zero;
+            *reinterpret_cast<fa_floatx4*>(&Ks[krow * FA_KS + 4 * kc4]) = kk;
             float* vd = &Vs[row * FA_VS + 4 * c4];
             vd[0] = vv.x;
             vd[1] = vv.y;

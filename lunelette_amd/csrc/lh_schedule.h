@@ -59,7 +59,8 @@ typedef struct {
     lh_token_params tokens[LH_MAX_BLOCK];
 } lh_step_params;
 
-/* Device KV layout: [layer][kv_head][capacity][128] FP32, K rotated, V raw. */
+/* Device KV layout: [layer][kv_head][capacity][128] FP32, K rotated (permuted
+ * within 64-position tiles, below), V raw. */
 #ifdef __HIPCC__
 #define LH_HOST_DEVICE __host__ __device__
 #else
@@ -69,6 +70,26 @@ static inline LH_HOST_DEVICE uint64_t lh_kv_index(uint64_t capacity, uint32_t la
     uint64_t position)
 {
     return (((uint64_t)layer * LH_KV_HEADS + kv_head) * capacity + position) * LH_HEAD_DIM;
+}
+
+/* K is stored in 64-position tiles (the attention block) at the same place
+ * as that layout, permuted inside each tile: the 16-byte word holding dims
+ * 32q + 4i .. 32q + 4i + 3 of the tile's position p is word
+ * ((p / 16) * 8 + i) * 64 + (p % 16) * 4 + q. A wave whose lane 4(p % 16) + q
+ * owns position 16w + p % 16, quarter q then reads its eight words as eight
+ * contiguous 1 KiB loads. V keeps the row layout. */
+static inline LH_HOST_DEVICE uint32_t lh_ktile_word(uint32_t p, uint32_t q, uint32_t i)
+{
+    return ((p >> 4) * 8 + i) * 64 + (p & 15) * 4 + q;
+}
+
+/* Float index of K's dim d at a position. */
+static inline LH_HOST_DEVICE uint64_t lh_k_index(uint64_t capacity, uint32_t layer, uint32_t kv_head,
+    uint64_t position, uint32_t d)
+{
+    const uint64_t tile = lh_kv_index(capacity, layer, kv_head, position & ~(uint64_t)63);
+    return tile + (uint64_t)lh_ktile_word((uint32_t)(position & 63), d >> 5, (d >> 2) & 7) * 4 +
+        (d & 3);
 }
 
 #endif

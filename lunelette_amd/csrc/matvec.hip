@@ -521,9 +521,8 @@ k_qkv_rope(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restr
                 qh[i] = out_lo;
                 qh[i + 64] = out_hi;
             } else {
-                float* kr = kcache + lh_kv_index(capacity, 0, head - 32, position);
-                kr[i] = out_lo;
-                kr[i + 64] = out_hi;
+                kcache[lh_k_index(capacity, 0, head - 32, position, i)] = out_lo;
+                kcache[lh_k_index(capacity, 0, head - 32, position, i + 64)] = out_hi;
             }
         } else {
             float* vr = vcache + lh_kv_index(capacity, 0, head - 40, position);

@@ -357,9 +357,10 @@ k_qkv_epilogue(const float* __restrict__ partial, size_t split_stride, float3 sc
         qh[i0 / 4] = make_float4(out_lo.x * f, out_lo.y * f, out_lo.z * f, out_lo.w * f);
         qh[i0 / 4 + 16] = make_float4(out_hi.x * f, out_hi.y * f, out_hi.z * f, out_hi.w * f);
     } else {
-        float4* kr = reinterpret_cast<float4*>(kcache + lh_kv_index(capacity, 0, head - 32, position));
-        kr[i0 / 4] = out_lo;
-        kr[i0 / 4 + 16] = out_hi;
+        *reinterpret_cast<float4*>(kcache + lh_k_index(capacity, 0, head - 32, position, i0)) =
+            out_lo;
+        *reinterpret_cast<float4*>(kcache + lh_k_index(capacity, 0, head - 32, position, i0 + 64)) =
+            out_hi;
     }
 }
 

@@ -103,9 +103,9 @@ __global__ void k_rope_append(const float* __restrict__ q_raw, const float* __re
         qout[(size_t)t * LH_QUERY + i] = rope_at(qr, tp->cosine, tp->sine, i) * tp->qfactor;
     }
     for (uint32_t k = threadIdx.x; k < LH_KV; k += blockDim.x) {
-        const uint64_t at = lh_kv_index(capacity, 0, k >> 7, position) + (k & 127u);
-        kcache[at] = rope_at(kr, tp->cosine, tp->sine, k);
-        vcache[at] = vr[k];
+        kcache[lh_k_index(capacity, 0, k >> 7, position, k & 127u)] =
+            rope_at(kr, tp->cosine, tp->sine, k);
+        vcache[lh_kv_index(capacity, 0, k >> 7, position) + (k & 127u)] = vr[k];
     }
 }
 

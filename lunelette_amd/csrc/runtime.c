@@ -930,14 +930,36 @@ int lunelette_metal_read_kv(const lunelette_metal *context, size_t layer, int ki
         position > rt->limits.context || count > rt->limits.context - position) {
         return -1;
     }
-    const float *base = (kind ? rt->d_values : rt->d_keys) +
-        (size_t)layer * LH_KV_HEADS * rt->limits.context * LH_HEAD_DIM;
-    for (size_t p = 0; p < count; p++) {
-        for (size_t h = 0; h < LH_KV_HEADS; h++) {
-            const float *src = base + lh_kv_index(rt->limits.context, 0, (uint32_t)h, position + p);
-            if (hipMemcpy(out + p * LH_KV + h * LH_HEAD_DIM, src, LH_HEAD_DIM * sizeof(float),
+    const size_t C = rt->limits.context;
+    const float *base = (kind ? rt->d_values : rt->d_keys) + (size_t)layer * LH_KV_HEADS * C *
+        LH_HEAD_DIM;
+    if (kind) {
+        for (size_t p = 0; p < count; p++) {
+            for (size_t h = 0; h < LH_KV_HEADS; h++) {
+                const float *src = base + lh_kv_index(C, 0, (uint32_t)h, position + p);
+                if (hipMemcpy(out + p * LH_KV + h * LH_HEAD_DIM, src, LH_HEAD_DIM * sizeof(float),
+                        hipMemcpyDeviceToHost) != hipSuccess) {
+                    return -1;
+                }
+            }
+        }
+        return 0;
+    }
+    /* K: copy each 64-position tile the range touches, then gather its rows
+     * out of the tile's word order. */
+    float tile[LH_ATTN_BLOCK * LH_HEAD_DIM];
+    for (size_t h = 0; h < LH_KV_HEADS; h++) {
+        for (size_t t0 = position & ~(size_t)63; t0 < position + count; t0 += LH_ATTN_BLOCK) {
+            if (hipMemcpy(tile, base + lh_kv_index(C, 0, (uint32_t)h, t0), sizeof tile,
                     hipMemcpyDeviceToHost) != hipSuccess) {
                 return -1;
+            }
+            for (size_t p = t0 < position ? position : t0;
+                 p < t0 + LH_ATTN_BLOCK && p < position + count; p++) {
+                for (uint32_t d = 0; d < LH_HEAD_DIM; d++) {
+                    out[(p - position) * LH_KV + h * LH_HEAD_DIM + d] =
+                        tile[lh_ktile_word((uint32_t)(p - t0), d >> 5, (d >> 2) & 7) * 4 + (d & 3)];
+                }
             }
         }
     }

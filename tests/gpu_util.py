@@ -60,6 +60,27 @@ def kv_from_device_layout(khm, position, count):
         count, 1024)
 
 
+def k_tiles(khm):
+    """[8][capacity][128] head-major K -> the device's tiled K: inside each
+    64-position tile, dims 32q + 4i .. +3 of position p at 16-byte word
+    ((p // 16) * 8 + i) * 64 + (p % 16) * 4 + q (lh_ktile_word)."""
+    h, c, _ = khm.shape
+    t = khm.reshape(h, c // 64, 4, 16, 4, 8, 4)        # head, tile, p//16, p%16, q, i, float
+    return np.ascontiguousarray(t.transpose(0, 1, 2, 5, 3, 4, 6)).reshape(h, c, 128)
+
+
+def k_untile(tiled):
+    """Inverse of k_tiles."""
+    h, c, _ = tiled.shape
+    t = tiled.reshape(h, c // 64, 4, 8, 16, 4, 4)      # head, tile, p//16, i, p%16, q, float
+    return np.ascontiguousarray(t.transpose(0, 1, 2, 4, 5, 3, 6)).reshape(h, c, 128)
+
+
+def keys_to_device(kpm, capacity, tail=0.0):
+    """Position-major K rows -> the device's K cache layout."""
+    return k_tiles(kv_to_device_layout(kpm, capacity, tail))
+
+
 def attention_on_device(gpu, entry, q, kpm, vpm, length, count, capacity, tail=0.0):
     """Run an attention entry point (lh_attention or lh_attention_mfma) on
     position-major q/K/V (cache rows past them hold `tail`); returns
@@ -71,7 +92,7 @@ def attention_on_device(gpu, entry, q, kpm, vpm, length, count, capacity, tail=0
         lh.check(gpu.lh_workspace_set_tokens(ws, ids.ctypes.data_as(lh.c_int64_p), length, count,
                                              None))
         d_q = lh.DeviceBuffer.from_array(q)
-        keys = lh.DeviceBuffer.from_array(kv_to_device_layout(kpm, capacity, tail))
+        keys = lh.DeviceBuffer.from_array(keys_to_device(kpm, capacity, tail))
         values = lh.DeviceBuffer.from_array(kv_to_device_layout(vpm, capacity, tail))
         out = lh.DeviceBuffer(count * 4096 * 4 + 16)
         lh.check(gpu.lh_memset_device(out.ptr, 0x5a, out.nbytes))

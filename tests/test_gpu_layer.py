@@ -39,7 +39,7 @@ def layer_host():
 def run_layer(gpu, host, x, kv_prefix_k, kv_prefix_v, length, count, capacity, path,
               resident=False):
     dev = gpu_util.DeviceLayer(host, resident=resident)
-    keys = lh.DeviceBuffer.from_array(gpu_util.kv_to_device_layout(kv_prefix_k, capacity))
+    keys = lh.DeviceBuffer.from_array(gpu_util.keys_to_device(kv_prefix_k, capacity))
     values = lh.DeviceBuffer.from_array(gpu_util.kv_to_device_layout(kv_prefix_v, capacity))
     d_x = lh.DeviceBuffer.from_array(x)
     ws = gpu.lh_workspace_create(capacity, max(count, 1))
@@ -52,7 +52,7 @@ def run_layer(gpu, host, x, kv_prefix_k, kv_prefix_v, length, count, capacity, p
                  "layer_forward")
         lh.check(gpu.lh_device_synchronize())
         out = d_x.download(np.float32)
-        k = keys.download(np.float32).reshape(8, capacity, 128)
+        k = gpu_util.k_untile(keys.download(np.float32).reshape(8, capacity, 128))
         v = values.download(np.float32).reshape(8, capacity, 128)
     finally:
         gpu.lh_workspace_destroy(ws)
@@ -114,7 +114,7 @@ def attention_on_device(gpu, q, kpm, vpm, length, count, capacity):
         lh.check(gpu.lh_workspace_set_tokens(ws, ids.ctypes.data_as(lh.c_int64_p), length, count,
                                              None))
         d_q = lh.DeviceBuffer.from_array(q)
-        keys = lh.DeviceBuffer.from_array(gpu_util.kv_to_device_layout(kpm, capacity))
+        keys = lh.DeviceBuffer.from_array(gpu_util.keys_to_device(kpm, capacity))
         values = lh.DeviceBuffer.from_array(gpu_util.kv_to_device_layout(vpm, capacity))
         out = lh.DeviceBuffer(count * 4096 * 4 + 16)
         lh.check(gpu.lh_memset_device(out.ptr, 0x5a, out.nbytes))
@@ -135,7 +135,7 @@ def test_attention_repeated_launches_one_workspace(gpu):
     total = 3000
     kpm = rng.normal(size=(total, 1024)).astype(np.float32)
     vpm = rng.normal(size=(total, 1024)).astype(np.float32)
-    keys = lh.DeviceBuffer.from_array(gpu_util.kv_to_device_layout(kpm, capacity))
+    keys = lh.DeviceBuffer.from_array(gpu_util.keys_to_device(kpm, capacity))
     values = lh.DeviceBuffer.from_array(gpu_util.kv_to_device_layout(vpm, capacity))
     ws = gpu.lh_workspace_create(capacity, block)
     assert ws, lh.last_error()

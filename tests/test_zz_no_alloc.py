@@ -16,7 +16,7 @@ pytestmark = pytest.mark.gpu
 
 def run_noalloc(gpu, q, kpm, vpm, length, count, capacity):
     d_q = lh.DeviceBuffer.from_array(q)
-    keys = lh.DeviceBuffer.from_array(gpu_util.kv_to_device_layout(kpm, capacity))
+    keys = lh.DeviceBuffer.from_array(gpu_util.keys_to_device(kpm, capacity))
     values = lh.DeviceBuffer.from_array(gpu_util.kv_to_device_layout(vpm, capacity))
     out = lh.DeviceBuffer(count * 4096 * 4 + 16)
     lh.check(gpu.lh_memset_device(out.ptr, 0x5a, out.nbytes))
