@@ -422,6 +422,11 @@ def long_context(lh, syn, Runtime, seed, prefill_mode):
         rt.close()
 
 
+# The host threads this process may use, read before the GPU runtime starts
+# (it can narrow the main thread's affinity later).
+START_AFFINITY = len(os.sched_getaffinity(0))
+
+
 def cpu_model():
     try:
         with open("/proc/cpuinfo") as f:
@@ -442,7 +447,7 @@ def cpu_baseline(syn, seed, budget_s=10.0):
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     import oracle_lib
     o = oracle_lib.load()
-    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or len(os.sched_getaffinity(0))
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or START_AFFINITY
     t0 = time.time()
     layers = [syn.layer(seed, i) for i in range(26)]
     model = oracle_lib.HostModel(syn.embedding(seed).reshape(-1), syn.final_norm(seed), layers,
@@ -473,7 +478,7 @@ def cpu_baseline(syn, seed, budget_s=10.0):
                       "lanes), KV prefix seeded N(0,1); %d steps on 1 thread" % (
                           steps, prefix + 1, prefix + steps, share,
                           os.environ.get("OMP_PROC_BIND"), steps1),
-            "value_1thread": one, "host_cpus": len(os.sched_getaffinity(0)),
+            "value_1thread": one, "host_cpus": START_AFFINITY, "online_cpus": os.cpu_count(),
             "cpu_model": cpu_model()}
 
 
