@@ -35,6 +35,13 @@
 // - Workgroup ids deal the (weight tile, split) columns round-robin to the 8
 //   XCDs and run a column's token tiles back to back on one XCD, so the
 //   weight tile is read from HBM once per XCD and from L2 after that.
+// - k_gemm_f16_stream (gate|up): the same stages over a stream-K partition.
+//   The (256-row column, 64-column stage) units are dealt in equal
+//   contiguous ranges to groups of one workgroup per token tile on one XCD,
+//   two workgroups per CU, so every CU holds the same work: the 1152
+//   split-K workgroups of gate|up at 256 tokens ran 2.25 rounds of 512 and
+//   left most CUs idle in the last. A group writes a partial per column it
+//   covers; k_split_silu sums each column's 2 or 3 in K order.
 // - Scales and epilogues live in the consumers: k_qkv_epilogue (scales, RoPE,
 //   query factor, KV append), k_split_silu (SiLU(gate)*up feeding the down
 //   projection's split) and k_combine_residual (split-K sum in split order,
@@ -46,6 +53,7 @@
 
 #include <stdlib.h>
 
+#include <algorithm>
 #include <type_traits>
 
 namespace lh {
@@ -168,6 +176,52 @@ __device__ __forceinline__ float4 sum_splits_scaled(const float4* __restrict__ p
     return acc;
 }
 
+// sum_splits over the first n (1 <= n <= S) partials only, in the same
+// order (n = S: bitwise sum_splits); the rest are neither loaded nor added.
+template <int S>
+__device__ __forceinline__ float4 sum_segments(const float4* __restrict__ p, size_t stride4,
+    uint32_t n)
+{
+    float4 v[S];
+#pragma unroll
+    for (int s = 0; s < S; s++) {
+        v[s] = s == 0 || (uint32_t)s < n ? p[s * stride4] : make_float4(0.f, 0.f, 0.f, 0.f);
+    }
+    float4 acc = v[0];
+#pragma unroll
+    for (int s = 1; s < S; s++) {
+        if ((uint32_t)s < n) {
+            acc.x = acc.x + v[s].x;
+            acc.y = acc.y + v[s].y;
+            acc.z = acc.z + v[s].z;
+            acc.w = acc.w + v[s].w;
+        }
+    }
+    return acc;
+}
+
+// Stream-K partition of a product's (column, stage) units, column = 256
+// weight rows, stage = 64 K columns, in column-major order: group g of
+// `groups` takes units [begin(g), begin(g + 1)), equal to within one.
+__host__ __device__ inline uint32_t stream_begin(uint32_t g, uint32_t units, uint32_t groups)
+{
+    return (uint32_t)((uint64_t)g * units / groups);
+}
+
+// The group whose range holds `unit`.
+__host__ __device__ inline uint32_t stream_group(uint32_t unit, uint32_t units, uint32_t groups)
+{
+    return (uint32_t)((((uint64_t)unit + 1) * groups - 1) / units);
+}
+
+// Number of groups (partials) that cover column c of `stages` stages.
+__host__ __device__ inline uint32_t stream_segments(uint32_t c, uint32_t stages, uint32_t units,
+    uint32_t groups)
+{
+    return stream_group(c * stages + stages - 1, units, groups) -
+        stream_group(c * stages, units, groups) + 1;
+}
+
 // xs[p][m][k] for p < 3 from FP32 rows, no normalization. grid (count,
 // ceil(width / 2048)), block 256: thread j of the row takes columns
 // 8j .. 8j+7 (width a multiple of 8, rows 16-byte aligned).
@@ -269,7 +323,9 @@ k_residual_norm_split(const float* __restrict__ partial, size_t split_stride, fl
 // Down-projection input: SiLU(s_g * gate) * (s_u * up) (src/metal_encode.m:
 // 162-171) from the gate|up GEMM partials P[s][m][0..18432) (gate rows first),
 // summed in split order and multiplied by their row scale in_scale[t] (a power
-// of two, exact). Each of the down projection's DOWN_SPLITS K ranges (576
+// of two, exact). groups = 0: S equal K splits; otherwise the stream-K
+// partials of `groups` groups (gemm_stream_tile), S >= every column's
+// segment count. Each of the down projection's DOWN_SPLITS K ranges (576
 // columns) gets its own power of two 2^e (its largest magnitude into
 // [2^14, 2^15)) before the split into two FP16 planes; out_scale[t][g] = 2^-e,
 // which the down projection's consumers apply to that split's partial. grid
@@ -281,7 +337,7 @@ template <int S>
 __global__ void __launch_bounds__(192)
 k_split_silu(const float* __restrict__ partial, size_t split_stride, float2 scales,
     const float* __restrict__ in_scale, uint16_t* __restrict__ xs,
-    float* __restrict__ out_scale, uint32_t stride_tokens)
+    float* __restrict__ out_scale, uint32_t stride_tokens, uint32_t groups)
 {
     __shared__ float wmax[3];
     const uint32_t t = blockIdx.x, grp = blockIdx.y, j = threadIdx.x;
@@ -291,8 +347,12 @@ k_split_silu(const float* __restrict__ partial, size_t split_stride, float2 scal
     const float4* row = reinterpret_cast<const float4*>(partial + (size_t)t * MAX_N) + c4;
     const size_t s4 = split_stride / 4;
     const float ts = in_scale[t], sg = scales.x, su = scales.y;
-    const float4 g = scale4(sum_splits<S>(row, s4), ts);
-    const float4 u = scale4(sum_splits<S>(row + LH_INNER / 4, s4), ts);
+    // Segments of the gate column (c4 / 64) and of the up column 36 later.
+    constexpr uint32_t STAGES = LH_HIDDEN / BK, UNITS = MAX_N / GN * STAGES;
+    const uint32_t ng = groups ? stream_segments(c4 / 64, STAGES, UNITS, groups) : S;
+    const uint32_t nu = groups ? stream_segments(c4 / 64 + LH_INNER / GN, STAGES, UNITS, groups) : S;
+    const float4 g = scale4(sum_segments<S>(row, s4, ng), ts);
+    const float4 u = scale4(sum_segments<S>(row + LH_INNER / 4, s4, nu), ts);
     const float4 y = make_float4(silu(g.x * sg) * (u.x * su), silu(g.y * sg) * (u.y * su),
         silu(g.z * sg) * (u.z * su), silu(g.w * sg) * (u.w * su));
     const float m = wave_max64(active ? absmax4(y) : 0.0f);
@@ -397,6 +457,96 @@ __device__ __forceinline__ void fp8x16_to_f16x8x2(u32x4 u, f16x8& lo, f16x8& hi)
     hi = __builtin_bit_cast(f16x8, b);
 }
 
+// One 64-column stage of a wave's 64 tokens x 64 weight rows: A fragments
+// (mf, p, h) from the stage's LDS buffer, read one (p, h) group of four ahead
+// of its MFMAs; each fragment feeds the four weight fragments of w (this
+// lane's 16 FP8 codes of rows 16 nf + lane % 16, columns 16 (lane / 16) ..
+// +15 of the stage).
+template <int P>
+__device__ __forceinline__ void gemm_stage(const uint8_t* buf, const u32x4 (&w)[4], uint32_t lane,
+    floatx4 (&acc)[4][4])
+{
+    using V = typename std::conditional<P == PLANES_BF16, bf16x8, f16x8>::type;
+    V b[4][2];
+#pragma unroll
+    for (int nf = 0; nf < 4; nf++) {
+        if constexpr (P == PLANES_BF16) {
+            fp8x16_to_bf16x8x2(w[nf], b[nf][0], b[nf][1]);
+        } else {
+            fp8x16_to_f16x8x2(w[nf], b[nf][0], b[nf][1]);
+        }
+    }
+    V ac[4], an[4];
+    // Groups j: k-slice h = j / P, planes from the smallest (p = P - 1) up.
+    auto read_group = [&](int j, V (&dst)[4]) {
+        const int h = j / P, p = (P - 1) - j % P;
+#pragma unroll
+        for (int mf = 0; mf < 4; mf++) {
+            dst[mf] = __builtin_bit_cast(V, *reinterpret_cast<const u32x4*>(
+                buf + ((mf * P + p) * 2 + h) * 1024 + 16 * lane));
+        }
+    };
+    read_group(0, ac);
+#pragma unroll
+    for (int j = 0; j < 2 * P; j++) {
+        if (j < 2 * P - 1) {
+            read_group(j + 1, an);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int mf = 0; mf < 4; mf++) {
+#pragma unroll
+            for (int nf = 0; nf < 4; nf++) {
+                if constexpr (P == PLANES_BF16) {
+                    acc[mf][nf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac[mf],
+                        b[nf][j / P], acc[mf][nf], 0, 0, 0);
+                } else {
+                    acc[mf][nf] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac[mf],
+                        b[nf][j / P], acc[mf][nf], 0, 0, 0);
+                }
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int mf = 0; mf < 4; mf++) {
+            ac[mf] = an[mf];
+        }
+    }
+}
+
+__device__ __forceinline__ void zero_tile(floatx4 (&acc)[4][4])
+{
+#pragma unroll
+    for (int mf = 0; mf < 4; mf++) {
+#pragma unroll
+        for (int nf = 0; nf < 4; nf++) {
+            acc[mf][nf] = floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+}
+
+// The wave's 64 x 64 tile into o[m][n0 + ..] for token rows m0.. < count.
+// D layout of v_mfma_f32_16x16x32_{bf16,f16}: lane l holds rows 4*(l/16) + r,
+// column l%16 of each 16x16 tile.
+__device__ __forceinline__ void store_tile(const floatx4 (&acc)[4][4], float* __restrict__ o,
+    uint32_t N, uint32_t m0, uint32_t n0, uint32_t count, uint32_t lane)
+{
+    const uint32_t g = lane >> 4, l16 = lane & 15;
+#pragma unroll
+    for (int mf = 0; mf < 4; mf++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const uint32_t m = m0 + 16 * mf + 4 * g + r;
+            if (m < count) {
+#pragma unroll
+                for (int nf = 0; nf < 4; nf++) {
+                    o[(size_t)m * N + n0 + 16 * nf + l16] = acc[mf][nf][r];
+                }
+            }
+        }
+    }
+}
+
 // P activation planes (PLANES_BF16 or PLANES_F16) of the same layout
 // xs[p][m][k]. grid: n_tiles * m_tiles * splits workgroups of 256 threads, two
 // resident per CU; (n_tiles * splits) a multiple of 8. W0 holds rows [0, boundary), W1
@@ -411,7 +561,6 @@ __device__ __forceinline__ void gemm_tile(const uint8_t* __restrict__ W0,
     uint32_t splits, float* __restrict__ out)
 {
     static_assert(P == PLANES_BF16 || P == PLANES_F16, "plane format");
-    using V = typename std::conditional<P == PLANES_BF16, bf16x8, f16x8>::type;
     constexpr uint32_t A_FRAGS = 4 * P * 2;   // 1 KB activation fragments per stage
     constexpr uint32_t PW = A_FRAGS / 4;      // fragments each wave loads
     __shared__ __attribute__((aligned(1024))) uint8_t As0[A_FRAGS * 1024];
@@ -451,62 +600,7 @@ __device__ __forceinline__ void gemm_tile(const uint8_t* __restrict__ W0,
         }
     };
     floatx4 acc[4][4];
-#pragma unroll
-    for (int mf = 0; mf < 4; mf++) {
-#pragma unroll
-        for (int nf = 0; nf < 4; nf++) {
-            acc[mf][nf] = floatx4{0.f, 0.f, 0.f, 0.f};
-        }
-    }
-    // One stage: A fragments (mf, p, h) read from LDS one (p, h) group of four
-    // ahead of its MFMAs; each fragment feeds the four weight fragments.
-    auto compute = [&](const uint8_t* buf, const u32x4 (&w)[4]) {
-        V b[4][2];
-#pragma unroll
-        for (int nf = 0; nf < 4; nf++) {
-            if constexpr (P == PLANES_BF16) {
-                fp8x16_to_bf16x8x2(w[nf], b[nf][0], b[nf][1]);
-            } else {
-                fp8x16_to_f16x8x2(w[nf], b[nf][0], b[nf][1]);
-            }
-        }
-        V ac[4], an[4];
-        // Groups j: k-slice h = j / P, planes from the smallest (p = P - 1) up.
-        auto read_group = [&](int j, V (&dst)[4]) {
-            const int h = j / P, p = (P - 1) - j % P;
-#pragma unroll
-            for (int mf = 0; mf < 4; mf++) {
-                dst[mf] = __builtin_bit_cast(V, *reinterpret_cast<const u32x4*>(
-                    buf + ((mf * P + p) * 2 + h) * 1024 + 16 * lane));
-            }
-        };
-        read_group(0, ac);
-#pragma unroll
-        for (int j = 0; j < 2 * P; j++) {
-            if (j < 2 * P - 1) {
-                read_group(j + 1, an);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int mf = 0; mf < 4; mf++) {
-#pragma unroll
-                for (int nf = 0; nf < 4; nf++) {
-                    if constexpr (P == PLANES_BF16) {
-                        acc[mf][nf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac[mf],
-                            b[nf][j / P], acc[mf][nf], 0, 0, 0);
-                    } else {
-                        acc[mf][nf] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ac[mf],
-                            b[nf][j / P], acc[mf][nf], 0, 0, 0);
-                    }
-                }
-            }
-            __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-            for (int mf = 0; mf < 4; mf++) {
-                ac[mf] = an[mf];
-            }
-        }
-    };
+    zero_tile(acc);
     // Double-buffered stages: the next stage's activation (direct to LDS) and
     // weight loads are issued after the barrier that ends every read of the
     // LDS buffer they overwrite, and complete (s_waitcnt 0 + barrier) before
@@ -525,7 +619,7 @@ __device__ __forceinline__ void gemm_tile(const uint8_t* __restrict__ W0,
             load_a((st + 1) * BK, As1);
             load_w((st + 1) * BK);
         }
-        compute(As0, wc);
+        gemm_stage<P>(As0, wc, lane, acc);
         if (st + 1 >= steps) {
             break;
         }
@@ -539,23 +633,110 @@ __device__ __forceinline__ void gemm_tile(const uint8_t* __restrict__ W0,
             load_a((st + 2) * BK, As0);
             load_w((st + 2) * BK);
         }
-        compute(As1, wc);
+        gemm_stage<P>(As1, wc, lane, acc);
     }
-    // D layout of v_mfma_f32_16x16x32_{bf16,f16}: lane l holds rows 4*(l/16) + r,
-    // column l%16 of each 16x16 tile.
-    float* o = out + (size_t)s * stride_tokens * N;
+    store_tile(acc, out + (size_t)s * stride_tokens * N, N, m0, nt * GN + wave * 64, count, lane);
+}
+
+// gemm_tile over a stream-K partition: grid 8 * gpx * m_tiles workgroups of
+// 256 threads (two resident per CU), `8 * gpx` groups of m_tiles workgroups,
+// one per 64-token tile, on one XCD so that they share each weight tile in
+// L2. A workgroup runs its group's units back to back, the next unit's loads
+// in flight during the current one across column boundaries, and writes one
+// partial per column it covers, into slot (group - first group of the
+// column): P[slot][m][n], slot stride stride_tokens * N. A column's
+// segments are its slots 0 .. stream_segments - 1, in K order; higher slots
+// are not written for it. Every workgroup holds the same work to within one
+// unit, so the launch has no partial last round.
+template <int P>
+__device__ __forceinline__ void gemm_stream_tile(const uint8_t* __restrict__ W0,
+    const uint8_t* __restrict__ W1, uint32_t boundary, uint32_t N, uint32_t K,
+    const uint16_t* __restrict__ xs, uint32_t stride_tokens, uint32_t count, uint32_t m_tiles,
+    uint32_t gpx, float* __restrict__ out)
+{
+    static_assert(P == PLANES_BF16 || P == PLANES_F16, "plane format");
+    constexpr uint32_t A_FRAGS = 4 * P * 2;
+    constexpr uint32_t PW = A_FRAGS / 4;
+    __shared__ __attribute__((aligned(1024))) uint8_t As0[A_FRAGS * 1024];
+    __shared__ __attribute__((aligned(1024))) uint8_t As1[A_FRAGS * 1024];
+    const uint32_t xcd = blockIdx.x & 7u, q = blockIdx.x >> 3;
+    const uint32_t mt = q % m_tiles, groups = 8 * gpx, G = xcd * gpx + q / m_tiles;
+    const uint32_t stages = K / BK, units = N / GN * stages;
+    const uint32_t u0 = stream_begin(G, units, groups), u1 = stream_begin(G + 1, units, groups);
+    if (u0 >= u1) {
+        return;
+    }
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t g = lane >> 4, l16 = lane & 15;
+    const uint32_t m0 = mt * GM;
+    const size_t plane = (size_t)stride_tokens * K;
+    const uint16_t* abase[PW];
 #pragma unroll
-    for (int mf = 0; mf < 4; mf++) {
+    for (int i = 0; i < (int)PW; i++) {
+        const uint32_t f = PW * wave + i, mf = f / (2 * P), p = (f / 2) % P, h = f % 2;
+        abase[i] = xs + p * plane + (size_t)(m0 + 16 * mf + l16) * K + 16 * g + 8 * h;
+    }
+    auto load_a = [&](uint32_t u, uint8_t* buf) {
+        const uint32_t dk = (u % stages) * BK;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            const uint32_t m = m0 + 16 * mf + 4 * g + r;
-            if (m < count) {
-#pragma unroll
-                for (int nf = 0; nf < 4; nf++) {
-                    o[(size_t)m * N + nt * GN + wave * 64 + 16 * nf + l16] = acc[mf][nf][r];
-                }
-            }
+        for (int i = 0; i < (int)PW; i++) {
+            __builtin_amdgcn_global_load_lds(abase[i] + dk, buf + (PW * wave + i) * 1024, 16, 0, 0);
         }
+    };
+    u32x4 wr[4];
+    auto load_w = [&](uint32_t u) {
+        const uint32_t nt = u / stages, n0 = nt * GN + wave * 64;
+        const uint8_t* Wt = n0 < boundary ? W0 + (size_t)n0 * K : W1 + (size_t)(n0 - boundary) * K;
+        const uint8_t* wrow = Wt + (size_t)l16 * K + (u - nt * stages) * BK + 16 * g;
+#pragma unroll
+        for (int nf = 0; nf < 4; nf++) {
+            wr[nf] = *reinterpret_cast<const u32x4*>(wrow + (size_t)16 * nf * K);
+        }
+    };
+    floatx4 acc[4][4];
+    zero_tile(acc);
+    // A column's partial leaves after its last stage or the range's last unit.
+    auto finish = [&](uint32_t u) {
+        const uint32_t nt = u / stages;
+        if (u + 1 == u1 || u + 1 == (nt + 1) * stages) {
+            const uint32_t slot = G - stream_group(nt * stages, units, groups);
+            store_tile(acc, out + (size_t)slot * stride_tokens * N, N, m0, nt * GN + wave * 64,
+                count, lane);
+            zero_tile(acc);
+        }
+    };
+    // The same double-buffered stages as gemm_tile, over units.
+    u32x4 wc[4];
+    load_a(u0, As0);
+    load_w(u0);
+    for (uint32_t u = u0; u < u1; u += 2) {
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+#pragma unroll
+        for (int nf = 0; nf < 4; nf++) {
+            wc[nf] = wr[nf];
+        }
+        if (u + 1 < u1) {
+            load_a(u + 1, As1);
+            load_w(u + 1);
+        }
+        gemm_stage<P>(As0, wc, lane, acc);
+        finish(u);
+        if (u + 1 >= u1) {
+            break;
+        }
+        __builtin_amdgcn_s_waitcnt(0);
+        __syncthreads();
+#pragma unroll
+        for (int nf = 0; nf < 4; nf++) {
+            wc[nf] = wr[nf];
+        }
+        if (u + 2 < u1) {
+            load_a(u + 2, As0);
+            load_w(u + 2);
+        }
+        gemm_stage<P>(As1, wc, lane, acc);
+        finish(u + 1);
     }
 }
 
@@ -575,6 +756,15 @@ k_gemm_f16(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint3
     uint32_t count, uint32_t m_tiles, uint32_t splits, float* __restrict__ out)
 {
     gemm_tile<PLANES_F16>(W0, W1, boundary, N, K, xs, stride_tokens, count, m_tiles, splits, out);
+}
+
+__global__ void __launch_bounds__(256, 2)
+k_gemm_f16_stream(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1,
+    uint32_t boundary, uint32_t N, uint32_t K, const uint16_t* __restrict__ xs,
+    uint32_t stride_tokens, uint32_t count, uint32_t m_tiles, uint32_t gpx, float* __restrict__ out)
+{
+    gemm_stream_tile<PLANES_F16>(W0, W1, boundary, N, K, xs, stride_tokens, count, m_tiles, gpx,
+        out);
 }
 
 // x[i] = x[i] + scale * (((p0 + p1) + p2) + ...) (deterministic split-K
@@ -692,6 +882,7 @@ static int with_splits(uint32_t splits, const char* what, F&& f)
         return -1;
     case 1: f(std::integral_constant<int, 1>{}); break;
     case 2: f(std::integral_constant<int, 2>{}); break;
+    case 3: f(std::integral_constant<int, 3>{}); break;
     case 4: f(std::integral_constant<int, 4>{}); break;
     case 8:
         if constexpr (MAXS >= 8) {
@@ -769,6 +960,41 @@ static int gemm(int planes, const uint8_t* W0, const uint8_t* W1, uint32_t bound
     return launched_ok("gemm");
 }
 
+// The FP16-plane product over a stream-K partition (gemm_stream_tile): the
+// most groups per XCD (<= 64 / m_tiles, two workgroups per CU) whose
+// partials fit the partial buffer and the consumer's MAXS slots. Returns the
+// slot count in *slots and the group count in *groups.
+template <uint32_t MAXS>
+static int gemm_stream(const uint8_t* W0, const uint8_t* W1, uint32_t boundary, uint32_t N,
+    uint32_t K, const uint16_t* xs, uint32_t stride, uint32_t count, float* out,
+    uint32_t* slots, uint32_t* groups, hipStream_t s)
+{
+    const uint32_t n_tiles = N / GN;
+    const uint32_t m_tiles = (count + GM - 1) / GM;
+    if (!count || N % GN || K % BK || boundary % GN || m_tiles * GM > stride || m_tiles > 64) {
+        lh_set_error("stream gemm: unsupported shape N=%u K=%u count=%u", N, K, count);
+        return -1;
+    }
+    const uint32_t stages = K / BK, units = n_tiles * stages;
+    for (uint32_t gpx = 64 / m_tiles; gpx > 0; gpx--) {
+        const uint32_t ng = 8 * gpx;
+        uint32_t most = 0;
+        for (uint32_t c = 0; c < n_tiles; c++) {
+            most = std::max(most, stream_segments(c, stages, units, ng));
+        }
+        if (most > MAXS || (size_t)most * stride * N > partial_floats(stride)) {
+            continue;
+        }
+        hipLaunchKernelGGL(k_gemm_f16_stream, dim3(ng * m_tiles), dim3(256), 0, s, W0,
+            W1 ? W1 : W0, boundary, N, K, xs, stride, count, m_tiles, gpx, out);
+        *slots = most;
+        *groups = ng;
+        return launched_ok("stream gemm");
+    }
+    lh_set_error("stream gemm: no partition fits N=%u K=%u count=%u", N, K, count);
+    return -1;
+}
+
 static int combine(const float* partial, uint32_t splits, uint32_t rows, uint32_t count,
     uint32_t stride, float scale, const float* in_scale, float* x, int residual, hipStream_t s)
 {
@@ -835,8 +1061,8 @@ extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, floa
     uint16_t* xs = ws->d_split;
     float* scale_a = token_scales(ws);
     float* scale_b = group_scales(ws);
-    // K splits (measured at 256 tokens): gate|up 4 (the partial buffer's
-    // limit), q|k|v 8, o 8, down 16.
+    // K splits (measured at 256 tokens): q|k|v 8, o 8, down 16; gate|up is
+    // stream-K.
     // q|k|v: 6144 rows, 3072 columns; scales, RoPE and the KV append in the
     // epilogue.
     const uint32_t sq = 8;
@@ -860,14 +1086,15 @@ extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, floa
         residual_norm_split(P, so, B, w->scale[3], NULL, d_x, w->post_norm, xs, scale_a, n, s)) {
         return -1;
     }
-    // gate|up: 18432 rows, 3072 columns; SiLU(gate)*up as the down
+    // gate|up: 18432 rows, 3072 columns, stream-K (at 256 tokens 128 groups of
+    // 27 stages, at most 3 partials per column); SiLU(gate)*up as the down
     // projection's input.
-    const uint32_t sg = 4;
-    if (gemm(PLANES_F16, w->gate, w->up, LH_INNER, MAX_N, LH_HIDDEN, xs, B, n, sg, P, s) ||
+    uint32_t sg = 0, groups = 0;
+    if (gemm_stream<4>(w->gate, w->up, LH_INNER, MAX_N, LH_HIDDEN, xs, B, n, P, &sg, &groups, s) ||
         with_splits<false, 4>(sg, "silu split", [&](auto S) {
             hipLaunchKernelGGL(k_split_silu<decltype(S)::value>, dim3(n, DOWN_SPLITS), dim3(192),
                 0, s, P, (size_t)B * MAX_N, make_float2(w->scale[4], w->scale[5]), scale_a, xs,
-                scale_b, B);
+                scale_b, B, groups);
         })) {
         return -1;
     }

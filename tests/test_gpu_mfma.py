@@ -93,10 +93,13 @@ def test_mfma_layer_config3(gpu):
             assert np.max(np.abs(g - w_) / np.max(np.abs(w_), axis=1, keepdims=True)) < 1e-5
 
 
-def test_mfma_layer_small_odd_block(gpu):
+@pytest.mark.parametrize("length,count", [(3, 5), (40, 100), (7, 130)])
+def test_mfma_layer_small_odd_block(gpu, length, count):
+    """One, two and three 64-token tiles, the last partial (the gate|up
+    stream-K partition takes 36, 30 and 21 groups per XCD there)."""
     from test_gpu_layer import oracle_layer, run_layer
     host = syn.layer(SEED, 1)
-    length, count, capacity = 3, 5, 256
+    capacity = 256
     x = syn.normal_f32(SEED, 9101, count * 3072)
     kpm = syn.normal_f32(SEED, 9102, length * 1024).reshape(length, 1024)
     vpm = syn.normal_f32(SEED, 9103, length * 1024).reshape(length, 1024)
