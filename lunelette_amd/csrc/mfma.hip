@@ -153,29 +153,6 @@ __device__ __forceinline__ float4 sum_splits(const float4* __restrict__ p, size_
     return acc;
 }
 
-// sum_splits with split s's partial first multiplied by sc[s] (powers of two,
-// so each product is exact and the sum is the unscaled one).
-template <int S>
-__device__ __forceinline__ float4 sum_splits_scaled(const float4* __restrict__ p, size_t stride4,
-    const float* __restrict__ sc)
-{
-    float4 v[S];
-#pragma unroll
-    for (int s = 0; s < S; s++) {
-        v[s] = p[s * stride4];
-    }
-    float4 acc = scale4(v[0], sc[0]);
-#pragma unroll
-    for (int s = 1; s < S; s++) {
-        const float4 w = scale4(v[s], sc[s]);
-        acc.x = acc.x + w.x;
-        acc.y = acc.y + w.y;
-        acc.z = acc.z + w.z;
-        acc.w = acc.w + w.w;
-    }
-    return acc;
-}
-
 // sum_splits over the first n (1 <= n <= S) partials only, in the same
 // order (n = S: bitwise sum_splits); the rest are neither loaded nor added.
 template <int S>
@@ -222,6 +199,14 @@ __host__ __device__ inline uint32_t stream_segments(uint32_t c, uint32_t stages,
         stream_group(c * stages, units, groups) + 1;
 }
 
+// Segments of column c (256 rows) of the down projection (3072 rows, 9216
+// columns) over `groups` stream-K groups.
+__device__ __forceinline__ uint32_t down_segments(uint32_t c, uint32_t groups)
+{
+    constexpr uint32_t STAGES = LH_INNER / BK, UNITS = LH_HIDDEN / GN * STAGES;
+    return stream_segments(c, STAGES, UNITS, groups);
+}
+
 // xs[p][m][k] for p < 3 from FP32 rows, no normalization. grid (count,
 // ceil(width / 2048)), block 256: thread j of the row takes columns
 // 8j .. 8j+7 (width a multiple of 8, rows 16-byte aligned).
@@ -249,14 +234,16 @@ k_split(const float* __restrict__ x, uint16_t* __restrict__ xs, uint32_t width,
 // scaled by the row's power of two 2^e and split into two FP16 planes, with
 // out_scale[t] = 2^-e to undo it on the GEMM's output; otherwise the three
 // exact BF16 planes (out_scale unused). The partials carry their own
-// scales per split, in_scale[t][s] (nullable; the down projection's). S = 0
+// groups > 0: the partials are the down projection's stream-K partials of
+// that many groups, each column summing only its segments. S = 0
 // only normalizes (the first layer's input norm). grid (count), block 768:
 // thread i owns columns 4i .. 4i+3.
 template <int S, bool F16>
 __global__ void __launch_bounds__(768)
 k_residual_norm_split(const float* __restrict__ partial, size_t split_stride, float scale,
-    const float* __restrict__ in_scale, float* __restrict__ x, const float* __restrict__ gamma,
-    uint16_t* __restrict__ xs, float* __restrict__ out_scale, uint32_t stride_tokens)
+    float* __restrict__ x, const float* __restrict__ gamma,
+    uint16_t* __restrict__ xs, float* __restrict__ out_scale, uint32_t stride_tokens,
+    uint32_t groups)
 {
     // Row in the [chunk][quad][lane] 16-byte-word layout: lane l's 16 values
     // of chunk c (columns c*1024 + 16l .. +15) are words (4c + q)*64 + l.
@@ -269,8 +256,9 @@ k_residual_norm_split(const float* __restrict__ partial, size_t split_stride, fl
     float4 v = xr[tid];
     if constexpr (S > 0) {
         const float4* pt = reinterpret_cast<const float4*>(partial + (size_t)t * LH_HIDDEN) + tid;
-        const float4 acc = in_scale ? sum_splits_scaled<S>(pt, split_stride / 4, in_scale + t * S)
-                                    : sum_splits<S>(pt, split_stride / 4);
+        const float4 acc = groups
+            ? sum_segments<S>(pt, split_stride / 4, down_segments(tid / 64, groups))
+            : sum_splits<S>(pt, split_stride / 4);
         v.x = v.x + acc.x * scale;
         v.y = v.y + acc.y * scale;
         v.z = v.z + acc.z * scale;
@@ -328,7 +316,7 @@ k_residual_norm_split(const float* __restrict__ partial, size_t split_stride, fl
 // segment count. Each of the down projection's DOWN_SPLITS K ranges (576
 // columns) gets its own power of two 2^e (its largest magnitude into
 // [2^14, 2^15)) before the split into two FP16 planes; out_scale[t][g] = 2^-e,
-// which the down projection's consumers apply to that split's partial. grid
+// which the down projection's GEMM applies to that granule's products. grid
 // (count, DOWN_SPLITS), block 192: thread j < 144 owns columns 576g + 4j .. +3.
 constexpr uint32_t DOWN_SPLITS = 16;
 constexpr uint32_t GROUP4 = LH_INNER / DOWN_SPLITS / 4;   // float4 columns per group: 144
@@ -648,20 +636,32 @@ __device__ __forceinline__ void gemm_tile(const uint8_t* __restrict__ W0,
 // segments are its slots 0 .. stream_segments - 1, in K order; higher slots
 // are not written for it. Every workgroup holds the same work to within one
 // unit, so the launch has no partial last round.
+//
+// With gscale, the planes of token m's K granule j (K / GRANULES columns)
+// carry the power of two 1/gscale[m][j] (k_split_silu): the accumulator is
+// kept in units of the current granule's planes, multiplied by
+// gscale[m][j] / gscale[m][j+1] where a segment crosses into the next
+// granule and by gscale[m][j] before it is stored, so the partials are
+// unscaled. The factors are powers of two (exact products); the workgroup's
+// 64 x GRANULES factors are staged in LDS before the first stage.
+constexpr uint32_t GRANULES = 16;
+static_assert(GRANULES == DOWN_SPLITS, "the down input's scale granules");
+
 template <int P>
 __device__ __forceinline__ void gemm_stream_tile(const uint8_t* __restrict__ W0,
     const uint8_t* __restrict__ W1, uint32_t boundary, uint32_t N, uint32_t K,
     const uint16_t* __restrict__ xs, uint32_t stride_tokens, uint32_t count, uint32_t m_tiles,
-    uint32_t gpx, float* __restrict__ out)
+    uint32_t gpx, const float* __restrict__ gscale, float* __restrict__ out)
 {
     static_assert(P == PLANES_BF16 || P == PLANES_F16, "plane format");
     constexpr uint32_t A_FRAGS = 4 * P * 2;
     constexpr uint32_t PW = A_FRAGS / 4;
     __shared__ __attribute__((aligned(1024))) uint8_t As0[A_FRAGS * 1024];
     __shared__ __attribute__((aligned(1024))) uint8_t As1[A_FRAGS * 1024];
+    __shared__ float4 gs[GM * GRANULES / 4];
     const uint32_t xcd = blockIdx.x & 7u, q = blockIdx.x >> 3;
     const uint32_t mt = q % m_tiles, groups = 8 * gpx, G = xcd * gpx + q / m_tiles;
-    const uint32_t stages = K / BK, units = N / GN * stages;
+    const uint32_t stages = K / BK, units = N / GN * stages, gstages = stages / GRANULES;
     const uint32_t u0 = stream_begin(G, units, groups), u1 = stream_begin(G + 1, units, groups);
     if (u0 >= u1) {
         return;
@@ -669,6 +669,11 @@ __device__ __forceinline__ void gemm_stream_tile(const uint8_t* __restrict__ W0,
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t g = lane >> 4, l16 = lane & 15;
     const uint32_t m0 = mt * GM;
+    if (gscale) {
+        // Rows past count take 1 (their products are never stored).
+        const float4 v = reinterpret_cast<const float4*>(gscale + (size_t)m0 * GRANULES)[tid];
+        gs[tid] = m0 + tid / 4 < count ? v : make_float4(1.f, 1.f, 1.f, 1.f);
+    }
     const size_t plane = (size_t)stride_tokens * K;
     const uint16_t* abase[PW];
 #pragma unroll
@@ -697,8 +702,25 @@ __device__ __forceinline__ void gemm_stream_tile(const uint8_t* __restrict__ W0,
     zero_tile(acc);
     // A column's partial leaves after its last stage or the range's last unit.
     auto finish = [&](uint32_t u) {
-        const uint32_t nt = u / stages;
-        if (u + 1 == u1 || u + 1 == (nt + 1) * stages) {
+        const uint32_t nt = u / stages, st = u - nt * stages;
+        const bool last = u + 1 == u1 || st + 1 == stages;
+        if (gscale && (last || (st + 1) % gstages == 0)) {
+            const uint32_t j = st / gstages;
+            const float* gf = reinterpret_cast<const float*>(gs);
+#pragma unroll
+            for (int mf = 0; mf < 4; mf++) {
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const float* row = gf + (16 * mf + 4 * g + r) * GRANULES;
+                    const float f = last ? row[j] : row[j] / row[j + 1];
+#pragma unroll
+                    for (int nf = 0; nf < 4; nf++) {
+                        acc[mf][nf][r] *= f;
+                    }
+                }
+            }
+        }
+        if (last) {
             const uint32_t slot = G - stream_group(nt * stages, units, groups);
             store_tile(acc, out + (size_t)slot * stride_tokens * N, N, m0, nt * GN + wave * 64,
                 count, lane);
@@ -761,30 +783,31 @@ k_gemm_f16(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint3
 __global__ void __launch_bounds__(256, 2)
 k_gemm_f16_stream(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1,
     uint32_t boundary, uint32_t N, uint32_t K, const uint16_t* __restrict__ xs,
-    uint32_t stride_tokens, uint32_t count, uint32_t m_tiles, uint32_t gpx, float* __restrict__ out)
+    uint32_t stride_tokens, uint32_t count, uint32_t m_tiles, uint32_t gpx,
+    const float* __restrict__ gscale, float* __restrict__ out)
 {
     gemm_stream_tile<PLANES_F16>(W0, W1, boundary, N, K, xs, stride_tokens, count, m_tiles, gpx,
-        out);
+        gscale, out);
 }
 
 // x[i] = x[i] + scale * (((p0 + p1) + p2) + ...) (deterministic split-K
 // combine with the residual add, src/metal_encode.m:160,175); without the
 // residual, x[i] = scale * (...). Partials P[s][i] with split stride
-// split_stride, split s of token m first times in_scale[m][s] when given; i
-// runs over count * rows in float4 units (rows4 = rows / 4 per token). grid
-// ceil(count * rows / 1024), block 256.
+// split_stride, or (groups > 0) the down projection's stream-K partials,
+// each column's segments only; i runs over count * rows in float4 units
+// (rows4 = rows / 4 per token). grid ceil(count * rows / 1024), block 256.
 template <int S>
 __global__ void __launch_bounds__(256)
 k_combine_residual(const float* __restrict__ partial, size_t split_stride, size_t n4, float scale,
-    const float* __restrict__ in_scale, uint32_t rows4, float* __restrict__ x, int residual)
+    uint32_t rows4, float* __restrict__ x, int residual, uint32_t groups)
 {
     const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;
     if (i >= n4) {
         return;
     }
     const float4* pi = reinterpret_cast<const float4*>(partial) + i;
-    const float4 acc = in_scale
-        ? sum_splits_scaled<S>(pi, split_stride / 4, in_scale + (i / rows4) * S)
+    const float4 acc = groups
+        ? sum_segments<S>(pi, split_stride / 4, down_segments((uint32_t)(i % rows4) / 64, groups))
         : sum_splits<S>(pi, split_stride / 4);
     float4* xr = reinterpret_cast<float4*>(x) + i;
     float4 v = make_float4(acc.x * scale, acc.y * scale, acc.z * scale, acc.w * scale);
@@ -913,24 +936,24 @@ static int split_rows(const float* x, uint16_t* xs, uint32_t width, uint32_t cou
     return launched_ok("split");
 }
 
-// x = x + scale * sum of `splits` partials, split s times in_scale[t][s] when
-// given (0 splits: x unchanged), then
+// x = x + scale * sum of `splits` partials (groups > 0: the down projection's
+// stream-K partials; 0 splits: x unchanged), then
 // the RMSNorm of x with gamma as the next GEMM's input planes in xs: two FP16
 // planes with their row scales in out_scale, or (out_scale NULL) three BF16
 // planes; rows of 3072.
 static int residual_norm_split(const float* partial, uint32_t splits, uint32_t stride,
-    float scale, const float* in_scale, float* x, const float* gamma, uint16_t* xs,
-    float* out_scale, uint32_t count, hipStream_t s)
+    float scale, float* x, const float* gamma, uint16_t* xs, float* out_scale, uint32_t count,
+    hipStream_t s, uint32_t groups = 0)
 {
     return with_splits<true>(splits, "residual norm split", [&](auto S) {
         if (out_scale) {
             hipLaunchKernelGGL((k_residual_norm_split<decltype(S)::value, true>), dim3(count),
-                dim3(768), 0, s, partial, (size_t)stride * LH_HIDDEN, scale, in_scale, x, gamma,
-                xs, out_scale, stride);
+                dim3(768), 0, s, partial, (size_t)stride * LH_HIDDEN, scale, x, gamma, xs,
+                out_scale, stride, groups);
         } else {
             hipLaunchKernelGGL((k_residual_norm_split<decltype(S)::value, false>), dim3(count),
-                dim3(768), 0, s, partial, (size_t)stride * LH_HIDDEN, scale, in_scale, x, gamma,
-                xs, out_scale, stride);
+                dim3(768), 0, s, partial, (size_t)stride * LH_HIDDEN, scale, x, gamma, xs,
+                out_scale, stride, groups);
         }
     });
 }
@@ -966,12 +989,13 @@ static int gemm(int planes, const uint8_t* W0, const uint8_t* W1, uint32_t bound
 // slot count in *slots and the group count in *groups.
 template <uint32_t MAXS>
 static int gemm_stream(const uint8_t* W0, const uint8_t* W1, uint32_t boundary, uint32_t N,
-    uint32_t K, const uint16_t* xs, uint32_t stride, uint32_t count, float* out,
-    uint32_t* slots, uint32_t* groups, hipStream_t s)
+    uint32_t K, const uint16_t* xs, uint32_t stride, uint32_t count, const float* gscale,
+    float* out, uint32_t* slots, uint32_t* groups, hipStream_t s)
 {
     const uint32_t n_tiles = N / GN;
     const uint32_t m_tiles = (count + GM - 1) / GM;
-    if (!count || N % GN || K % BK || boundary % GN || m_tiles * GM > stride || m_tiles > 64) {
+    if (!count || N % GN || K % BK || boundary % GN || m_tiles * GM > stride || m_tiles > 64 ||
+        (gscale && K % (BK * GRANULES))) {
         lh_set_error("stream gemm: unsupported shape N=%u K=%u count=%u", N, K, count);
         return -1;
     }
@@ -986,7 +1010,7 @@ static int gemm_stream(const uint8_t* W0, const uint8_t* W1, uint32_t boundary, 
             continue;
         }
         hipLaunchKernelGGL(k_gemm_f16_stream, dim3(ng * m_tiles), dim3(256), 0, s, W0,
-            W1 ? W1 : W0, boundary, N, K, xs, stride, count, m_tiles, gpx, out);
+            W1 ? W1 : W0, boundary, N, K, xs, stride, count, m_tiles, gpx, gscale, out);
         *slots = most;
         *groups = ng;
         return launched_ok("stream gemm");
@@ -996,13 +1020,13 @@ static int gemm_stream(const uint8_t* W0, const uint8_t* W1, uint32_t boundary, 
 }
 
 static int combine(const float* partial, uint32_t splits, uint32_t rows, uint32_t count,
-    uint32_t stride, float scale, const float* in_scale, float* x, int residual, hipStream_t s)
+    uint32_t stride, float scale, float* x, int residual, hipStream_t s, uint32_t groups = 0)
 {
     const size_t n4 = (size_t)count * rows / 4;
     return with_splits(splits, "split-K combine", [&](auto S) {
         hipLaunchKernelGGL(k_combine_residual<decltype(S)::value>,
             dim3((unsigned)((n4 + 255) / 256)), dim3(256), 0, s, partial,
-            (size_t)stride * rows, n4, scale, in_scale, rows / 4, x, residual);
+            (size_t)stride * rows, n4, scale, rows / 4, x, residual, groups);
     });
 }
 
@@ -1032,15 +1056,15 @@ extern "C" int lh_fp8_gemm(lh_workspace* ws, const uint8_t* d_w, float scale, co
             B, n, splits, ws->d_gemm, s)) {
         return -1;
     }
-    return combine(ws->d_gemm, splits, (uint32_t)rows, n, B, scale, NULL, d_y, 0, s);
+    return combine(ws->d_gemm, splits, (uint32_t)rows, n, B, scale, d_y, 0, s);
 }
 
 // One layer over ws->count tokens. input_split: ws->d_split already holds the
 // BF16 planes of input_norm(x) (the previous layer's last kernel wrote them);
 // next_norm: the last kernel also writes them for the following layer (NULL:
 // plain residual combine). The gate|up and down inputs travel as two FP16
-// planes with power-of-two scales (per token for gate|up, per token and K split
-// for down). The q|k|v input stays
+// planes with power-of-two scales (per token for gate|up, per token and
+// 576-column K granule for down). The q|k|v input stays
 // in three exact BF16 planes: its error reaches the attention scores, which
 // the softmax amplifies (at scores of a few hundred, two FP16 planes put the
 // config-3 layer at 1.2e-3 of the row maximum, over the 1e-3 tolerance), and
@@ -1067,7 +1091,7 @@ extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, floa
     // epilogue.
     const uint32_t sq = 8;
     if ((!input_split &&
-            residual_norm_split(NULL, 0, B, 1.0f, NULL, d_x, w->input_norm, xs, NULL, n, s)) ||
+            residual_norm_split(NULL, 0, B, 1.0f, d_x, w->input_norm, xs, NULL, n, s)) ||
         gemm(PLANES_BF16, w->qkv, NULL, LH_QKV_ROWS, LH_QKV_ROWS, LH_HIDDEN, xs, B, n, sq, P, s) ||
         with_splits(sq, "qkv epilogue", [&](auto S) {
             hipLaunchKernelGGL(k_qkv_epilogue<decltype(S)::value>, dim3(n, 3), dim3(256), 0, s,
@@ -1083,14 +1107,15 @@ extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, floa
             n, C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_attn, xs, B, s) ||
         launched_ok("attention") ||
         gemm(PLANES_BF16, w->o, NULL, LH_HIDDEN, LH_HIDDEN, LH_QUERY, xs, B, n, so, P, s) ||
-        residual_norm_split(P, so, B, w->scale[3], NULL, d_x, w->post_norm, xs, scale_a, n, s)) {
+        residual_norm_split(P, so, B, w->scale[3], d_x, w->post_norm, xs, scale_a, n, s)) {
         return -1;
     }
     // gate|up: 18432 rows, 3072 columns, stream-K (at 256 tokens 128 groups of
     // 27 stages, at most 3 partials per column); SiLU(gate)*up as the down
     // projection's input.
     uint32_t sg = 0, groups = 0;
-    if (gemm_stream<4>(w->gate, w->up, LH_INNER, MAX_N, LH_HIDDEN, xs, B, n, P, &sg, &groups, s) ||
+    if (gemm_stream<4>(w->gate, w->up, LH_INNER, MAX_N, LH_HIDDEN, xs, B, n, NULL, P, &sg,
+            &groups, s) ||
         with_splits<false, 4>(sg, "silu split", [&](auto S) {
             hipLaunchKernelGGL(k_split_silu<decltype(S)::value>, dim3(n, DOWN_SPLITS), dim3(192),
                 0, s, P, (size_t)B * MAX_N, make_float2(w->scale[4], w->scale[5]), scale_a, xs,
@@ -1098,13 +1123,18 @@ extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, floa
         })) {
         return -1;
     }
-    // down: 3072 rows, 9216 columns, residual (and the next layer's input
+    // down: 3072 rows, 9216 columns, stream-K (at 256 tokens 128 groups of
+    // 13-14 stages, 11-12 partials per column) with the input's granule
+    // scales applied in the GEMM; residual (and the next layer's input
     // planes).
-    const uint32_t sd = DOWN_SPLITS;   // also the granule of the down input's scales
-    if (gemm(PLANES_F16, w->down, NULL, LH_HIDDEN, LH_HIDDEN, LH_INNER, xs, B, n, sd, P, s)) {
+    uint32_t sd = 0, dgroups = 0;
+    if (gemm_stream<16>(w->down, NULL, LH_HIDDEN, LH_HIDDEN, LH_INNER, xs, B, n, scale_b, P, &sd,
+            &dgroups, s)) {
         return -1;
     }
+    // Segment counts vary by column: sum with the 16-slot kernels.
+    sd = 16;
     return next_norm
-        ? residual_norm_split(P, sd, B, w->scale[6], scale_b, d_x, next_norm, xs, NULL, n, s)
-        : combine(P, sd, LH_HIDDEN, n, B, w->scale[6], scale_b, d_x, 1, s);
+        ? residual_norm_split(P, sd, B, w->scale[6], d_x, next_norm, xs, NULL, n, s, dgroups)
+        : combine(P, sd, LH_HIDDEN, n, B, w->scale[6], d_x, 1, s, dgroups);
 }
