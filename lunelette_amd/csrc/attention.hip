@@ -15,10 +15,11 @@
 //
 // KV layout [kv_head][capacity][128] per layer: a block's K or V tile is one
 // contiguous 32 KiB read (K's words permuted inside the tile, lh_ktile_word).
-// K goes straight to registers (lane = position, quarter of the head
-// dimension), V is staged in LDS for the P.V chains, so a
-// workgroup holds 35 KiB of LDS and four fit on a CU. Rows at or past
-// length+t+1 never enter arithmetic. The combine runs as its own kernel: the
+// q and K go to LDS by direct loads (the scores read them there: lane =
+// position, quarter of the head dimension); V comes to registers meanwhile and
+// overwrites K's LDS region once the scores are done, for the P.V chains. A
+// workgroup holds 35 KiB of LDS and 85 registers, so four fit on a CU. Rows at
+// or past length+t+1 never enter arithmetic. The combine runs as its own kernel: the
 // kernel boundary publishes the partials device-wide, where an in-kernel
 // hand-off costs an L2 write-back or same-address atomics per workgroup.
 #include "lh_device.h"
@@ -36,7 +37,8 @@ k_attn_blocks(const float* __restrict__ q, const float* __restrict__ kcache,
     const float* __restrict__ vcache, const lh_step_params* __restrict__ params,
     uint32_t capacity, float* __restrict__ PM, float* __restrict__ PT, float* __restrict__ PA)
 {
-    __shared__ float4 Vt[LH_ATTN_BLOCK][LH_HEAD_DIM / 4];
+    // One 32 KiB tile region holds K for the scores, then V for the P.V chains.
+    __shared__ float4 T[LH_ATTN_BLOCK * LH_HEAD_DIM / 4];
     __shared__ float4 qs[4][LH_HEAD_DIM / 4];
     __shared__ float S[4][LH_ATTN_BLOCK];
     const uint32_t b = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
@@ -48,47 +50,81 @@ k_attn_blocks(const float* __restrict__ q, const float* __restrict__ kcache,
     // ceil((length + count) / 64) blocks of a capacity that is a multiple of
     // 64, so all 64 rows are in bounds; rows past the valid count are never
     // used in arithmetic.
-    // K: wave w covers positions 16w..16w+15; lane = 4 * (position - 16w) +
-    // quarter, and the tile's word order (lh_ktile_word) makes each of the
-    // eight loads one contiguous 1 KiB read.
-    const uint32_t p = 16 * wave + (lane >> 2), quarter = lane & 3;
-    float4 k[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        k[i] = kb[(wave * 8 + i) * 64 + lane];
-    }
-    float4 vr[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        vr[i] = vb[tid + 256 * i];   // row (tid + 256 i) >> 5, float4 column tid & 31
-    }
-    const uint32_t n = params->length + t + 1;
-    if (b * LH_ATTN_BLOCK >= n) {
-        return;
-    }
-    const uint32_t nbc = capacity / LH_ATTN_BLOCK;
-    const uint32_t rest = n - b * LH_ATTN_BLOCK;
-    const uint32_t valid = rest < LH_ATTN_BLOCK ? rest : LH_ATTN_BLOCK;
+    // Issue order: the four query rows (2 KiB) and the K tile go to LDS by
+    // direct loads, then the V tile to registers. Vector loads complete in
+    // issue order, so the scores wait for q and K only (an explicit vmcnt(8))
+    // and V lands while they run.
     if (tid < 128) {
-        reinterpret_cast<float4*>(qs)[tid] = reinterpret_cast<const float4*>(
-            q + (size_t)t * LH_QUERY + kvh * 4 * LH_HEAD_DIM)[tid];
+        __builtin_amdgcn_global_load_lds(reinterpret_cast<const float4*>(
+            q + (size_t)t * LH_QUERY + kvh * 4 * LH_HEAD_DIM) + tid,
+            reinterpret_cast<float4*>(qs) + 64 * wave, 16, 0, 0);
     }
+    // K: wave w covers positions 16w..16w+15; lane = 4 * (position - 16w) +
+    // quarter. The tile's word order (lh_ktile_word) makes load i of wave w
+    // the contiguous 1 KiB of words (8w + i) * 64 .. +63, written to LDS in
+    // the same order, so lane l later reads word (8w + i) * 64 + l.
+    const uint32_t p = 16 * wave + (lane >> 2), quarter = lane & 3;
 #pragma unroll
     for (int i = 0; i < 8; i++) {
-        reinterpret_cast<float4*>(Vt)[tid + 256 * i] = vr[i];
+        __builtin_amdgcn_global_load_lds(kb + (wave * 8 + i) * 64 + lane,
+            T + (wave * 8 + i) * 64, 16, 0, 0);
     }
-    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);   // V's loads stay behind K's
+    // (A native vector type: a float4 struct copy is a memcpy that, with the
+    // intrinsics around it, stays in scratch memory.)
+    typedef float v4f __attribute__((ext_vector_type(4)));
+    v4f vr[8];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        vr[i] = reinterpret_cast<const v4f*>(vb)[tid + 256 * i];   // row (tid + 256 i) >> 5
+    }
+    // No early exit for blocks past token t's last position (multi-token
+    // steps): a branch here lets the compiler sink the V loads below it. Such
+    // a workgroup runs with valid = 0 and writes nothing.
+    const uint32_t n = params->length + t + 1;
+    const uint32_t nbc = capacity / LH_ATTN_BLOCK;
+    const uint32_t rest = n > b * LH_ATTN_BLOCK ? n - b * LH_ATTN_BLOCK : 0;
+    const uint32_t valid = rest < LH_ATTN_BLOCK ? rest : LH_ATTN_BLOCK;
+    // s_waitcnt vmcnt(8), then a bare barrier: __syncthreads()'s workgroup
+    // fence would also wait for the V loads.
+    __builtin_amdgcn_s_waitcnt(0x0f78);
+    __builtin_amdgcn_s_barrier();
+    // The K and q words of step i + 1 are read while step i's products run.
     float c[4] = {0.f, 0.f, 0.f, 0.f};
+    float4 k = T[wave * 8 * 64 + lane];
+    float4 qq[4];
+#pragma unroll
+    for (int hh = 0; hh < 4; hh++) {
+        qq[hh] = qs[hh][8 * quarter];
+    }
 #pragma unroll
     for (int i = 0; i < 8; i++) {
+        float4 kn, qn[4];
+        if (i < 7) {
+            kn = T[(wave * 8 + i + 1) * 64 + lane];
+#pragma unroll
+            for (int hh = 0; hh < 4; hh++) {
+                qn[hh] = qs[hh][8 * quarter + i + 1];
+            }
+        }
 #pragma unroll
         for (int hh = 0; hh < 4; hh++) {
-            const float4 qq = qs[hh][8 * quarter + i];
-            c[hh] = __builtin_fmaf(qq.x, k[i].x, c[hh]);
-            c[hh] = __builtin_fmaf(qq.y, k[i].y, c[hh]);
-            c[hh] = __builtin_fmaf(qq.z, k[i].z, c[hh]);
-            c[hh] = __builtin_fmaf(qq.w, k[i].w, c[hh]);
+            c[hh] = __builtin_fmaf(qq[hh].x, k.x, c[hh]);
+            c[hh] = __builtin_fmaf(qq[hh].y, k.y, c[hh]);
+            c[hh] = __builtin_fmaf(qq[hh].z, k.z, c[hh]);
+            c[hh] = __builtin_fmaf(qq[hh].w, k.w, c[hh]);
         }
+        if (i < 7) {
+            k = kn;
+#pragma unroll
+            for (int hh = 0; hh < 4; hh++) {
+                qq[hh] = qn[hh];
+            }
+        }
+        // Each step's four chains complete here (an empty asm that reads and
+        // writes them), so the compiler cannot defer three of them past the
+        // loop with every step's operands held in registers.
+        asm volatile("" : "+v"(c[0]), "+v"(c[1]), "+v"(c[2]), "+v"(c[3]));
     }
 #pragma unroll
     for (int hh = 0; hh < 4; hh++) {
@@ -97,23 +133,39 @@ k_attn_blocks(const float* __restrict__ q, const float* __restrict__ kcache,
             S[hh][p] = v * LH_SCORE_SCALE;
         }
     }
+    __syncthreads();   // every read of K is done; S holds the scores
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+        reinterpret_cast<v4f*>(T)[tid + 256 * i] = vr[i];
+    }
     __syncthreads();
-    // Wave w = head kvh*4 + w from here on; lane = position.
+    // Wave w = head kvh*4 + w from here on; lane = position. e_j reaches every
+    // lane by a scalar read of lane j.
     const float s = lane < valid ? S[wave][lane] : -__builtin_inff();
     const float m = wave_max64(s);
     const float e = lane < valid ? expf_cw(s - m) : 0.0f;
     const float total = wave_tree64(e);
-    __syncthreads();
-    S[wave][lane] = e;
-    __syncthreads();
     const uint32_t d0 = 2 * lane;
     float a0 = 0.0f, a1 = 0.0f;
-    const float* vt = reinterpret_cast<const float*>(Vt) + d0;
-    for (uint32_t j = 0; j < valid; j++) {
-        const float ej = S[wave][j];
-        const float2 v = *reinterpret_cast<const float2*>(vt + j * LH_HEAD_DIM);
-        a0 = __builtin_fmaf(ej, v.x, a0);
-        a1 = __builtin_fmaf(ej, v.y, a1);
+    const float* vt = reinterpret_cast<const float*>(T) + d0;
+    if (valid == LH_ATTN_BLOCK) {
+#pragma unroll
+        for (uint32_t j = 0; j < LH_ATTN_BLOCK; j++) {
+            const float ej = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
+            const float2 v = *reinterpret_cast<const float2*>(vt + j * LH_HEAD_DIM);
+            a0 = __builtin_fmaf(ej, v.x, a0);
+            a1 = __builtin_fmaf(ej, v.y, a1);
+        }
+    } else {
+        for (uint32_t j = 0; j < valid; j++) {
+            const float ej = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
+            const float2 v = *reinterpret_cast<const float2*>(vt + j * LH_HEAD_DIM);
+            a0 = __builtin_fmaf(ej, v.x, a0);
+            a1 = __builtin_fmaf(ej, v.y, a1);
+        }
+    }
+    if (!valid) {
+        return;
     }
     const size_t th = (size_t)t * LH_HEADS + kvh * 4 + wave;
     if (lane == 0) {
