@@ -438,31 +438,28 @@ extern "C" int lh_launch_embed(const uint16_t* E, const lh_step_params* params, 
 
 // ---------------------------------------------------------------------------
 // Multi-token attention on the matrix cores (the PREFILL_MPS path; the
-// precise path keeps the block/combine kernels above). FP32 MFMA
-// (v_mfma_f32_16x16x4_f32): products exact, FP32 accumulation in the
-// hardware's order, so the result is tolerance-checked, not bit-mirrored.
+// precise path keeps the block/combine kernels above): a flash attention on
+// the BF16 matrix cores (v_mfma_f32_16x16x32_bf16), tolerance-checked, not
+// bit-mirrored.
 //
 // Workgroup (16-token tile, kv head); wave w is query head 4*kvh + w over the
-// tile's tokens, so the four GQA heads share every K/V tile staged in LDS.
+// tile's tokens, so the four GQA heads share every K/V block staged in LDS.
 // Per 64-position block:
-//   S[16 x 64] = Q[16 x 128] K^T: lane group g = lane/16 feeds dims
-//     32g .. 32g+31 (one per MFMA step) of both operands; Q stays in registers.
+//   S[16 x 64] = Q[16 x 128] K^T, Q in registers;
 //   online softmax per token row in the base-2 domain (v_exp_f32), causal mask
 //   p <= length + t;
-//   O[16 x 128] += P[16 x 64] V through a per-wave P tile in LDS: lane group g
-//     feeds positions 16g .. 16g+15.
-// out = O / l. grid (ceil(count/16), 8, splits), block 256. With splits > 1
-// split z takes a contiguous range of the tile's blocks and writes its
-// unnormalized (max, sum, O) rows as part z of PM/PT/PA (partial stride
+//   O[16 x 128] += P[16 x 64] V through a per-wave P tile in LDS.
+// out = O / l. grid tiles * 8 * splits (1-D, fa_coords), block 256. With
+// splits > 1 split z takes a contiguous range of the tile's blocks and writes
+// its unnormalized (max, sum, O) rows as part z of PM/PT/PA (partial stride
 // capacity/64 per (token, head)), merged by k_attn_merge. With xs set, the
 // output goes to xs as the hi/mid/lo BF16 planes the o-projection GEMM reads
 // (plane stride xs_tokens * 4096) instead of FP32 rows of out.
-// LDS is the K tile (33 KiB, reused for the four P tiles after a barrier) and
-// the V tile (33 KiB), under 256 registers, so two workgroups share a CU and
-// the launcher sizes splits for about 512 workgroups. Measured alternative:
-// BF16 MFMA with both operands split in three exact planes (six products per
-// k chunk) ran at 1.2x on long prefixes and 0.6x on short ones, its K/V
-// splitting and transposes costing as much VALU time as the MFMAs saved.
+// Measured at 256 tokens after a 4096-token prefix: 169 us, against 198 us for
+// the same structure on the FP32 matrix cores (v_mfma_f32_16x16x4_f32, exact
+// products). Per block and workgroup (two per CU): splitting K and V into
+// planes 6.6k cycles, QK^T 6.3k, softmax 3.3k, PV 3.4k; the planes' VALU and
+// LDS work, not the matrix cores, set the time.
 namespace lh {
 
 constexpr uint32_t FA_TQ = 16;                      // tokens per workgroup
@@ -492,35 +489,120 @@ __device__ __forceinline__ float quad16_sum(float v)
     return v + __shfl_xor(v, 8, 64);
 }
 
+// Workgroup coordinates of the matrix-core attention: a 1-D grid of
+// tiles * 8 * splits workgroups whose ids are dealt round-robin to the 8
+// XCDs, arranged so that XCD x runs every (token tile, KV split) of kv head
+// x. The 16-token tiles of a kv head then re-read its K/V blocks from their
+// XCD's L2 instead of the Infinity Cache.
+struct FaCoords {
+    uint32_t t0, kvh, z, splits;
+};
+
+__device__ __forceinline__ FaCoords fa_coords(uint32_t tiles)
+{
+    const uint32_t w = blockIdx.x, qq = w >> 3;
+    return {(qq % tiles) * FA_TQ, w & 7u, qq / tiles, gridDim.x / (8 * tiles)};
+}
+
+
+// The same flash attention on the BF16 matrix cores. Every FP32 operand is
+// split into BF16 planes by truncation (hi = top 8 significant bits, the
+// remainders exact in FP32):
+//   QK^T: Q and K in three planes (hi + mid + lo == x exactly); the six
+//     cross products whose weight is above 2^-24 of the leading one
+//     (ql kh, qh kl, qm km, qm kh, qh km, qh kh, smallest first), so the
+//     scores carry about FP32 accuracy, which the softmax needs;
+//   PV: P and V in two planes (hi + mid, 16 significant bits); products
+//     pm vh, ph vm, ph vh, so the output's relative error stays near 2^-16.
+// Every BF16 product is exact in FP32; accumulation is the hardware's FP32.
+// v_mfma_f32_16x16x32_bf16 runs 16 times the FLOPs of v_mfma_f32_16x16x4_f32
+// per cycle, so nine products take about a third of the FP32 path's matrix
+// time. Workgroup and grid as described above (16 tokens x one kv head, wave
+// = query head, KV splits merged by k_attn_merge).
+// LDS (80 KiB, two workgroups per CU): the block's K planes [3][64 pos][128
+// dims] and V planes transposed [2][128 dims][64 pos], each 16-byte chunk of
+// a row XOR-swizzled by the row index so that the MFMA operand reads are
+// conflict-free (K) or 2-way (V); after the scores each wave's P planes
+// [2][16 tokens][64 pos] reuse the K planes' space.
+typedef __bf16 fa_bf16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t fa_u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr uint32_t FB_KPLANE = LH_ATTN_BLOCK * LH_HEAD_DIM * 2;   // bytes per K plane
+constexpr uint32_t FB_VPLANE = LH_ATTN_BLOCK * LH_HEAD_DIM * 2;   // bytes per V plane
+constexpr uint32_t FB_PPLANE = FA_TQ * LH_ATTN_BLOCK * 2;         // bytes per P plane
+
+// Byte offset of (row r, element e) in a K plane: rows of 256 bytes, chunk
+// e / 8 XOR (r & 15).
+__device__ __forceinline__ uint32_t fb_k_at(uint32_t r, uint32_t e)
+{
+    return r * 256 + (((e >> 3) ^ (r & 15)) << 4) + (e & 7) * 2;
+}
+
+// Byte offset of (dim d, position r) in a transposed V plane: rows of 128
+// bytes, chunk r / 8 XOR (d & 7).
+__device__ __forceinline__ uint32_t fb_v_at(uint32_t d, uint32_t r)
+{
+    return d * 128 + (((r >> 3) ^ (d & 7)) << 4) + (r & 7) * 2;
+}
+
+// Byte offset of (token t, position r) in a P plane: rows of 128 bytes.
+__device__ __forceinline__ uint32_t fb_p_at(uint32_t t, uint32_t r)
+{
+    return t * 128 + (((r >> 3) ^ (t & 7)) << 4) + (r & 7) * 2;
+}
+
+__device__ __forceinline__ uint32_t fb_hi(float x)
+{
+    return __float_as_uint(x) >> 16;
+}
+
+// Two truncated BF16 planes of x: hi and mid (x - hi, truncated).
+__device__ __forceinline__ void fb_split2(float x, uint32_t& h, uint32_t& m)
+{
+    const uint32_t hb = __float_as_uint(x) & 0xffff0000u;
+    h = hb >> 16;
+    m = __float_as_uint(x - __uint_as_float(hb)) >> 16;
+}
+
 __global__ void __launch_bounds__(256, 2)
-k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
+k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
     const float* __restrict__ vcache, uint32_t length, uint32_t count, uint32_t capacity,
     float* __restrict__ PM, float* __restrict__ PT, float* __restrict__ PA, float* __restrict__ out,
     uint16_t* __restrict__ xs, uint32_t xs_tokens)
 {
-    __shared__ __attribute__((aligned(16))) float Ks[LH_ATTN_BLOCK * FA_KS];
-    __shared__ float Vs[LH_ATTN_BLOCK * FA_VS];
-    // Each wave's P tile reuses the K tile's space once every wave has read K.
-    float (*Ps)[FA_TQ * FA_PS] = reinterpret_cast<float (*)[FA_TQ * FA_PS]>(Ks);
-    static_assert(4 * FA_TQ * FA_PS <= LH_ATTN_BLOCK * FA_KS, "P tiles fit the K tile");
-    const uint32_t t0 = blockIdx.x * FA_TQ, kvh = blockIdx.y;
+    __shared__ __attribute__((aligned(16))) uint8_t Kp[3 * FB_KPLANE];
+    __shared__ __attribute__((aligned(16))) uint8_t Vp[2 * FB_VPLANE];
+    static_assert(4 * 2 * FB_PPLANE <= 3 * FB_KPLANE, "P planes fit the K planes");
+    const FaCoords fc = fa_coords((count + FA_TQ - 1) / FA_TQ);
+    const uint32_t t0 = fc.t0, kvh = fc.kvh;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t g = lane >> 4, l16 = lane & 15;
     const uint32_t head = kvh * 4 + wave;
     const uint32_t last = (t0 + FA_TQ < count ? t0 + FA_TQ : count) - 1;   // last real token
-    // Q operand: lane (token l16, group g) holds dims 32g .. 32g+31.
+    // Q operand of k-chunk kc: lane (token l16, group g) holds dims
+    // 32 kc + 8g .. +7, as three planes.
     const uint32_t tq = t0 + l16 <= last ? t0 + l16 : last;
-    fa_floatx4 qv[8];
+    fa_bf16x8 qp[3][4];
     {
-        const fa_floatx4* src = reinterpret_cast<const fa_floatx4*>(
-            q + (size_t)tq * LH_QUERY + head * LH_HEAD_DIM + 32 * g);
+        const float4* src = reinterpret_cast<const float4*>(
+            q + (size_t)tq * LH_QUERY + head * LH_HEAD_DIM + 8 * g);
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            qv[i] = src[i];
+        for (int kc = 0; kc < 4; kc++) {
+            const float4 a = src[8 * kc], b = src[8 * kc + 1];
+            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+            fa_u32x4 h, m, l;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const bf16x3 x0 = split3(v[2 * e]), x1 = split3(v[2 * e + 1]);
+                h[e] = x0.hi | (x1.hi << 16);
+                m[e] = x0.mid | (x1.mid << 16);
+                l[e] = x0.lo | (x1.lo << 16);
+            }
+            qp[0][kc] = __builtin_bit_cast(fa_bf16x8, h);
+            qp[1][kc] = __builtin_bit_cast(fa_bf16x8, m);
+            qp[2][kc] = __builtin_bit_cast(fa_bf16x8, l);
         }
     }
-    // Accumulator rows held by this lane: tokens t0 + 4g + r (clamped to the
-    // last real token for the mask; their outputs are not stored).
     uint32_t limit[4];
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -539,17 +621,17 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
         o[i] = fa_floatx4{0.f, 0.f, 0.f, 0.f};
     }
     const uint32_t nb = (length + last + 1 + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
-    const uint32_t splits = gridDim.z, z = blockIdx.z;
+    const uint32_t splits = fc.splits, z = fc.z;
     const uint32_t per = (nb + splits - 1) / splits;
     const uint32_t b_begin = z * per < nb ? z * per : nb;
     const uint32_t b_end = b_begin + per < nb ? b_begin + per : nb;
     const size_t head_base = lh_kv_index(capacity, 0, kvh, 0);
-    float* pw = Ps[wave];
-    // K and V of block b in registers (thread tid holds float4 words
-    // tid + 256i of each 64 x 128 tile); every row is inside the capacity
-    // (the block count never exceeds it). The next block's loads are issued
-    // before this block's MFMAs, and two workgroups share a CU, so one
-    // stages its tiles while the other runs MFMAs.
+    uint8_t* pw = Kp + wave * 2 * FB_PPLANE;
+    // Raw K and V of block b in registers, the next block's issued before
+    // this block's MFMAs. K: thread tid holds float4 words tid + 256 i of the
+    // tile (lh_ktile_word order); V: rows 2 rp and 2 rp + 1, float4 column
+    // tid % 32, rp = tid / 32 + 8 i, so that two consecutive positions of a
+    // dimension pack into one 32-bit word of the transposed planes.
     fa_floatx4 kr[8], vr[8];
     auto load_block = [&](uint32_t b) {
         const fa_floatx4* kb = reinterpret_cast<const fa_floatx4*>(
@@ -559,59 +641,83 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
 #pragma unroll
         for (int i = 0; i < 8; i++) {
             kr[i] = kb[tid + 256 * i];
-            vr[i] = vb[tid + 256 * i];
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t rp = (tid >> 5) + 8 * i;
+            vr[2 * i] = vb[(2 * rp) * 32 + (tid & 31)];
+            vr[2 * i + 1] = vb[(2 * rp + 1) * 32 + (tid & 31)];
         }
     };
     if (b_begin < b_end) {
         load_block(b_begin);
     }
     // Rows past the tile's last visible position hold whatever an earlier
-    // sequence (or a failed step) left in the cache. Masked weights are 0, and
-    // 0 * Inf would be NaN in P.V, so those rows are staged as zeros.
+    // sequence (or a failed step) left in the cache; they are staged as zeros
+    // (0 * Inf would be NaN in P.V).
     const uint32_t visible = length + last;
+    const fa_floatx4 zero = fa_floatx4{0.f, 0.f, 0.f, 0.f};
     for (uint32_t b = b_begin; b < b_end; b++) {
-        // Stage K (float4 rows, stride 132) and V (stride 129) of the block.
-        __syncthreads();   // the previous block's tiles are consumed
+        __syncthreads();   // the previous block's planes and P tiles are consumed
 #pragma unroll
         for (int i = 0; i < 8; i++) {
-            const uint32_t idx = tid + 256 * i, row = idx >> 5, c4 = idx & 31;
-            // K word idx = tid + 256 i of the tile (lh_ktile_word order) holds
-            // position (idx >> 9) * 16 + (idx & 63) / 4 = 16 (i / 2) + lane / 4,
-            // dims 32 (idx & 3) + 4 ((idx >> 6) & 7) = 32 (lane % 4) + 4 (wave + 4 (i % 2)).
+            // K word tid + 256 i: position 16 (i / 2) + lane / 4, dims
+            // 32 (lane % 4) + 4 (wave + 4 (i % 2)) .. +3.
             const uint32_t krow = 16 * (i >> 1) + (lane >> 2);
-            const uint32_t kc4 = 8 * (lane & 3) + wave + 4 * (i & 1);
-            const bool live = b * LH_ATTN_BLOCK + row <= visible;
-            const bool klive = b * LH_ATTN_BLOCK + krow <= visible;
-            const fa_floatx4 zero = fa_floatx4{0.f, 0.f, 0.f, 0.f};
-            const fa_floatx4 kk = klive ? kr[i] : zero, vv = live ? vr[i] : zero;
-            *reinterpret_cast<fa_floatx4*>(&Ks[krow * FA_KS + 4 * kc4]) = kk;
-            float* vd = &Vs[row * FA_VS + 4 * c4];
-            vd[0] = vv.x;
-            vd[1] = vv.y;
-            vd[2] = vv.z;
-            vd[3] = vv.w;
+            const uint32_t kd = 32 * (lane & 3) + 4 * (wave + 4 * (i & 1));
+            const fa_floatx4 kk = b * LH_ATTN_BLOCK + krow <= visible ? kr[i] : zero;
+            const bf16x3 a0 = split3(kk.x), a1 = split3(kk.y), a2 = split3(kk.z), a3 = split3(kk.w);
+            const uint32_t at = fb_k_at(krow, kd);
+            *reinterpret_cast<uint2*>(Kp + at) =
+                make_uint2(a0.hi | (a1.hi << 16), a2.hi | (a3.hi << 16));
+            *reinterpret_cast<uint2*>(Kp + FB_KPLANE + at) =
+                make_uint2(a0.mid | (a1.mid << 16), a2.mid | (a3.mid << 16));
+            *reinterpret_cast<uint2*>(Kp + 2 * FB_KPLANE + at) =
+                make_uint2(a0.lo | (a1.lo << 16), a2.lo | (a3.lo << 16));
+        }
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t rp = (tid >> 5) + 8 * i, r0 = 2 * rp, d0 = 4 * (tid & 31);
+            const fa_floatx4 v0 = b * LH_ATTN_BLOCK + r0 <= visible ? vr[2 * i] : zero;
+            const fa_floatx4 v1 = b * LH_ATTN_BLOCK + r0 + 1 <= visible ? vr[2 * i + 1] : zero;
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                uint32_t h0, m0, h1, m1;
+                fb_split2(v0[e], h0, m0);
+                fb_split2(v1[e], h1, m1);
+                const uint32_t at = fb_v_at(d0 + e, r0);
+                *reinterpret_cast<uint32_t*>(Vp + at) = h0 | (h1 << 16);
+                *reinterpret_cast<uint32_t*>(Vp + FB_VPLANE + at) = m0 | (m1 << 16);
+            }
         }
         __syncthreads();
         if (b + 1 < b_end) {
             load_block(b + 1);   // in flight during this block's MFMAs
         }
-        // S tiles j = 0..3: positions 16j + l16 of the block.
+        // S tiles j = 0..3: positions 16j + l16; k-chunk kc: dims 32kc + 8g .. +7.
         fa_floatx4 s[4];
 #pragma unroll
         for (int j = 0; j < 4; j++) {
-            s[j] = fa_floatx4{0.f, 0.f, 0.f, 0.f};
-            const fa_floatx4* kp = reinterpret_cast<const fa_floatx4*>(&Ks[(16 * j + l16) * FA_KS + 32 * g]);
+            s[j] = zero;
+        }
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                const fa_floatx4 kk = kp[i];
-                s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[i].x, kk.x, s[j], 0, 0, 0);
-                s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[i].y, kk.y, s[j], 0, 0, 0);
-                s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[i].z, kk.z, s[j], 0, 0, 0);
-                s[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(qv[i].w, kk.w, s[j], 0, 0, 0);
+        for (int kc = 0; kc < 4; kc++) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t at = fb_k_at(16 * j + l16, 32 * kc + 8 * g);
+                const fa_bf16x8 kh = *reinterpret_cast<const fa_bf16x8*>(Kp + at);
+                const fa_bf16x8 km = *reinterpret_cast<const fa_bf16x8*>(Kp + FB_KPLANE + at);
+                const fa_bf16x8 kl = *reinterpret_cast<const fa_bf16x8*>(Kp + 2 * FB_KPLANE + at);
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[2][kc], kh, s[j], 0, 0, 0);
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[0][kc], kl, s[j], 0, 0, 0);
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[1][kc], km, s[j], 0, 0, 0);
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[1][kc], kh, s[j], 0, 0, 0);
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[0][kc], km, s[j], 0, 0, 0);
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[0][kc], kh, s[j], 0, 0, 0);
             }
         }
-        __syncthreads();   // every wave has read K; P tiles reuse its space
-        // Scale, causal mask, online softmax; P to this wave's LDS tile.
+        __syncthreads();   // every wave has read the K planes; P tiles reuse them
+        // Scale, causal mask, online softmax; P planes to this wave's tile.
 #pragma unroll
         for (int r = 0; r < 4; r++) {
             float mx = -__builtin_inff();
@@ -633,7 +739,11 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
             for (int j = 0; j < 4; j++) {
                 const float e = empty ? 0.0f : __builtin_amdgcn_exp2f(s[j][r] - m_new);
                 sum = sum + e;
-                pw[(4 * g + r) * FA_PS + 16 * j + l16] = e;
+                uint32_t h, mm;
+                fb_split2(e, h, mm);
+                const uint32_t at = fb_p_at(4 * g + r, 16 * j + l16);
+                *reinterpret_cast<uint16_t*>(pw + at) = (uint16_t)h;
+                *reinterpret_cast<uint16_t*>(pw + FB_PPLANE + at) = (uint16_t)mm;
             }
             l[r] = l[r] * alpha + quad16_sum(sum);
             m[r] = m_new;
@@ -642,24 +752,27 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
                 o[i][r] = o[i][r] * alpha;
             }
         }
-        // O += P V. A operand: lane (token l16, group g) holds P[l16][16g .. 16g+15].
-        fa_floatx4 pv[4];
-        {
-            const fa_floatx4* pp = reinterpret_cast<const fa_floatx4*>(&pw[l16 * FA_PS + 16 * g]);
+        // O += P V. A operand of position chunk pc: lane (token l16, group g)
+        // holds P[l16][32 pc + 8g .. +7]; B: V rows 32 pc + 8g .. +7 of dim
+        // 16 i + l16. The wave reads back only its own P tile, and a wave's
+        // LDS accesses complete in order.
+        fa_bf16x8 ph[2], pm[2];
 #pragma unroll
-            for (int i = 0; i < 4; i++) {
-                pv[i] = pp[i];
-            }
+        for (int pc = 0; pc < 2; pc++) {
+            const uint32_t at = fb_p_at(l16, 32 * pc + 8 * g);
+            ph[pc] = *reinterpret_cast<const fa_bf16x8*>(pw + at);
+            pm[pc] = *reinterpret_cast<const fa_bf16x8*>(pw + FB_PPLANE + at);
         }
 #pragma unroll
         for (int i = 0; i < 8; i++) {
 #pragma unroll
-            for (int k = 0; k < 4; k++) {
-                const float* vrow = &Vs[(16 * g + 4 * k) * FA_VS + 16 * i + l16];
-                o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[k].x, vrow[0], o[i], 0, 0, 0);
-                o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[k].y, vrow[FA_VS], o[i], 0, 0, 0);
-                o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[k].z, vrow[2 * FA_VS], o[i], 0, 0, 0);
-                o[i] = __builtin_amdgcn_mfma_f32_16x16x4f32(pv[k].w, vrow[3 * FA_VS], o[i], 0, 0, 0);
+            for (int pc = 0; pc < 2; pc++) {
+                const uint32_t at = fb_v_at(16 * i + l16, 32 * pc + 8 * g);
+                const fa_bf16x8 vh = *reinterpret_cast<const fa_bf16x8*>(Vp + at);
+                const fa_bf16x8 vm = *reinterpret_cast<const fa_bf16x8*>(Vp + FB_VPLANE + at);
+                o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pm[pc], vh, o[i], 0, 0, 0);
+                o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph[pc], vm, o[i], 0, 0, 0);
+                o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph[pc], vh, o[i], 0, 0, 0);
             }
         }
     }
@@ -695,7 +808,7 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
     }
 }
 
-// Merge of k_attn_mfma's KV splits (tolerance path): per (token, head)
+// Merge of k_attn_mfma_bf16's KV splits (tolerance path): per (token, head)
 // M = max m_z, f_z = exp2(m_z - M) (base-2 maxima), out = (sum f_z O_z) / (sum f_z l_z) with
 // the sums in split order. A split whose positions are all masked for the row
 // holds m = -inf, l = 0, O = 0 and contributes nothing; split 0 always holds
@@ -758,8 +871,8 @@ extern "C" int lh_launch_attention_mfma(const float* q, const float* kcache_laye
     const uint32_t by_length = nb / 2;
     splits = splits < by_length ? splits : by_length;
     splits = splits ? splits : 1;
-    hipLaunchKernelGGL(lh::k_attn_mfma, dim3(tiles, LH_KV_HEADS, splits), dim3(256), 0, s, q,
-        kcache_layer, vcache_layer, length, count, capacity, PM, PT, PA, out, xs, xs_tokens);
+    hipLaunchKernelGGL(lh::k_attn_mfma_bf16, dim3(tiles * LH_KV_HEADS * splits), dim3(256), 0, s,
+        q, kcache_layer, vcache_layer, length, count, capacity, PM, PT, PA, out, xs, xs_tokens);
     if (splits > 1) {
         hipLaunchKernelGGL(lh::k_attn_merge, dim3(count * LH_HEADS / 4), dim3(256), 0, s, PM, PT,
             PA, capacity, splits, count, out, xs, xs_tokens);
