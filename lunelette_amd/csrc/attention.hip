@@ -442,24 +442,25 @@ extern "C" int lh_launch_embed(const uint16_t* E, const lh_step_params* params, 
 // the BF16 matrix cores (v_mfma_f32_16x16x32_bf16), tolerance-checked, not
 // bit-mirrored.
 //
-// Workgroup (16-token tile, kv head); wave w is query head 4*kvh + w over the
-// tile's tokens, so the four GQA heads share every K/V block staged in LDS.
-// Per 64-position block:
+// Workgroup (32-token tile, kv head), eight waves: wave w is query head
+// 4*kvh + w % 4 over the tile's 16-token half w / 4, so the four GQA heads and
+// both halves share every K/V block staged in LDS (one staging serves 32
+// tokens), one workgroup per CU. Per 64-position block:
 //   S[16 x 64] = Q[16 x 128] K^T, Q in registers;
 //   online softmax per token row in the base-2 domain (v_exp_f32), causal mask
 //   p <= length + t;
 //   O[16 x 128] += P[16 x 64] V through a per-wave P tile in LDS.
-// out = O / l. grid tiles * 8 * splits (1-D, fa_coords), block 256. With
+// out = O / l. grid tiles * 8 * splits (1-D, fa_coords), block 512. With
 // splits > 1 split z takes a contiguous range of the tile's blocks and writes
 // its unnormalized (max, sum, O) rows as part z of PM/PT/PA (partial stride
 // capacity/64 per (token, head)), merged by k_attn_merge. With xs set, the
 // output goes to xs as the hi/mid/lo BF16 planes the o-projection GEMM reads
 // (plane stride xs_tokens * 4096) instead of FP32 rows of out.
-// Measured at 256 tokens after a 4096-token prefix: 169 us, against 198 us for
-// the same structure on the FP32 matrix cores (v_mfma_f32_16x16x4_f32, exact
-// products). Per block and workgroup (two per CU): splitting K and V into
-// planes 6.6k cycles, QK^T 6.3k, softmax 3.3k, PV 3.4k; the planes' VALU and
-// LDS work, not the matrix cores, set the time.
+// Measured at 256 tokens after a 4096-token prefix: 129 us. The same kernel
+// with 16-token workgroups of four waves, two per CU, ran 169 us (per block
+// and workgroup: splitting K and V into planes 6.6k cycles, QK^T 6.3k,
+// softmax 3.3k, PV 3.4k); the FP32 matrix cores (v_mfma_f32_16x16x4_f32,
+// exact products) with the 16-token structure 198 us.
 namespace lh {
 
 constexpr uint32_t FA_TQ = 16;                      // tokens per workgroup
@@ -517,9 +518,8 @@ __device__ __forceinline__ FaCoords fa_coords(uint32_t tiles)
 // Every BF16 product is exact in FP32; accumulation is the hardware's FP32.
 // v_mfma_f32_16x16x32_bf16 runs 16 times the FLOPs of v_mfma_f32_16x16x4_f32
 // per cycle, so nine products take about a third of the FP32 path's matrix
-// time. Workgroup and grid as described above (16 tokens x one kv head, wave
-// = query head, KV splits merged by k_attn_merge).
-// LDS (80 KiB, two workgroups per CU): the block's K planes [3][64 pos][128
+// time. Workgroup and grid as described above.
+// LDS (80 KiB): the block's K planes [3][64 pos][128
 // dims] and V planes transposed [2][128 dims][64 pos], each 16-byte chunk of
 // a row XOR-swizzled by the row index so that the MFMA operand reads are
 // conflict-free (K) or 2-way (V); after the scores each wave's P planes
@@ -564,7 +564,7 @@ __device__ __forceinline__ void fb_split2(float x, uint32_t& h, uint32_t& m)
     m = __float_as_uint(x - __uint_as_float(hb)) >> 16;
 }
 
-__global__ void __launch_bounds__(256, 2)
+__global__ void __launch_bounds__(512, 1)
 k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
     const float* __restrict__ vcache, uint32_t length, uint32_t count, uint32_t capacity,
     float* __restrict__ PM, float* __restrict__ PT, float* __restrict__ PA, float* __restrict__ out,
@@ -572,13 +572,16 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
 {
     __shared__ __attribute__((aligned(16))) uint8_t Kp[3 * FB_KPLANE];
     __shared__ __attribute__((aligned(16))) uint8_t Vp[2 * FB_VPLANE];
-    static_assert(4 * 2 * FB_PPLANE <= 3 * FB_KPLANE, "P planes fit the K planes");
-    const FaCoords fc = fa_coords((count + FA_TQ - 1) / FA_TQ);
-    const uint32_t t0 = fc.t0, kvh = fc.kvh;
+    static_assert(8 * 2 * FB_PPLANE <= 3 * FB_KPLANE, "P planes fit the K planes");
+    const FaCoords fc = fa_coords((count + 2 * FA_TQ - 1) / (2 * FA_TQ));
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const uint32_t t0 = 2 * fc.t0 + FA_TQ * (wave >> 2), kvh = fc.kvh;
     const uint32_t g = lane >> 4, l16 = lane & 15;
-    const uint32_t head = kvh * 4 + wave;
-    const uint32_t last = (t0 + FA_TQ < count ? t0 + FA_TQ : count) - 1;   // last real token
+    const uint32_t head = kvh * 4 + (wave & 3);
+    // The second 16-token subtile can lie past count: it then runs on the
+    // first subtile's last token (clamped) and stores nothing.
+    const uint32_t t0c = t0 < count ? t0 : t0 - FA_TQ;
+    const uint32_t last = (t0c + FA_TQ < count ? t0c + FA_TQ : count) - 1;   // last real token
     // Q operand of k-chunk kc: lane (token l16, group g) holds dims
     // 32 kc + 8g .. +7, as three planes.
     const uint32_t tq = t0 + l16 <= last ? t0 + l16 : last;
@@ -620,7 +623,11 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
     for (int i = 0; i < 8; i++) {
         o[i] = fa_floatx4{0.f, 0.f, 0.f, 0.f};
     }
-    const uint32_t nb = (length + last + 1 + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
+    // The block range and the staging's visible rows follow the workgroup's
+    // last token (both subtiles share every barrier and every staged block).
+    const uint32_t tw = 2 * fc.t0;
+    const uint32_t last_wg = (tw + 2 * FA_TQ < count ? tw + 2 * FA_TQ : count) - 1;
+    const uint32_t nb = (length + last_wg + 1 + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
     const uint32_t splits = fc.splits, z = fc.z;
     const uint32_t per = (nb + splits - 1) / splits;
     const uint32_t b_begin = z * per < nb ? z * per : nb;
@@ -632,19 +639,19 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
     // tile (lh_ktile_word order); V: rows 2 rp and 2 rp + 1, float4 column
     // tid % 32, rp = tid / 32 + 8 i, so that two consecutive positions of a
     // dimension pack into one 32-bit word of the transposed planes.
-    fa_floatx4 kr[8], vr[8];
+    fa_floatx4 kr[4], vr[4];
     auto load_block = [&](uint32_t b) {
         const fa_floatx4* kb = reinterpret_cast<const fa_floatx4*>(
             kcache + head_base + (size_t)b * LH_ATTN_BLOCK * LH_HEAD_DIM);
         const fa_floatx4* vb = reinterpret_cast<const fa_floatx4*>(
             vcache + head_base + (size_t)b * LH_ATTN_BLOCK * LH_HEAD_DIM);
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            kr[i] = kb[tid + 256 * i];
+        for (int i = 0; i < 4; i++) {
+            kr[i] = kb[tid + 512 * i];
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t rp = (tid >> 5) + 8 * i;
+        for (int i = 0; i < 2; i++) {
+            const uint32_t rp = (tid >> 5) + 16 * i;
             vr[2 * i] = vb[(2 * rp) * 32 + (tid & 31)];
             vr[2 * i + 1] = vb[(2 * rp + 1) * 32 + (tid & 31)];
         }
@@ -655,16 +662,18 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
     // Rows past the tile's last visible position hold whatever an earlier
     // sequence (or a failed step) left in the cache; they are staged as zeros
     // (0 * Inf would be NaN in P.V).
-    const uint32_t visible = length + last;
+    const uint32_t visible = length + last_wg;
     const fa_floatx4 zero = fa_floatx4{0.f, 0.f, 0.f, 0.f};
     for (uint32_t b = b_begin; b < b_end; b++) {
         __syncthreads();   // the previous block's planes and P tiles are consumed
 #pragma unroll
-        for (int i = 0; i < 8; i++) {
-            // K word tid + 256 i: position 16 (i / 2) + lane / 4, dims
-            // 32 (lane % 4) + 4 (wave + 4 (i % 2)) .. +3.
-            const uint32_t krow = 16 * (i >> 1) + (lane >> 2);
-            const uint32_t kd = 32 * (lane & 3) + 4 * (wave + 4 * (i & 1));
+        for (int i = 0; i < 4; i++) {
+            // K word tid + 512 i = (tid % 256) + 256 i2, i2 = 2 i + tid / 256:
+            // position 16 (i2 / 2) + lane / 4, dims 32 (lane % 4) +
+            // 4 (w4 + 4 (i2 % 2)) .. +3, w4 = (tid / 64) % 4.
+            const uint32_t i2 = 2 * i + (tid >> 8), w4 = wave & 3;
+            const uint32_t krow = 16 * (i2 >> 1) + (lane >> 2);
+            const uint32_t kd = 32 * (lane & 3) + 4 * (w4 + 4 * (i2 & 1));
             const fa_floatx4 kk = b * LH_ATTN_BLOCK + krow <= visible ? kr[i] : zero;
             const bf16x3 a0 = split3(kk.x), a1 = split3(kk.y), a2 = split3(kk.z), a3 = split3(kk.w);
             const uint32_t at = fb_k_at(krow, kd);
@@ -676,8 +685,8 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
                 make_uint2(a0.lo | (a1.lo << 16), a2.lo | (a3.lo << 16));
         }
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint32_t rp = (tid >> 5) + 8 * i, r0 = 2 * rp, d0 = 4 * (tid & 31);
+        for (int i = 0; i < 2; i++) {
+            const uint32_t rp = (tid >> 5) + 16 * i, r0 = 2 * rp, d0 = 4 * (tid & 31);
             const fa_floatx4 v0 = b * LH_ATTN_BLOCK + r0 <= visible ? vr[2 * i] : zero;
             const fa_floatx4 v1 = b * LH_ATTN_BLOCK + r0 + 1 <= visible ? vr[2 * i + 1] : zero;
 #pragma unroll
@@ -776,6 +785,9 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
             }
         }
     }
+    if (t0 >= count) {
+        return;
+    }
     const uint32_t nbc = capacity / LH_ATTN_BLOCK;
 #pragma unroll
     for (int r = 0; r < 4; r++) {
@@ -862,16 +874,16 @@ extern "C" int lh_launch_attention_mfma(const float* q, const float* kcache_laye
         (xs && xs_tokens < count)) {
         return -1;
     }
-    // KV splits so that about 512 workgroups run (two per CU): each takes at
+    // KV splits so that about 256 workgroups run (one per CU): each takes at
     // least 2 blocks of the longest tile (a 256-token chunk with no prefix
     // runs 2 splits), at most one partial per block.
-    const uint32_t tiles = (count + lh::FA_TQ - 1) / lh::FA_TQ;
+    const uint32_t tiles = (count + 2 * lh::FA_TQ - 1) / (2 * lh::FA_TQ);
     const uint32_t nb = (length + count + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
-    uint32_t splits = 512 / (tiles * LH_KV_HEADS);
+    uint32_t splits = 256 / (tiles * LH_KV_HEADS);
     const uint32_t by_length = nb / 2;
     splits = splits < by_length ? splits : by_length;
     splits = splits ? splits : 1;
-    hipLaunchKernelGGL(lh::k_attn_mfma_bf16, dim3(tiles * LH_KV_HEADS * splits), dim3(256), 0, s,
+    hipLaunchKernelGGL(lh::k_attn_mfma_bf16, dim3(tiles * LH_KV_HEADS * splits), dim3(512), 0, s,
         q, kcache_layer, vcache_layer, length, count, capacity, PM, PT, PA, out, xs, xs_tokens);
     if (splits > 1) {
         hipLaunchKernelGGL(lh::k_attn_merge, dim3(count * LH_HEADS / 4), dim3(256), 0, s, PM, PT,
