@@ -456,11 +456,14 @@ extern "C" int lh_launch_embed(const uint16_t* E, const lh_step_params* params, 
 // capacity/64 per (token, head)), merged by k_attn_merge. With xs set, the
 // output goes to xs as the hi/mid/lo BF16 planes the o-projection GEMM reads
 // (plane stride xs_tokens * 4096) instead of FP32 rows of out.
-// Measured at 256 tokens after a 4096-token prefix: 129 us. The same kernel
-// with 16-token workgroups of four waves, two per CU, ran 169 us (per block
-// and workgroup: splitting K and V into planes 6.6k cycles, QK^T 6.3k,
-// softmax 3.3k, PV 3.4k); the FP32 matrix cores (v_mfma_f32_16x16x4_f32,
-// exact products) with the 16-token structure 198 us.
+// Measured at 256 tokens after a 4096-token prefix: 106 us; per block and
+// workgroup about 2.0k cycles of plane split, 3.1k of QK^T (at the matrix
+// cores' rate for two waves per SIMD), 2.0k of PV and 2.5k of barrier skew.
+// Before: V's transposed planes and the P tiles in 128-byte rows with an XOR
+// swizzle (16-way bank conflicts on the staging writes, 5.3k cycles of split)
+// and the softmax's row reductions through LDS swizzles, 129 us; 16-token
+// workgroups of four waves, two per CU, 169 us; the FP32 matrix cores
+// (v_mfma_f32_16x16x4_f32, exact products) with 16-token workgroups 198 us.
 namespace lh {
 
 constexpr uint32_t FA_TQ = 16;                      // tokens per workgroup
@@ -474,20 +477,30 @@ constexpr float FA_SCALE_LOG2 = 0.12751743074062763f;
 
 typedef float fa_floatx4 __attribute__((ext_vector_type(4)));
 
+// Maximum and sum over each aligned group of 16 lanes, in every lane of the
+// group: rotations by 8, 4, 2, 1 within the 16-lane row (DPP row_ror, VALU
+// only). Each lane sums in its own order, so the sums of a group may differ
+// in the last bits (tolerance path only).
+template <int R>
+__device__ __forceinline__ float row_ror(float v)
+{
+    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x120 + R, 0xf, 0xf, false));
+}
+
 __device__ __forceinline__ float quad16_max(float v)
 {
-    v = fmaxf(v, __shfl_xor(v, 1, 64));
-    v = fmaxf(v, __shfl_xor(v, 2, 64));
-    v = fmaxf(v, __shfl_xor(v, 4, 64));
-    return fmaxf(v, __shfl_xor(v, 8, 64));
+    v = fmaxf(v, row_ror<8>(v));
+    v = fmaxf(v, row_ror<4>(v));
+    v = fmaxf(v, row_ror<2>(v));
+    return fmaxf(v, row_ror<1>(v));
 }
 
 __device__ __forceinline__ float quad16_sum(float v)
 {
-    v = v + __shfl_xor(v, 1, 64);
-    v = v + __shfl_xor(v, 2, 64);
-    v = v + __shfl_xor(v, 4, 64);
-    return v + __shfl_xor(v, 8, 64);
+    v = v + row_ror<8>(v);
+    v = v + row_ror<4>(v);
+    v = v + row_ror<2>(v);
+    return v + row_ror<1>(v);
 }
 
 // Workgroup coordinates of the matrix-core attention: a 1-D grid of
@@ -519,17 +532,21 @@ __device__ __forceinline__ FaCoords fa_coords(uint32_t tiles)
 // v_mfma_f32_16x16x32_bf16 runs 16 times the FLOPs of v_mfma_f32_16x16x4_f32
 // per cycle, so nine products take about a third of the FP32 path's matrix
 // time. Workgroup and grid as described above.
-// LDS (80 KiB): the block's K planes [3][64 pos][128
-// dims] and V planes transposed [2][128 dims][64 pos], each 16-byte chunk of
-// a row XOR-swizzled by the row index so that the MFMA operand reads are
-// conflict-free (K) or 2-way (V); after the scores each wave's P planes
-// [2][16 tokens][64 pos] reuse the K planes' space.
+// LDS (84 KiB): the block's K planes [3][64 pos][128 dims], each 16-byte
+// chunk of a row XOR-swizzled by the row index, and V planes transposed
+// [2][128 dims][64 pos] in 144-byte rows, so the MFMA operand reads and the
+// staging writes are conflict-free; after the scores each wave's P planes
+// [2][16 tokens][64 pos] (144-byte rows) reuse the K planes' space.
 typedef __bf16 fa_bf16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t fa_u32x4 __attribute__((ext_vector_type(4)));
 
+// Transposed V and P rows hold 64 positions (128 bytes) padded to 144 bytes:
+// 16 consecutive rows then start 36 banks apart, which spreads the operand
+// reads and the staging writes over all 64 banks.
+constexpr uint32_t FB_ROW = 144;
 constexpr uint32_t FB_KPLANE = LH_ATTN_BLOCK * LH_HEAD_DIM * 2;   // bytes per K plane
-constexpr uint32_t FB_VPLANE = LH_ATTN_BLOCK * LH_HEAD_DIM * 2;   // bytes per V plane
-constexpr uint32_t FB_PPLANE = FA_TQ * LH_ATTN_BLOCK * 2;         // bytes per P plane
+constexpr uint32_t FB_VPLANE = LH_HEAD_DIM * FB_ROW;              // bytes per V plane
+constexpr uint32_t FB_PPLANE = FA_TQ * FB_ROW;                    // bytes per P plane
 
 // Byte offset of (row r, element e) in a K plane: rows of 256 bytes, chunk
 // e / 8 XOR (r & 15).
@@ -538,17 +555,16 @@ __device__ __forceinline__ uint32_t fb_k_at(uint32_t r, uint32_t e)
     return r * 256 + (((e >> 3) ^ (r & 15)) << 4) + (e & 7) * 2;
 }
 
-// Byte offset of (dim d, position r) in a transposed V plane: rows of 128
-// bytes, chunk r / 8 XOR (d & 7).
+// Byte offset of (dim d, position r) in a transposed V plane.
 __device__ __forceinline__ uint32_t fb_v_at(uint32_t d, uint32_t r)
 {
-    return d * 128 + (((r >> 3) ^ (d & 7)) << 4) + (r & 7) * 2;
+    return d * FB_ROW + r * 2;
 }
 
-// Byte offset of (token t, position r) in a P plane: rows of 128 bytes.
+// Byte offset of (token t, position r) in a P plane.
 __device__ __forceinline__ uint32_t fb_p_at(uint32_t t, uint32_t r)
 {
-    return t * 128 + (((r >> 3) ^ (t & 7)) << 4) + (r & 7) * 2;
+    return t * FB_ROW + r * 2;
 }
 
 __device__ __forceinline__ uint32_t fb_hi(float x)
@@ -639,7 +655,17 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
     // tile (lh_ktile_word order); V: rows 2 rp and 2 rp + 1, float4 column
     // tid % 32, rp = tid / 32 + 8 i, so that two consecutive positions of a
     // dimension pack into one 32-bit word of the transposed planes.
-    fa_floatx4 kr[4], vr[4];
+    // V staging item j (0..7) of thread tid: lane l of wave w takes dim
+    // 16 (j % 8) + l % 16 and positions r0, r0 + 1 with r0 = 2 (4 w + l / 16),
+    // so one wave instruction covers 16 dims x 4 position pairs: the loads
+    // read 4 x 64 contiguous bytes, and the packed-pair writes of the
+    // transposed planes land on 64 distinct banks.
+    auto v_item = [&](int j, uint32_t& d, uint32_t& r0) {
+        d = 16 * j + (lane & 15);
+        r0 = 2 * (4 * wave + (lane >> 4));
+    };
+    fa_floatx4 kr[4];
+    float vr[16];
     auto load_block = [&](uint32_t b) {
         const fa_floatx4* kb = reinterpret_cast<const fa_floatx4*>(
             kcache + head_base + (size_t)b * LH_ATTN_BLOCK * LH_HEAD_DIM);
@@ -649,11 +675,13 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
         for (int i = 0; i < 4; i++) {
             kr[i] = kb[tid + 512 * i];
         }
+        const float* vf = reinterpret_cast<const float*>(vb);
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const uint32_t rp = (tid >> 5) + 16 * i;
-            vr[2 * i] = vb[(2 * rp) * 32 + (tid & 31)];
-            vr[2 * i + 1] = vb[(2 * rp + 1) * 32 + (tid & 31)];
+        for (int j = 0; j < 8; j++) {
+            uint32_t d, r0;
+            v_item(j, d, r0);
+            vr[2 * j] = vf[r0 * LH_HEAD_DIM + d];
+            vr[2 * j + 1] = vf[(r0 + 1) * LH_HEAD_DIM + d];
         }
     };
     if (b_begin < b_end) {
@@ -685,19 +713,17 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
                 make_uint2(a0.lo | (a1.lo << 16), a2.lo | (a3.lo << 16));
         }
 #pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const uint32_t rp = (tid >> 5) + 16 * i, r0 = 2 * rp, d0 = 4 * (tid & 31);
-            const fa_floatx4 v0 = b * LH_ATTN_BLOCK + r0 <= visible ? vr[2 * i] : zero;
-            const fa_floatx4 v1 = b * LH_ATTN_BLOCK + r0 + 1 <= visible ? vr[2 * i + 1] : zero;
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                uint32_t h0, m0, h1, m1;
-                fb_split2(v0[e], h0, m0);
-                fb_split2(v1[e], h1, m1);
-                const uint32_t at = fb_v_at(d0 + e, r0);
-                *reinterpret_cast<uint32_t*>(Vp + at) = h0 | (h1 << 16);
-                *reinterpret_cast<uint32_t*>(Vp + FB_VPLANE + at) = m0 | (m1 << 16);
-            }
+        for (int j = 0; j < 8; j++) {
+            uint32_t d, r0;
+            v_item(j, d, r0);
+            const float v0 = b * LH_ATTN_BLOCK + r0 <= visible ? vr[2 * j] : 0.0f;
+            const float v1 = b * LH_ATTN_BLOCK + r0 + 1 <= visible ? vr[2 * j + 1] : 0.0f;
+            uint32_t h0, m0, h1, m1;
+            fb_split2(v0, h0, m0);
+            fb_split2(v1, h1, m1);
+            const uint32_t at = fb_v_at(d, r0);
+            *reinterpret_cast<uint32_t*>(Vp + at) = h0 | (h1 << 16);
+            *reinterpret_cast<uint32_t*>(Vp + FB_VPLANE + at) = m0 | (m1 << 16);
         }
         __syncthreads();
         if (b + 1 < b_end) {
