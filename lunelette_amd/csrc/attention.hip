@@ -826,7 +826,8 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
 #pragma unroll
             for (int i = 0; i < 8; i++) {
                 if (xs) {
-                    store_split1(xs, (size_t)xs_tokens * LH_QUERY, at + 16 * i, o[i][r] / l[r]);
+                    store_split1(xs, (size_t)xs_tokens * LH_QUERY,
+                        xs_at(t, head * LH_HEAD_DIM + l16 + 16 * i, LH_QUERY), o[i][r] / l[r]);
                 } else {
                     out[at + 16 * i] = o[i][r] / l[r];
                 }
@@ -857,7 +858,17 @@ k_attn_merge(const float* __restrict__ PM, const float* __restrict__ PT,
     const float* __restrict__ PA, uint32_t capacity, uint32_t parts, uint32_t count,
     float* __restrict__ out, uint16_t* __restrict__ xs, uint32_t xs_tokens)
 {
-    const uint32_t th = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    // Workgroup w merges four heads of one token. When count is a multiple of
+    // 128 the workgroups of a 16-token group share an XCD (ids are dealt
+    // round-robin to the 8 XCDs), so the plane blocks the group shares
+    // (xs_at) are written through one L2.
+    uint32_t th = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (count % 128 == 0) {
+        const uint32_t w = blockIdx.x, q = w >> 3, hg = q & 7;
+        const uint32_t t = (((q >> 7) << 3) + (w & 7)) * 16 + ((q >> 3) & 15);
+        th = t * LH_HEADS + hg * 4 + (threadIdx.x >> 6);
+    }
+    const uint32_t lane = threadIdx.x & 63;
     if (th >= count * LH_HEADS) {
         return;
     }
@@ -882,8 +893,13 @@ k_attn_merge(const float* __restrict__ PM, const float* __restrict__ PT,
     const size_t at = (size_t)t * LH_QUERY + h * LH_HEAD_DIM + 2 * lane;
     if (xs) {
         const size_t plane = (size_t)xs_tokens * LH_QUERY;
-        store_split1(xs, plane, at, A.x / T);
-        store_split1(xs, plane, at + 1, A.y / T);
+        // The lane's two columns are adjacent in the plane: one 4-byte store
+        // per plane.
+        const size_t at2 = xs_at(t, h * LH_HEAD_DIM + 2 * lane, LH_QUERY);
+        const bf16x3 a = split3(A.x / T), b = split3(A.y / T);
+        *reinterpret_cast<uint32_t*>(xs + at2) = a.hi | (b.hi << 16);
+        *reinterpret_cast<uint32_t*>(xs + plane + at2) = a.mid | (b.mid << 16);
+        *reinterpret_cast<uint32_t*>(xs + 2 * plane + at2) = a.lo | (b.lo << 16);
     } else {
         *reinterpret_cast<float2*>(out + at) = make_float2(A.x / T, A.y / T);
     }

@@ -138,6 +138,34 @@ __device__ __forceinline__ float silu(float v)
     return v / (1.0f + expf_cw(-v));
 }
 
+// Element (token t, column c) of one activation plane of the matrix-core
+// GEMMs, for a K-column plane (K a multiple of 64). The plane is tiled so
+// that each MFMA A fragment is one contiguous 1 KiB block: 16 tokens x one
+// 64-column stage x one 8-column half h of each 16-column group g. Block
+// ((t / 16) * (K / 64) + c / 64) * 2 + h holds, at 16-byte word
+// g * 16 + t % 16, the eight columns 16g + 8h .. +7 of token t, so lane
+// l = 16g + t % 16 of a wave reads its fragment with one 16-byte load at
+// l * 16 bytes. Four columns c .. c+3 with c % 4 == 0 stay contiguous.
+__device__ __forceinline__ size_t xs_at(uint32_t t, uint32_t c, uint32_t K)
+{
+    return ((((size_t)(t >> 4) * (K >> 6) + (c >> 6)) * 2 + ((c >> 3) & 1)) << 9) +
+        ((((c >> 4) & 3) * 16 + (t & 15)) << 3) + (c & 7);
+}
+
+// Token of workgroup w in a launch of one workgroup per token row (count
+// rows) that writes activation planes: when count is a multiple of 128,
+// every 16-token group goes to one XCD (workgroup ids are dealt round-robin
+// to the 8 XCDs), so the plane blocks it shares (xs_at) are written through
+// one L2; otherwise token w.
+__device__ __forceinline__ uint32_t xs_token(uint32_t w, uint32_t count)
+{
+    if (count % 128) {
+        return w;
+    }
+    const uint32_t q = w >> 3;
+    return (((q >> 4) << 3) + (w & 7)) * 16 + (q & 15);
+}
+
 // Exact split x = hi + mid + lo into three BF16 values (truncations; each
 // residual is exact in FP32 because each step removes the leading 8
 // significant bits), returned as 16-bit patterns.

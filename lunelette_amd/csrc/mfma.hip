@@ -214,15 +214,15 @@ __global__ void __launch_bounds__(256)
 k_split(const float* __restrict__ x, uint16_t* __restrict__ xs, uint32_t width,
     uint32_t stride_tokens)
 {
-    const uint32_t t = blockIdx.x, j = blockIdx.y * 256 + threadIdx.x;
+    const uint32_t t = xs_token(blockIdx.x, gridDim.x), j = blockIdx.y * 256 + threadIdx.x;
     if (8 * j >= width) {
         return;
     }
     const float4* row = reinterpret_cast<const float4*>(x + (size_t)t * width);
     const float4 a = row[2 * j], b = row[2 * j + 1];
-    const size_t plane = (size_t)stride_tokens * width, at = (size_t)t * width + 8 * j;
-    store_split4(xs, plane, at, a);
-    store_split4(xs, plane, at + 4, b);
+    const size_t plane = (size_t)stride_tokens * width;
+    store_split4(xs, plane, xs_at(t, 8 * j, width), a);
+    store_split4(xs, plane, xs_at(t, 8 * j + 4, width), b);
 }
 
 // One token row of 3072 per workgroup: with S > 0, the split-K residual
@@ -250,7 +250,7 @@ k_residual_norm_split(const float* __restrict__ partial, size_t split_stride, fl
     __shared__ float4 row_l[LH_HIDDEN / 4];
     __shared__ float r_s;
     __shared__ float wmax[LH_HIDDEN / 4 / 64];
-    const uint32_t t = blockIdx.x, tid = threadIdx.x;
+    const uint32_t t = xs_token(blockIdx.x, gridDim.x), tid = threadIdx.x;
     float4* xr = reinterpret_cast<float4*>(x + (size_t)t * LH_HIDDEN);
     const float4 g = reinterpret_cast<const float4*>(gamma)[tid];
     float4 v = xr[tid];
@@ -287,7 +287,7 @@ k_residual_norm_split(const float* __restrict__ partial, size_t split_stride, fl
     const float r = r_s;
     const float4 y = make_float4(g.x * (v.x * r), g.y * (v.y * r), g.z * (v.z * r), g.w * (v.w * r));
     if constexpr (!F16) {
-        store_split4(xs, (size_t)stride_tokens * LH_HIDDEN, (size_t)t * LH_HIDDEN + 4 * tid, y);
+        store_split4(xs, (size_t)stride_tokens * LH_HIDDEN, xs_at(t, 4 * tid, LH_HIDDEN), y);
         return;
     }
     const float m = wave_max64(absmax4(y));
@@ -304,7 +304,7 @@ k_residual_norm_split(const float* __restrict__ partial, size_t split_stride, fl
     if (tid == 0) {
         out_scale[t] = exp2i(-e);
     }
-    store_f16x2_4(xs, (size_t)stride_tokens * LH_HIDDEN, (size_t)t * LH_HIDDEN + 4 * tid,
+    store_f16x2_4(xs, (size_t)stride_tokens * LH_HIDDEN, xs_at(t, 4 * tid, LH_HIDDEN),
         scale4(y, exp2i(e)));
 }
 
@@ -328,7 +328,7 @@ k_split_silu(const float* __restrict__ partial, size_t split_stride, float2 scal
     float* __restrict__ out_scale, uint32_t stride_tokens, uint32_t groups)
 {
     __shared__ float wmax[3];
-    const uint32_t t = blockIdx.x, grp = blockIdx.y, j = threadIdx.x;
+    const uint32_t t = xs_token(blockIdx.x, gridDim.x), grp = blockIdx.y, j = threadIdx.x;
     const bool active = j < GROUP4;
     // Idle lanes load (and discard) the group's last column: no branch around loads.
     const uint32_t c4 = grp * GROUP4 + (active ? j : GROUP4 - 1);
@@ -353,7 +353,7 @@ k_split_silu(const float* __restrict__ partial, size_t split_stride, float2 scal
         out_scale[t * DOWN_SPLITS + grp] = exp2i(-e);
     }
     if (active) {
-        store_f16x2_4(xs, (size_t)stride_tokens * LH_INNER, (size_t)t * LH_INNER + 4 * c4,
+        store_f16x2_4(xs, (size_t)stride_tokens * LH_INNER, xs_at(t, 4 * c4, LH_INNER),
             scale4(y, exp2i(e)));
     }
 }
@@ -572,12 +572,15 @@ __device__ __forceinline__ void gemm_tile(const uint8_t* __restrict__ W0,
 #pragma unroll
     for (int i = 0; i < (int)PW; i++) {
         const uint32_t f = PW * wave + i, mf = f / (2 * P), p = (f / 2) % P, h = f % 2;
-        asrc[i] = xs + p * plane + (size_t)(m0 + 16 * mf + l16) * K + k0 + 16 * g + 8 * h;
+        asrc[i] = xs + p * plane + xs_at(m0 + 16 * mf, k0 + 8 * h, K) + 8 * lane;
     }
+    // One contiguous 1 KiB fragment per load (xs_at): stage dk / 64 further
+    // on is 1024 elements further on.
     auto load_a = [&](uint32_t dk, uint8_t* buf) {
 #pragma unroll
         for (int i = 0; i < (int)PW; i++) {
-            __builtin_amdgcn_global_load_lds(asrc[i] + dk, buf + (PW * wave + i) * 1024, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(asrc[i] + (dk / BK) * 1024, buf + (PW * wave + i) * 1024,
+                16, 0, 0);
         }
     };
     u32x4 wr[4];
@@ -679,13 +682,14 @@ __device__ __forceinline__ void gemm_stream_tile(const uint8_t* __restrict__ W0,
 #pragma unroll
     for (int i = 0; i < (int)PW; i++) {
         const uint32_t f = PW * wave + i, mf = f / (2 * P), p = (f / 2) % P, h = f % 2;
-        abase[i] = xs + p * plane + (size_t)(m0 + 16 * mf + l16) * K + 16 * g + 8 * h;
+        abase[i] = xs + p * plane + xs_at(m0 + 16 * mf, 8 * h, K) + 8 * lane;
     }
     auto load_a = [&](uint32_t u, uint8_t* buf) {
-        const uint32_t dk = (u % stages) * BK;
+        const uint32_t st = u % stages;
 #pragma unroll
         for (int i = 0; i < (int)PW; i++) {
-            __builtin_amdgcn_global_load_lds(abase[i] + dk, buf + (PW * wave + i) * 1024, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(abase[i] + st * 1024, buf + (PW * wave + i) * 1024, 16,
+                0, 0);
         }
     };
     u32x4 wr[4];
