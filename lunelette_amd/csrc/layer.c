@@ -77,7 +77,38 @@ void lh_workspace_destroy(lh_workspace *ws)
         lh_dev_free(device[i]);
     }
     lh_host_free(ws->h_params);
+    free(ws->h_yarn);
+    free(ws->h_yarn_ready);
     free(ws);
+}
+
+/* Row p of the workspace's host YaRN table (cos[64], sin[64]), computed by
+ * lh_yarn on first use: a 256-token chunk otherwise spends about 0.35 ms of
+ * host time in powf/sinf/cosf before its first launch. NULL when the table
+ * cannot be allocated. */
+static const float *yarn_row(lh_workspace *ws, size_t p)
+{
+    if (!ws->h_yarn) {
+        ws->h_yarn = malloc(ws->capacity * 128 * sizeof(float));
+        ws->h_yarn_ready = calloc(ws->capacity, 1);
+        if (!ws->h_yarn || !ws->h_yarn_ready) {
+            free(ws->h_yarn);
+            free(ws->h_yarn_ready);
+            ws->h_yarn = NULL;
+            ws->h_yarn_ready = NULL;
+            lh_set_error("workspace: host allocation failed");
+            return NULL;
+        }
+    }
+    float *row = ws->h_yarn + p * 128;
+    if (!ws->h_yarn_ready[p]) {
+        float cosine[128], sine[128];
+        lh_yarn((uint32_t)p, cosine, sine);
+        memcpy(row, cosine, 64 * sizeof(float));
+        memcpy(row + 64, sine, 64 * sizeof(float));
+        ws->h_yarn_ready[p] = 1;
+    }
+    return row;
 }
 
 int lh_workspace_set_tokens(lh_workspace *ws, const int64_t *ids, size_t length, size_t count,
@@ -106,10 +137,15 @@ int lh_workspace_set_tokens(lh_workspace *ws, const int64_t *ids, size_t length,
         tp->id = (int32_t)ids[t];
         tp->position = position;
         tp->qfactor = lh_query_factor(position);
-        if (lh_yarn(position, tp->cosine, tp->sine)) {
-            lh_set_error("set_tokens: position out of range");
+        /* lh_yarn's rows repeat their 64 values in both halves. */
+        const float *row = yarn_row(ws, position);
+        if (!row) {
             return -1;
         }
+        memcpy(tp->cosine, row, 64 * sizeof(float));
+        memcpy(tp->cosine + 64, row, 64 * sizeof(float));
+        memcpy(tp->sine, row + 64, 64 * sizeof(float));
+        memcpy(tp->sine + 64, row + 64, 64 * sizeof(float));
     }
     const size_t bytes = offsetof(lh_step_params, tokens) + count * sizeof(lh_token_params);
     if (check(hipMemcpyAsync(ws->d_params, p, bytes, hipMemcpyHostToDevice, s),
@@ -130,23 +166,15 @@ int lh_workspace_prepare_decode(lh_workspace *ws)
     if (ws->d_yarn) {
         return 0;
     }
-    const size_t floats = ws->capacity * 128;
-    float *table = malloc(floats * sizeof(float));
-    if (!table) {
-        lh_set_error("prepare_decode: host allocation failed");
-        return -1;
-    }
-    float cosine[128], sine[128];
     for (size_t p = 0; p < ws->capacity; p++) {
-        lh_yarn((uint32_t)p, cosine, sine);
-        memcpy(table + p * 128, cosine, 64 * sizeof(float));
-        memcpy(table + p * 128 + 64, sine, 64 * sizeof(float));
+        if (!yarn_row(ws, p)) {
+            return -1;
+        }
     }
-    const int failed = alloc_device((void **)&ws->d_yarn, floats * sizeof(float), &ws->bytes) ||
-        check(hipMemcpy(ws->d_yarn, table, floats * sizeof(float), hipMemcpyHostToDevice),
-            "prepare_decode upload");
-    free(table);
-    return failed ? -1 : 0;
+    const size_t bytes = ws->capacity * 128 * sizeof(float);
+    return alloc_device((void **)&ws->d_yarn, bytes, &ws->bytes) ||
+        check(hipMemcpy(ws->d_yarn, ws->h_yarn, bytes, hipMemcpyHostToDevice),
+            "prepare_decode upload") ? -1 : 0;
 }
 
 int lh_workspace_set_decode(lh_workspace *ws, const uint16_t *d_embedding, int64_t id,

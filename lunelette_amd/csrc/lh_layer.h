@@ -22,6 +22,8 @@ struct lh_workspace {
     float *d_PM, *d_PT;            /* [B][32][C/64] block maxima and sums */
     float *d_PA;                   /* [B][32][C/64][128] block P.V partials */
     float *d_yarn;                 /* [C][128]: cos[64], sin[64] per position (decode) */
+    float *h_yarn;                 /* host copy of the same rows, filled on first use */
+    uint8_t *h_yarn_ready;         /* [C]: row p of h_yarn holds lh_yarn(p) */
     /* MFMA path: BF16 hi/mid/lo splits of the GEMM inputs, [3][B][K]. */
     uint16_t *d_split;
     float *d_gemm;                 /* [B][18432] GEMM outputs */
