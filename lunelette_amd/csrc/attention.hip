@@ -584,7 +584,7 @@ __global__ void __launch_bounds__(512, 1)
 k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
     const float* __restrict__ vcache, uint32_t length, uint32_t count, uint32_t capacity,
     float* __restrict__ PM, float* __restrict__ PT, float* __restrict__ PA, float* __restrict__ out,
-    uint16_t* __restrict__ xs, uint32_t xs_tokens)
+    uint16_t* __restrict__ xs, uint32_t xs_tokens, float* __restrict__ xs_scale)
 {
     __shared__ __attribute__((aligned(16))) uint8_t Kp[3 * FB_KPLANE];
     __shared__ __attribute__((aligned(16))) uint8_t Vp[2 * FB_VPLANE];
@@ -811,6 +811,27 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
             }
         }
     }
+    // Output planes (one split): each token's four query heads of this kv
+    // head (512 columns, one K split of the o projection) share one power of
+    // two 2^e, their largest magnitude into [2^14, 2^15), before the split
+    // into two FP16 planes; xs_scale[t][kv head] = 2^-e. The heads' maxima
+    // meet in LDS before any wave leaves.
+    __shared__ float gmax[2 * FA_TQ][4];
+    if (splits == 1 && xs) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            float mr = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                mr = fmaxf(mr, fabsf(o[i][r] / l[r]));
+            }
+            mr = quad16_max(mr);
+            if (l16 == 0) {
+                gmax[FA_TQ * (wave >> 2) + 4 * g + r][wave & 3] = mr;
+            }
+        }
+        __syncthreads();
+    }
     if (t0 >= count) {
         return;
     }
@@ -823,12 +844,24 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
         }
         if (splits == 1) {
             const size_t at = (size_t)t * LH_QUERY + head * LH_HEAD_DIM + l16;
+            if (xs) {
+                const float* gm = gmax[FA_TQ * (wave >> 2) + 4 * g + r];
+                const int e = row_exponent(fmaxf(fmaxf(gm[0], gm[1]), fmaxf(gm[2], gm[3])));
+                if (l16 == 0 && (wave & 3) == 0) {
+                    xs_scale[t * LH_KV_HEADS + kvh] = exp2i(-e);
+                }
+                const float f = exp2i(e);
+                const size_t plane = (size_t)xs_tokens * LH_QUERY;
 #pragma unroll
-            for (int i = 0; i < 8; i++) {
-                if (xs) {
-                    store_split1(xs, (size_t)xs_tokens * LH_QUERY,
-                        xs_at(t, head * LH_HEAD_DIM + l16 + 16 * i, LH_QUERY), o[i][r] / l[r]);
-                } else {
+                for (int i = 0; i < 8; i++) {
+                    float rest;
+                    const size_t xa = xs_at(t, head * LH_HEAD_DIM + l16 + 16 * i, LH_QUERY);
+                    xs[xa] = (uint16_t)f16_hi(o[i][r] / l[r] * f, rest);
+                    xs[plane + xa] = (uint16_t)f16_bits(rest);
+                }
+            } else {
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
                     out[at + 16 * i] = o[i][r] / l[r];
                 }
             }
@@ -856,7 +889,8 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
 __global__ void __launch_bounds__(256)
 k_attn_merge(const float* __restrict__ PM, const float* __restrict__ PT,
     const float* __restrict__ PA, uint32_t capacity, uint32_t parts, uint32_t count,
-    float* __restrict__ out, uint16_t* __restrict__ xs, uint32_t xs_tokens)
+    float* __restrict__ out, uint16_t* __restrict__ xs, uint32_t xs_tokens,
+    float* __restrict__ xs_scale)
 {
     // Workgroup w merges four heads of one token. When count is a multiple of
     // 128 the workgroups of a 16-token group share an XCD (ids are dealt
@@ -892,14 +926,27 @@ k_attn_merge(const float* __restrict__ PM, const float* __restrict__ PT,
     const uint32_t t = th / LH_HEADS, h = th % LH_HEADS;
     const size_t at = (size_t)t * LH_QUERY + h * LH_HEAD_DIM + 2 * lane;
     if (xs) {
-        const size_t plane = (size_t)xs_tokens * LH_QUERY;
-        // The lane's two columns are adjacent in the plane: one 4-byte store
-        // per plane.
-        const size_t at2 = xs_at(t, h * LH_HEAD_DIM + 2 * lane, LH_QUERY);
-        const bf16x3 a = split3(A.x / T), b = split3(A.y / T);
-        *reinterpret_cast<uint32_t*>(xs + at2) = a.hi | (b.hi << 16);
-        *reinterpret_cast<uint32_t*>(xs + plane + at2) = a.mid | (b.mid << 16);
-        *reinterpret_cast<uint32_t*>(xs + 2 * plane + at2) = a.lo | (b.lo << 16);
+        // The workgroup's waves are the four query heads of one kv head for
+        // one token: 512 columns, one K split of the o projection. They share
+        // one power of two 2^e (their largest magnitude into [2^14, 2^15))
+        // before the split into two FP16 planes; xs_scale[t][kv head] = 2^-e,
+        // which the o projection's GEMM applies to that split's products. The
+        // lane's two columns are adjacent in the plane: one 4-byte store per
+        // plane.
+        __shared__ float gmax[4];
+        const float vx = A.x / T, vy = A.y / T;
+        const float mw = wave_max64(fmaxf(fabsf(vx), fabsf(vy)));
+        if (lane == 0) {
+            gmax[threadIdx.x >> 6] = mw;
+        }
+        __syncthreads();
+        const int e = row_exponent(fmaxf(fmaxf(gmax[0], gmax[1]), fmaxf(gmax[2], gmax[3])));
+        if (threadIdx.x == 0) {
+            xs_scale[t * LH_KV_HEADS + h / 4] = exp2i(-e);
+        }
+        const float f = exp2i(e);
+        store_f16x2_2(xs, (size_t)xs_tokens * LH_QUERY,
+            xs_at(t, h * LH_HEAD_DIM + 2 * lane, LH_QUERY), vx * f, vy * f);
     } else {
         *reinterpret_cast<float2*>(out + at) = make_float2(A.x / T, A.y / T);
     }
@@ -910,26 +957,28 @@ k_attn_merge(const float* __restrict__ PM, const float* __restrict__ PT,
 extern "C" int lh_launch_attention_mfma(const float* q, const float* kcache_layer,
     const float* vcache_layer, const lh_step_params* params, uint32_t length, uint32_t count,
     uint32_t capacity, float* PM, float* PT, float* PA, float* out, uint16_t* xs, uint32_t xs_tokens,
-    hipStream_t s)
+    float* xs_scale, hipStream_t s)
 {
     if (!count || capacity % LH_ATTN_BLOCK || length + count > capacity ||
-        (xs && xs_tokens < count)) {
+        (xs && (xs_tokens < count || !xs_scale))) {
         return -1;
     }
-    // KV splits so that about 256 workgroups run (one per CU): each takes at
-    // least 2 blocks of the longest tile (a 256-token chunk with no prefix
-    // runs 2 splits), at most one partial per block.
+    // KV splits so that about 256 workgroups run (one per CU), at most one
+    // per block of the longest tile (a 256-token chunk with no prefix runs 4
+    // splits of one block: measured 2.7 us per layer faster than 2 splits of
+    // two blocks, the merge included).
     const uint32_t tiles = (count + 2 * lh::FA_TQ - 1) / (2 * lh::FA_TQ);
     const uint32_t nb = (length + count + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
     uint32_t splits = 256 / (tiles * LH_KV_HEADS);
-    const uint32_t by_length = nb / 2;
+    const uint32_t by_length = nb;
     splits = splits < by_length ? splits : by_length;
     splits = splits ? splits : 1;
     hipLaunchKernelGGL(lh::k_attn_mfma_bf16, dim3(tiles * LH_KV_HEADS * splits), dim3(512), 0, s,
-        q, kcache_layer, vcache_layer, length, count, capacity, PM, PT, PA, out, xs, xs_tokens);
+        q, kcache_layer, vcache_layer, length, count, capacity, PM, PT, PA, out, xs, xs_tokens,
+        xs_scale);
     if (splits > 1) {
         hipLaunchKernelGGL(lh::k_attn_merge, dim3(count * LH_HEADS / 4), dim3(256), 0, s, PM, PT,
-            PA, capacity, splits, count, out, xs, xs_tokens);
+            PA, capacity, splits, count, out, xs, xs_tokens, xs_scale);
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

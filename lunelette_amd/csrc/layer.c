@@ -354,7 +354,7 @@ int lh_attention_mfma(const float *d_q, const float *d_keys, const float *d_valu
     }
     return launched(lh_launch_attention_mfma(d_q, d_keys, d_values, ws->d_params,
         (uint32_t)ws->length, (uint32_t)ws->count, (uint32_t)ws->capacity, ws->d_PM, ws->d_PT,
-        ws->d_PA, d_out, NULL, 0, (hipStream_t)stream), "attention");
+        ws->d_PA, d_out, NULL, 0, NULL, (hipStream_t)stream), "attention");
 }
 
 int lh_head_forward(const uint16_t *d_embedding, const float *d_gamma, const float *d_xrow,

@@ -203,4 +203,51 @@ __device__ __forceinline__ void store_split1(uint16_t* xs, size_t plane, size_t 
     xs[2 * plane + at] = (uint16_t)a.lo;
 }
 
+// 2^e as a float, e in [-126, 127].
+__device__ __forceinline__ float exp2i(int e)
+{
+    return __uint_as_float((uint32_t)(e + 127) << 23);
+}
+
+// Scale exponent of a row whose largest magnitude is m: m * 2^e lies in
+// [2^14, 2^15), inside FP16's normal range, so neither FP16 plane overflows.
+// 0 for m = 0 or nonfinite m; clamped to [-126, 126] (subnormal m gives 126).
+__device__ __forceinline__ int row_exponent(float m)
+{
+    const uint32_t field = (__float_as_uint(m) >> 23) & 0xffu;
+    if (!(m > 0.0f) || field == 0xffu) {
+        return 0;
+    }
+    if (field == 0) {
+        return 126;
+    }
+    const int e = 141 - (int)field;   // m = f * 2^(field - 126), f in [0.5, 1)
+    return e < -126 ? -126 : (e > 126 ? 126 : e);
+}
+
+// Two-plane FP16 form of an (already scaled) value: h = f16(v), l = f16(v - h);
+// v - h is exact in FP32, so h + l carries about 22 significant bits.
+__device__ __forceinline__ uint32_t f16_hi(float v, float& rest)
+{
+    const _Float16 h = (_Float16)v;
+    rest = v - (float)h;
+    return __builtin_bit_cast(uint16_t, h);
+}
+
+__device__ __forceinline__ uint32_t f16_bits(float v)
+{
+    return __builtin_bit_cast(uint16_t, (_Float16)v);
+}
+
+// Two adjacent scaled values into the two FP16 planes of xs, one 4-byte
+// store per plane; `at` is even.
+__device__ __forceinline__ void store_f16x2_2(uint16_t* xs, size_t plane, size_t at, float a,
+    float b)
+{
+    float ra, rb;
+    const uint32_t ha = f16_hi(a, ra), hb = f16_hi(b, rb);
+    *reinterpret_cast<uint32_t*>(xs + at) = ha | (hb << 16);
+    *reinterpret_cast<uint32_t*>(xs + plane + at) = f16_bits(ra) | (f16_bits(rb) << 16);
+}
+
 }  // namespace lh

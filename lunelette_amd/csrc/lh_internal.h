@@ -32,11 +32,14 @@ int lh_launch_attention(const float *q, const float *kcache_layer, const float *
     const lh_step_params *params, uint32_t length, uint32_t count, uint32_t capacity, float *PM,
     float *PT, float *PA, float *out, hipStream_t s);
 /* Matrix-core attention for multi-token steps (tolerance path). With xs set
- * the output goes to the BF16 hi/mid/lo planes of xs (token stride xs_tokens)
- * instead of FP32 rows of out. */
+ * the output goes to the two scaled FP16 planes of xs (token stride
+ * xs_tokens, the o projection's input) instead of FP32 rows of out, with
+ * xs_scale[t][kv head] = 2^-e for the planes of token t's 512 columns of that
+ * kv head's query heads. */
 int lh_launch_attention_mfma(const float *q, const float *kcache_layer, const float *vcache_layer,
     const lh_step_params *params, uint32_t length, uint32_t count, uint32_t capacity, float *PM,
-    float *PT, float *PA, float *out, uint16_t *xs, uint32_t xs_tokens, hipStream_t s);
+    float *PT, float *PA, float *out, uint16_t *xs, uint32_t xs_tokens, float *xs_scale,
+    hipStream_t s);
 /* Block-grid width of the attention kernel. */
 uint32_t lh_attention_blocks(uint32_t length, uint32_t count);
 int lh_launch_embed(const uint16_t *E, const lh_step_params *params, uint32_t count, float *x,

@@ -5,12 +5,11 @@
 // P[s][m][n] = sum over the split's columns k of X[m][k] * dec(W[n][k]), FP32.
 // - X (FP32 activations) reaches the GEMM as planes of 16-bit values, in one
 //   of two formats. Three BF16 planes: X == hi + mid + lo exactly (k_split,
-//   and the attention output for the o projection). Two FP16 planes of the
-//   row scaled by a power of two: X * 2^e == h + l to about 22 significant
-//   bits, with 2^e bringing the row's largest magnitude into [2^14, 2^15) so
-//   that nothing overflows (the gate|up and down inputs, whose producers see
-//   whole token rows); the consumer multiplies the summed
-//   partials by 2^-e, exactly. W stays FP8 in HBM and is decoded exactly to
+//   the q|k|v input). Two FP16 planes of the row, or of a K range of it,
+//   scaled by a power of two: X * 2^e == h + l to about 22 significant bits,
+//   with 2^e bringing the range's largest magnitude into [2^14, 2^15) so
+//   that nothing overflows (the o, gate|up and down inputs); the GEMM or the
+//   consumer multiplies the products by 2^-e, exactly. W stays FP8 in HBM and is decoded exactly to
 //   BF16 or FP16 (v_cvt_scalef32_pk_{bf16,f16}_fp8, unit scale: every E4M3FN
 //   value has at most 4 significant bits and fits either type). The plane
 //   products accumulate in FP32.
@@ -72,42 +71,6 @@ constexpr uint32_t MAX_N = 2 * LH_INNER;  // widest GEMM: gate|up
 // Activation plane formats of the GEMM: three exact BF16 planes (hi + mid + lo),
 // or two FP16 planes of a row scaled by 2^e (h + l, about 22 significant bits).
 enum { PLANES_BF16 = 3, PLANES_F16 = 2 };
-
-// 2^e as a float, e in [-126, 127].
-__device__ __forceinline__ float exp2i(int e)
-{
-    return __uint_as_float((uint32_t)(e + 127) << 23);
-}
-
-// Scale exponent of a row whose largest magnitude is m: m * 2^e lies in
-// [2^14, 2^15), inside FP16's normal range, so neither plane overflows. 0 for
-// m = 0 or nonfinite m; clamped to [-126, 126] (subnormal m gives 126).
-__device__ __forceinline__ int row_exponent(float m)
-{
-    const uint32_t field = (__float_as_uint(m) >> 23) & 0xffu;
-    if (!(m > 0.0f) || field == 0xffu) {
-        return 0;
-    }
-    if (field == 0) {
-        return 126;
-    }
-    const int e = 141 - (int)field;   // m = f * 2^(field - 126), f in [0.5, 1)
-    return e < -126 ? -126 : (e > 126 ? 126 : e);
-}
-
-// Two-plane FP16 form of an (already scaled) value: h = f16(v), l = f16(v - h);
-// v - h is exact in FP32, so h + l carries about 22 significant bits.
-__device__ __forceinline__ uint32_t f16_hi(float v, float& rest)
-{
-    const _Float16 h = (_Float16)v;
-    rest = v - (float)h;
-    return __builtin_bit_cast(uint16_t, h);
-}
-
-__device__ __forceinline__ uint32_t f16_bits(float v)
-{
-    return __builtin_bit_cast(uint16_t, (_Float16)v);
-}
 
 // Four consecutive scaled values into the two FP16 planes of xs (plane stride
 // `plane` elements), one 8-byte store per plane; `at` is a multiple of 4.
@@ -477,6 +440,11 @@ __device__ __forceinline__ void gemm_stage(const uint8_t* buf, const u32x4 (&w)[
     read_group(0, ac);
 #pragma unroll
     for (int j = 0; j < 2 * P; j++) {
+        // Wait for this group's reads (LDS only: s_waitcnt lgkmcnt(0) with
+        // vmcnt and expcnt at their maxima, so the next stage's global loads
+        // stay in flight) before the next group's are issued. The
+        // compiler's own wait would come after them and wait for both.
+        __builtin_amdgcn_s_waitcnt(0xc07f);
         if (j < 2 * P - 1) {
             read_group(j + 1, an);
         }
@@ -542,11 +510,16 @@ __device__ __forceinline__ void store_tile(const floatx4 (&acc)[4][4], float* __
 // out: P[s][m][n] with split stride stride_tokens * N; token rows >= count
 // are not written (their activation rows, < m_tiles * 64 <= stride_tokens,
 // are read).
+//
+// With gscale, the planes of token m's K split s carry the power of two
+// 1/gscale[m][s] (row stride `splits`; the attention's output for the o
+// projection): the split's products are multiplied by gscale[m][s] (exact)
+// before the store, so the partials leave unscaled.
 template <int P>
 __device__ __forceinline__ void gemm_tile(const uint8_t* __restrict__ W0,
     const uint8_t* __restrict__ W1, uint32_t boundary, uint32_t N, uint32_t K,
     const uint16_t* __restrict__ xs, uint32_t stride_tokens, uint32_t count, uint32_t m_tiles,
-    uint32_t splits, float* __restrict__ out)
+    uint32_t splits, const float* __restrict__ gscale, float* __restrict__ out)
 {
     static_assert(P == PLANES_BF16 || P == PLANES_F16, "plane format");
     constexpr uint32_t A_FRAGS = 4 * P * 2;   // 1 KB activation fragments per stage
@@ -625,6 +598,20 @@ __device__ __forceinline__ void gemm_tile(const uint8_t* __restrict__ W0,
             load_w((st + 2) * BK);
         }
         gemm_stage<P>(As1, wc, lane, acc);
+    }
+    if (gscale) {
+        // Rows past count read a stale factor and are not stored.
+#pragma unroll
+        for (int mf = 0; mf < 4; mf++) {
+#pragma unroll
+            for (int r = 0; r < 4; r++) {
+                const float f = gscale[(size_t)(m0 + 16 * mf + 4 * g + r) * splits + s];
+#pragma unroll
+                for (int nf = 0; nf < 4; nf++) {
+                    acc[mf][nf][r] *= f;
+                }
+            }
+        }
     }
     store_tile(acc, out + (size_t)s * stride_tokens * N, N, m0, nt * GN + wave * 64, count, lane);
 }
@@ -773,15 +760,18 @@ k_gemm_bf16(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint
     uint32_t N, uint32_t K, const uint16_t* __restrict__ xs, uint32_t stride_tokens,
     uint32_t count, uint32_t m_tiles, uint32_t splits, float* __restrict__ out)
 {
-    gemm_tile<PLANES_BF16>(W0, W1, boundary, N, K, xs, stride_tokens, count, m_tiles, splits, out);
+    gemm_tile<PLANES_BF16>(W0, W1, boundary, N, K, xs, stride_tokens, count, m_tiles, splits,
+        nullptr, out);
 }
 
 __global__ void __launch_bounds__(256, 2)
 k_gemm_f16(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint32_t boundary,
     uint32_t N, uint32_t K, const uint16_t* __restrict__ xs, uint32_t stride_tokens,
-    uint32_t count, uint32_t m_tiles, uint32_t splits, float* __restrict__ out)
+    uint32_t count, uint32_t m_tiles, uint32_t splits, const float* __restrict__ gscale,
+    float* __restrict__ out)
 {
-    gemm_tile<PLANES_F16>(W0, W1, boundary, N, K, xs, stride_tokens, count, m_tiles, splits, out);
+    gemm_tile<PLANES_F16>(W0, W1, boundary, N, K, xs, stride_tokens, count, m_tiles, splits,
+        gscale, out);
 }
 
 __global__ void __launch_bounds__(256, 2)
@@ -851,7 +841,8 @@ static size_t partial_floats(uint32_t B)
 
 // Bytes of the activation planes: three BF16 (or two FP16) planes of up to
 // 9216 columns per token. The scales of the FP16 planes follow them: one per
-// token for the gate|up input, DOWN_SPLITS per token for the down input.
+// token for the gate|up input, DOWN_SPLITS per token for the down input (the
+// same slots first hold the o input's eight per token, one per kv head).
 static size_t plane_bytes(size_t B)
 {
     return 3 * B * LH_INNER * sizeof(uint16_t);
@@ -967,7 +958,7 @@ static int residual_norm_split(const float* partial, uint32_t splits, uint32_t s
 // multiple of 64*splits, (N/256 * splits) a multiple of 8.
 static int gemm(int planes, const uint8_t* W0, const uint8_t* W1, uint32_t boundary, uint32_t N,
     uint32_t K, const uint16_t* xs, uint32_t stride, uint32_t count, uint32_t splits, float* out,
-    hipStream_t s)
+    hipStream_t s, const float* gscale = nullptr)
 {
     const uint32_t n_tiles = N / GN;
     const uint32_t m_tiles = (count + GM - 1) / GM;
@@ -982,7 +973,7 @@ static int gemm(int planes, const uint8_t* W0, const uint8_t* W1, uint32_t bound
             W0, W1 ? W1 : W0, boundary, N, K, xs, stride, count, m_tiles, splits, out);
     } else {
         hipLaunchKernelGGL(k_gemm_f16, dim3(n_tiles * m_tiles * splits), dim3(256), 0, s,
-            W0, W1 ? W1 : W0, boundary, N, K, xs, stride, count, m_tiles, splits, out);
+            W0, W1 ? W1 : W0, boundary, N, K, xs, stride, count, m_tiles, splits, gscale, out);
     }
     return launched_ok("gemm");
 }
@@ -1066,13 +1057,13 @@ extern "C" int lh_fp8_gemm(lh_workspace* ws, const uint8_t* d_w, float scale, co
 // One layer over ws->count tokens. input_split: ws->d_split already holds the
 // BF16 planes of input_norm(x) (the previous layer's last kernel wrote them);
 // next_norm: the last kernel also writes them for the following layer (NULL:
-// plain residual combine). The gate|up and down inputs travel as two FP16
-// planes with power-of-two scales (per token for gate|up, per token and
-// 576-column K granule for down). The q|k|v input stays
-// in three exact BF16 planes: its error reaches the attention scores, which
-// the softmax amplifies (at scores of a few hundred, two FP16 planes put the
-// config-3 layer at 1.2e-3 of the row maximum, over the 1e-3 tolerance), and
-// so does the attention output, which no single workgroup sees whole.
+// plain residual combine). The o, gate|up and down inputs travel as two
+// FP16 planes with power-of-two scales (per token and kv head for o, per
+// token for gate|up, per token and 576-column K granule for down). The q|k|v
+// input stays in three exact BF16 planes: its error reaches the attention
+// scores, which the softmax amplifies (at scores of a few hundred, two FP16
+// planes put the config-3 layer at 1.2e-3 of the row maximum, over the 1e-3
+// tolerance).
 extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, float* d_keys,
     float* d_values, lh_workspace* ws, int input_split, const float* next_norm, hipStream_t s)
 {
@@ -1089,11 +1080,11 @@ extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, floa
     uint16_t* xs = ws->d_split;
     float* scale_a = token_scales(ws);
     float* scale_b = group_scales(ws);
-    // K splits (measured at 256 tokens): q|k|v 8, o 8, down 16; gate|up is
+    // K splits (measured at 256 tokens): q|k|v 4, o 8, down 16; gate|up is
     // stream-K.
     // q|k|v: 6144 rows, 3072 columns; scales, RoPE and the KV append in the
     // epilogue.
-    const uint32_t sq = 8;
+    const uint32_t sq = 4;
     if ((!input_split &&
             residual_norm_split(NULL, 0, B, 1.0f, d_x, w->input_norm, xs, NULL, n, s)) ||
         gemm(PLANES_BF16, w->qkv, NULL, LH_QKV_ROWS, LH_QKV_ROWS, LH_HIDDEN, xs, B, n, sq, P, s) ||
@@ -1104,13 +1095,17 @@ extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, floa
         })) {
         return -1;
     }
-    // Attention writes the o projection's input as BF16 planes; o: 3072 rows,
-    // 4096 columns; residual, post-norm and the gate|up input after it.
-    const uint32_t so = 8;
+    // Attention writes the o projection's input as two FP16 planes with a
+    // power-of-two scale per (token, kv head): the kv head's four query heads
+    // are one of o's eight 512-column K splits, whose products the GEMM
+    // scales back. o: 3072 rows, 4096 columns; residual, post-norm and the
+    // gate|up input after it.
+    const uint32_t so = LH_KV_HEADS;
     if (lh_launch_attention_mfma(ws->d_q, d_keys, d_values, ws->d_params, (uint32_t)ws->length,
-            n, C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_attn, xs, B, s) ||
+            n, C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_attn, xs, B, scale_b, s) ||
         launched_ok("attention") ||
-        gemm(PLANES_BF16, w->o, NULL, LH_HIDDEN, LH_HIDDEN, LH_QUERY, xs, B, n, so, P, s) ||
+        gemm(PLANES_F16, w->o, NULL, LH_HIDDEN, LH_HIDDEN, LH_QUERY, xs, B, n, so, P, s,
+            scale_b) ||
         residual_norm_split(P, so, B, w->scale[3], d_x, w->post_norm, xs, scale_a, n, s)) {
         return -1;
     }

@@ -10,9 +10,17 @@ holds the CPU oracle's streams (tests/golden/make_stream_golden.py):
   the fixture's first divergence between the two oracle schedules (None: the
   two schedules select the same 1024 tokens for this seed, so the GPU stream
   equals the reference-literal one throughout);
-- the MPS path (matrix-core prefill, tolerance-equal logits) must select the
-  same 1024 tokens as well: its prefill logits differ from the oracle's by
-  rounding only, and decode runs the bit-exact decode kernels.
+- the MPS path (matrix-core prefill, tolerance-equal logits, then the
+  bit-exact decode kernels over the KV cache it wrote) must select the same
+  tokens up to the first step where the oracle's own top-2 logit gap is within
+  twice the MPS path's logit error there: its KV cache differs from the
+  oracle's by rounding, which can flip a near-tie and no other step. At a
+  divergence the two paths rerun in lockstep, both fed the fixture's ids,
+  which checks every step up to it: the MPS logits within 1e-3 of the logit
+  range of the precise path's, and the flip at a gap below twice that error.
+  (For this seed step 172 is such a near-tie: the oracle's top-2 gap there is
+  4.0e-5 of the logit range, 3.7e-4 absolute; the summation order of the
+  matrix-core prefill decides which side of it the MPS stream lands on.)
 """
 import json
 import os
@@ -71,9 +79,45 @@ def test_precise_stream_matches_oracle_mirror(gpu):
           "reference-literal oracle" % (len(tokens), len(tokens), ref_agree))
 
 
+def lockstep_logits(fx, prefill_mode, steps):
+    """Logits of the prompt's last chunk and of `steps` - 1 decodes fed the
+    fixture's ids, one call at a time."""
+    rt = Runtime(seed=fx["seed"], layers=fx["layers"], context=fx["context"], block=256,
+                 prefill=prefill_mode)
+    try:
+        prompt = syn.tokens(fx["seed"], 1, fx["prompt"])
+        chunk = fx["chunk"]
+        logits = rt.prefill(prompt[:chunk])
+        for begin in range(chunk, fx["prompt"], chunk):
+            logits = rt.append(prompt[begin:begin + chunk])
+        yield logits
+        for i in range(steps - 1):
+            yield rt.decode(fx["tokens_mirror"][i])
+    finally:
+        rt.close()
+
+
 def test_mps_stream_matches_oracle(gpu):
     fx = fixture()
+    want = fx["tokens_mirror"]
     tokens = run_stream(fx, lh.PREFILL_MPS)
-    n = agreement(tokens, fx["tokens_mirror"])
+    n = agreement(tokens, want)
     print("MPS stream: first %d/%d tokens equal the mirror oracle" % (n, len(tokens)))
-    assert n == len(fx["tokens_mirror"]) == len(tokens)
+    assert len(tokens) == len(want)
+    if n == len(want):
+        return
+    worst = 0.0
+    for i, (ref, got) in enumerate(zip(lockstep_logits(fx, lh.PREFILL_CUSTOM, n + 1),
+                                       lockstep_logits(fx, lh.PREFILL_MPS, n + 1))):
+        span = float(ref.max() - ref.min())
+        err = float(np.max(np.abs(got - ref)))
+        worst = max(worst, err / span)
+        assert err <= 1e-3 * span, "step %d: MPS logit error %.3g of range %.3g" % (i, err, span)
+        assert int(np.argmax(ref)) == want[i], "precise path left the fixture at %d" % i
+        if i == n:
+            top2 = np.partition(ref, -2)[-2:]
+            gap = float(top2[1] - top2[0])
+            print("MPS stream: step %d is a near-tie: top-2 gap %.3g (%.3g of the range), "
+                  "MPS logit error %.3g; largest error over steps 0..%d: %.3g of the range"
+                  % (n, gap, gap / span, err, n, worst))
+            assert 2 * err >= gap, "step %d flipped at gap %.4g, error %.4g" % (n, gap, err)
