@@ -6,7 +6,8 @@ tied BF16 131072-token head), context capacity 4352, block 256. A seeded
 512-token prompt is prefilled in two 256-token chunks (prefill + append), then
 greedy decode runs for --steps tokens; a step is one decode call (all layers,
 the head, the 512 KiB of logits reaching host memory and host greedy
-selection). value = decode tokens/s; prefill tokens/s is reported beside it.
+selection). value = decode tokens/s; prefill tokens/s (the median of 5 timed
+512-token prefills from an empty cache) is reported beside it.
 After the timed calls the same workload runs untimed on the bit-exact path
 (precise prefill, then the same decode kernels), and its ids are compared with
 the oracle's token fixture (tokens_match_fixture = how many lead in
@@ -34,6 +35,7 @@ import ctypes
 import hashlib
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -43,6 +45,8 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
+# Timed repetitions of the 512-token prefill (median reported).
+PREFILL_TRIALS = 5
 METRIC = "decode tok/s + 256-chunk prefill tok/s @4352 ctx; FP8 matvec % HBM peak"
 
 # FP8 weight elements per layer and projection.
@@ -537,18 +541,26 @@ def main():
         token = rt.greedy()
     rt.reset()
 
-    lh.check(lh.lib().lh_device_synchronize())
-    t = time.perf_counter()
-    rt.prefill(prompt[:256], copy=False)
-    chunk1_ms = rt.last_device_ms()
-    rt.append(prompt[256:], copy=False)
-    chunk2_ms = rt.last_device_ms()
-    lh.check(lh.lib().lh_device_synchronize())
-    prefill_s = time.perf_counter() - t
+    # The 512-token prefill, timed PREFILL_TRIALS times from an empty cache
+    # (median reported); the decode below continues the last one.
+    walls, chunks1, chunks2 = [], [], []
+    for trial in range(PREFILL_TRIALS):
+        if trial:
+            rt.reset()
+        lh.check(lh.lib().lh_device_synchronize())
+        t = time.perf_counter()
+        rt.prefill(prompt[:256], copy=False)
+        chunks1.append(rt.last_device_ms())
+        rt.append(prompt[256:], copy=False)
+        chunks2.append(rt.last_device_ms())
+        lh.check(lh.lib().lh_device_synchronize())
+        walls.append(time.perf_counter() - t)
+    prefill_s = statistics.median(walls)
+    chunk1_ms, chunk2_ms = statistics.median(chunks1), statistics.median(chunks2)
     token = rt.greedy()
     tokens = [token]
-    log("prefill 512 tokens: %.1f ms (device %.1f + %.1f ms)" % (prefill_s * 1e3, chunk1_ms,
-                                                                 chunk2_ms))
+    log("prefill 512 tokens: %.1f ms (device %.1f + %.1f ms), median of %d" % (
+        prefill_s * 1e3, chunk1_ms, chunk2_ms, PREFILL_TRIALS))
 
     lh.check(lh.lib().lh_device_synchronize())
     device_ms = 0.0
@@ -589,6 +601,7 @@ def main():
         "decode_device_ms_per_step": round(device_ms / args.steps, 4),
         "prefill_tok_s": round(512 / prefill_s, 1),
         "prefill_device_ms_per_chunk": [round(chunk1_ms, 3), round(chunk2_ms, 3)],
+        "prefill_trials": PREFILL_TRIALS,
         "tokens_sha256": hashlib.sha256(np.array(tokens, np.int64).tobytes()).hexdigest()[:16],
         "first_tokens": tokens[:8],
     }

@@ -439,8 +439,8 @@ extern "C" int lh_launch_embed(const uint16_t* E, const lh_step_params* params, 
 // ---------------------------------------------------------------------------
 // Multi-token attention on the matrix cores (the PREFILL_MPS path; the
 // precise path keeps the block/combine kernels above): a flash attention on
-// the BF16 matrix cores (v_mfma_f32_16x16x32_bf16), tolerance-checked, not
-// bit-mirrored.
+// the FP16 and BF16 matrix cores (v_mfma_f32_16x16x32_{f16,bf16}),
+// tolerance-checked, not bit-mirrored.
 //
 // Workgroup (32-token tile, kv head), eight waves: wave w is query head
 // 4*kvh + w % 4 over the tile's 16-token half w / 4, so the four GQA heads and
@@ -454,22 +454,27 @@ extern "C" int lh_launch_embed(const uint16_t* E, const lh_step_params* params, 
 // splits > 1 split z takes a contiguous range of the tile's blocks and writes
 // its unnormalized (max, sum, O) rows as part z of PM/PT/PA (partial stride
 // capacity/64 per (token, head)), merged by k_attn_merge. With xs set, the
-// output goes to xs as the hi/mid/lo BF16 planes the o-projection GEMM reads
-// (plane stride xs_tokens * 4096) instead of FP32 rows of out.
-// Measured at 256 tokens after a 4096-token prefix: 106 us; per block and
-// workgroup about 2.0k cycles of plane split, 3.1k of QK^T (at the matrix
-// cores' rate for two waves per SIMD), 2.0k of PV and 2.5k of barrier skew.
-// Before: V's transposed planes and the P tiles in 128-byte rows with an XOR
-// swizzle (16-way bank conflicts on the staging writes, 5.3k cycles of split)
-// and the softmax's row reductions through LDS swizzles, 129 us; 16-token
+// output goes to xs as the o projection's two FP16 planes (plane stride
+// xs_tokens * 4096, one power of two per (token, kv head) in xs_scale)
+// instead of FP32 rows of out.
+// Measured at 256 tokens after a 4096-token prefix: 94 us (104 us with QK^T
+// over three exact BF16 planes of Q and K, six products: 3.1k of a block's
+// cycles went to QK^T at the matrix cores' rate for two waves per SIMD). Per
+// block and workgroup before that change: about 2.0k cycles of plane split,
+// 3.1k of QK^T, 2.0k of PV and 2.5k of barrier skew. Earlier: V's
+// transposed planes and the P tiles in 128-byte rows with an XOR swizzle
+// (16-way bank conflicts on the staging writes, 5.3k cycles of split) and
+// the softmax's row reductions through LDS swizzles, 129 us; 16-token
 // workgroups of four waves, two per CU, 169 us; the FP32 matrix cores
 // (v_mfma_f32_16x16x4_f32, exact products) with 16-token workgroups 198 us.
+// Also measured: waves as (head, 32-position half) over all 32 tokens with
+// S^T in registers feeding PV directly and the raw tiles through LDS by
+// direct loads: 94 us at the 4096-token prefix but slower on short prefixes
+// (16.8 against 12.5 us on a 256-token chunk with no prefix): its per-block
+// staging and two barriers per block dominated, as here.
 namespace lh {
 
 constexpr uint32_t FA_TQ = 16;                      // tokens per workgroup
-constexpr uint32_t FA_KS = LH_HEAD_DIM + 4;         // K tile row stride (floats)
-constexpr uint32_t FA_VS = LH_HEAD_DIM + 1;         // V tile row stride
-constexpr uint32_t FA_PS = LH_ATTN_BLOCK + 4;       // P tile row stride
 // Scores in the base-2 domain: s = q.k * (1/sqrt(128)) * log2(e), so the
 // softmax weights are exp2(s - m) on the hardware v_exp_f32; the row maxima
 // in PM are in this domain too (k_attn_merge).
@@ -503,6 +508,20 @@ __device__ __forceinline__ float quad16_sum(float v)
     return v + row_ror<1>(v);
 }
 
+// Maximum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four lane groups that
+// hold one MFMA operand row), in all four: v_permlane16_swap /
+// v_permlane32_swap of a register with itself hands every lane its
+// partner's value in one of the two results.
+__device__ __forceinline__ float col4_max(float v)
+{
+    const uint32_t u = __float_as_uint(v);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const float w = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+    const uint32_t x = __float_as_uint(w);
+    const auto b = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
 // Workgroup coordinates of the matrix-core attention: a 1-D grid of
 // tiles * 8 * splits workgroups whose ids are dealt round-robin to the 8
 // XCDs, arranged so that XCD x runs every (token tile, KV split) of kv head
@@ -519,25 +538,27 @@ __device__ __forceinline__ FaCoords fa_coords(uint32_t tiles)
 }
 
 
-// The same flash attention on the BF16 matrix cores. Every FP32 operand is
-// split into BF16 planes by truncation (hi = top 8 significant bits, the
-// remainders exact in FP32):
-//   QK^T: Q and K in three planes (hi + mid + lo == x exactly); the six
-//     cross products whose weight is above 2^-24 of the leading one
-//     (ql kh, qh kl, qm km, qm kh, qh km, qh kh, smallest first), so the
-//     scores carry about FP32 accuracy, which the softmax needs;
-//   PV: P and V in two planes (hi + mid, 16 significant bits); products
-//     pm vh, ph vm, ph vh, so the output's relative error stays near 2^-16.
-// Every BF16 product is exact in FP32; accumulation is the hardware's FP32.
-// v_mfma_f32_16x16x32_bf16 runs 16 times the FLOPs of v_mfma_f32_16x16x4_f32
-// per cycle, so nine products take about a third of the FP32 path's matrix
-// time. Workgroup and grid as described above.
-// LDS (84 KiB): the block's K planes [3][64 pos][128 dims], each 16-byte
-// chunk of a row XOR-swizzled by the row index, and V planes transposed
-// [2][128 dims][64 pos] in 144-byte rows, so the MFMA operand reads and the
-// staging writes are conflict-free; after the scores each wave's P planes
-// [2][16 tokens][64 pos] (144-byte rows) reuse the K planes' space.
+// The operands as 16-bit planes:
+//   QK^T: Q and K as two FP16 planes of the row scaled by a power of two
+//     (its largest magnitude into [2^14, 2^15)): per (token, head) row for
+//     Q, per position for K, h = f16(x 2^e), l = f16(x 2^e - h), about 22
+//     significant bits each. Products ql kh, qh kl, qh kh (smallest first;
+//     ql kl lies near 2^-22 of the leading one), then times 2^-eq 2^-ek
+//     (exact), so the scores keep near-FP32 accuracy, which the softmax
+//     needs;
+//   PV: P and V in two truncated BF16 planes (hi + mid, 16 significant
+//     bits); products pm vh, ph vm, ph vh, so the output's relative error
+//     stays near 2^-16.
+// Every 16-bit product is exact in FP32; accumulation is the hardware's FP32.
+// Workgroup and grid as described above.
+// LDS (85 KiB): the block's K planes [2][64 pos][128 dims] (in a three-plane
+// region), each 16-byte chunk of a row XOR-swizzled by the row index, the 64
+// per-position factors 2^-ek, and V planes transposed [2][128 dims][64 pos]
+// in 144-byte rows, so the MFMA operand reads and the staging writes are
+// conflict-free; after the scores each wave's P planes [2][16 tokens][64 pos]
+// (144-byte rows) reuse the K region.
 typedef __bf16 fa_bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 fa_f16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t fa_u32x4 __attribute__((ext_vector_type(4)));
 
 // Transposed V and P rows hold 64 positions (128 bytes) padded to 144 bytes:
@@ -572,6 +593,17 @@ __device__ __forceinline__ uint32_t fb_hi(float x)
     return __float_as_uint(x) >> 16;
 }
 
+// Two FP16 planes of four values scaled by f (h = f16(v f), l = f16(v f - h)),
+// packed as two 32-bit pairs each.
+__device__ __forceinline__ void f16_planes4(float4 v, float f, uint2& h, uint2& l)
+{
+    float r0, r1, r2, r3;
+    const uint32_t a = f16_hi(v.x * f, r0), b = f16_hi(v.y * f, r1);
+    const uint32_t c = f16_hi(v.z * f, r2), d = f16_hi(v.w * f, r3);
+    h = make_uint2(a | (b << 16), c | (d << 16));
+    l = make_uint2(f16_bits(r0) | (f16_bits(r1) << 16), f16_bits(r2) | (f16_bits(r3) << 16));
+}
+
 // Two truncated BF16 planes of x: hi and mid (x - hi, truncated).
 __device__ __forceinline__ void fb_split2(float x, uint32_t& h, uint32_t& m)
 {
@@ -581,13 +613,15 @@ __device__ __forceinline__ void fb_split2(float x, uint32_t& h, uint32_t& m)
 }
 
 __global__ void __launch_bounds__(512, 1)
-k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
+k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
     const float* __restrict__ vcache, uint32_t length, uint32_t count, uint32_t capacity,
     float* __restrict__ PM, float* __restrict__ PT, float* __restrict__ PA, float* __restrict__ out,
     uint16_t* __restrict__ xs, uint32_t xs_tokens, float* __restrict__ xs_scale)
 {
+    // K uses two of Kp's three planes; the P tiles need all three.
     __shared__ __attribute__((aligned(16))) uint8_t Kp[3 * FB_KPLANE];
     __shared__ __attribute__((aligned(16))) uint8_t Vp[2 * FB_VPLANE];
+    __shared__ float sk[LH_ATTN_BLOCK];
     static_assert(8 * 2 * FB_PPLANE <= 3 * FB_KPLANE, "P planes fit the K planes");
     const FaCoords fc = fa_coords((count + 2 * FA_TQ - 1) / (2 * FA_TQ));
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -599,27 +633,41 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
     const uint32_t t0c = t0 < count ? t0 : t0 - FA_TQ;
     const uint32_t last = (t0c + FA_TQ < count ? t0c + FA_TQ : count) - 1;   // last real token
     // Q operand of k-chunk kc: lane (token l16, group g) holds dims
-    // 32 kc + 8g .. +7, as three planes.
+    // 32 kc + 8g .. +7, as two FP16 planes of the row scaled by 2^eq (its
+    // largest magnitude into [2^14, 2^15)). fq[r] = 2^-eq * log2(e) /
+    // sqrt(128) for the S rows 4g + r this lane holds.
     const uint32_t tq = t0 + l16 <= last ? t0 + l16 : last;
-    fa_bf16x8 qp[3][4];
+    fa_f16x8 qh[4], ql[4];
+    float fq[4];
     {
         const float4* src = reinterpret_cast<const float4*>(
             q + (size_t)tq * LH_QUERY + head * LH_HEAD_DIM + 8 * g);
+        float4 a[4], b[4];
+        float mx = 0.0f;
 #pragma unroll
         for (int kc = 0; kc < 4; kc++) {
-            const float4 a = src[8 * kc], b = src[8 * kc + 1];
-            const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
-            fa_u32x4 h, m, l;
+            a[kc] = src[8 * kc];
+            b[kc] = src[8 * kc + 1];
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a[kc].x), fabsf(a[kc].y)),
+                                 fmaxf(fabsf(a[kc].z), fabsf(a[kc].w))));
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(b[kc].x), fabsf(b[kc].y)),
+                                 fmaxf(fabsf(b[kc].z), fabsf(b[kc].w))));
+        }
+        const int eq = row_exponent(col4_max(mx));
+        const float f = exp2i(eq);
+        const float fs = exp2i(-eq) * FA_SCALE_LOG2;
 #pragma unroll
-            for (int e = 0; e < 4; e++) {
-                const bf16x3 x0 = split3(v[2 * e]), x1 = split3(v[2 * e + 1]);
-                h[e] = x0.hi | (x1.hi << 16);
-                m[e] = x0.mid | (x1.mid << 16);
-                l[e] = x0.lo | (x1.lo << 16);
-            }
-            qp[0][kc] = __builtin_bit_cast(fa_bf16x8, h);
-            qp[1][kc] = __builtin_bit_cast(fa_bf16x8, m);
-            qp[2][kc] = __builtin_bit_cast(fa_bf16x8, l);
+        for (int r = 0; r < 4; r++) {
+            fq[r] = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (4 * g + r),
+                __float_as_int(fs)));
+        }
+#pragma unroll
+        for (int kc = 0; kc < 4; kc++) {
+            uint2 h0, l0, h1, l1;
+            f16_planes4(a[kc], f, h0, l0);
+            f16_planes4(b[kc], f, h1, l1);
+            qh[kc] = __builtin_bit_cast(fa_f16x8, fa_u32x4{h0.x, h0.y, h1.x, h1.y});
+            ql[kc] = __builtin_bit_cast(fa_f16x8, fa_u32x4{l0.x, l0.y, l1.x, l1.y});
         }
     }
     uint32_t limit[4];
@@ -664,6 +712,12 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
         d = 16 * j + (lane & 15);
         r0 = 2 * (4 * wave + (lane >> 4));
     };
+    // K: wave w takes positions 8w .. 8w+7 of the block; lane l holds
+    // position kp = 8w + (l % 32) / 4, quarter kq = l % 4, dims
+    // 32 kq + 4 (2i + l / 32) .. +3 for i = 0..3 (tile word order
+    // lh_ktile_word: each load reads two contiguous 512-byte runs), so the
+    // eight lanes of a position hold all its 128 dims.
+    const uint32_t kp = 8 * wave + ((lane & 31) >> 2), kq = lane & 3, khalf = lane >> 5;
     fa_floatx4 kr[4];
     float vr[16];
     auto load_block = [&](uint32_t b) {
@@ -673,7 +727,7 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
             vcache + head_base + (size_t)b * LH_ATTN_BLOCK * LH_HEAD_DIM);
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            kr[i] = kb[tid + 512 * i];
+            kr[i] = kb[lh_ktile_word(kp, kq, 2 * i + khalf)];
         }
         const float* vf = reinterpret_cast<const float*>(vb);
 #pragma unroll
@@ -694,23 +748,37 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
     const fa_floatx4 zero = fa_floatx4{0.f, 0.f, 0.f, 0.f};
     for (uint32_t b = b_begin; b < b_end; b++) {
         __syncthreads();   // the previous block's planes and P tiles are consumed
+        {
+            // K: the position's largest magnitude over its eight lanes (a
+            // DPP quad, then the other 32-lane half), its power of two 2^ek
+            // (into [2^14, 2^15)), and the two FP16 planes; sk[p] = 2^-ek.
+            const bool kvis = b * LH_ATTN_BLOCK + kp <= visible;
+            float mx = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            // K word tid + 512 i = (tid % 256) + 256 i2, i2 = 2 i + tid / 256:
-            // position 16 (i2 / 2) + lane / 4, dims 32 (lane % 4) +
-            // 4 (w4 + 4 (i2 % 2)) .. +3, w4 = (tid / 64) % 4.
-            const uint32_t i2 = 2 * i + (tid >> 8), w4 = wave & 3;
-            const uint32_t krow = 16 * (i2 >> 1) + (lane >> 2);
-            const uint32_t kd = 32 * (lane & 3) + 4 * (w4 + 4 * (i2 & 1));
-            const fa_floatx4 kk = b * LH_ATTN_BLOCK + krow <= visible ? kr[i] : zero;
-            const bf16x3 a0 = split3(kk.x), a1 = split3(kk.y), a2 = split3(kk.z), a3 = split3(kk.w);
-            const uint32_t at = fb_k_at(krow, kd);
-            *reinterpret_cast<uint2*>(Kp + at) =
-                make_uint2(a0.hi | (a1.hi << 16), a2.hi | (a3.hi << 16));
-            *reinterpret_cast<uint2*>(Kp + FB_KPLANE + at) =
-                make_uint2(a0.mid | (a1.mid << 16), a2.mid | (a3.mid << 16));
-            *reinterpret_cast<uint2*>(Kp + 2 * FB_KPLANE + at) =
-                make_uint2(a0.lo | (a1.lo << 16), a2.lo | (a3.lo << 16));
+            for (int i = 0; i < 4; i++) {
+                kr[i] = kvis ? kr[i] : zero;
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(kr[i].x), fabsf(kr[i].y)),
+                                     fmaxf(fabsf(kr[i].z), fabsf(kr[i].w))));
+            }
+            mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mx), 0xB1, 0xf,
+                0xf, false)));   // quad_perm [1,0,3,2]
+            mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mx), 0x4E, 0xf,
+                0xf, false)));   // quad_perm [2,3,0,1]
+            const uint32_t mu = __float_as_uint(mx);
+            const auto p32 = __builtin_amdgcn_permlane32_swap(mu, mu, false, false);
+            const int ek = row_exponent(fmaxf(__uint_as_float(p32[0]), __uint_as_float(p32[1])));
+            if ((lane & 35) == 0) {
+                sk[kp] = exp2i(-ek);
+            }
+            const float f = exp2i(ek);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                uint2 h, lo;
+                f16_planes4(make_float4(kr[i].x, kr[i].y, kr[i].z, kr[i].w), f, h, lo);
+                const uint32_t at = fb_k_at(kp, 32 * kq + 4 * (2 * i + khalf));
+                *reinterpret_cast<uint2*>(Kp + at) = h;
+                *reinterpret_cast<uint2*>(Kp + FB_KPLANE + at) = lo;
+            }
         }
 #pragma unroll
         for (int j = 0; j < 8; j++) {
@@ -731,24 +799,22 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
         }
         // S tiles j = 0..3: positions 16j + l16; k-chunk kc: dims 32kc + 8g .. +7.
         fa_floatx4 s[4];
+        float fk[4];   // 2^-ek of this lane's S columns
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             s[j] = zero;
+            fk[j] = sk[16 * j + l16];
         }
 #pragma unroll
         for (int kc = 0; kc < 4; kc++) {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const uint32_t at = fb_k_at(16 * j + l16, 32 * kc + 8 * g);
-                const fa_bf16x8 kh = *reinterpret_cast<const fa_bf16x8*>(Kp + at);
-                const fa_bf16x8 km = *reinterpret_cast<const fa_bf16x8*>(Kp + FB_KPLANE + at);
-                const fa_bf16x8 kl = *reinterpret_cast<const fa_bf16x8*>(Kp + 2 * FB_KPLANE + at);
-                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[2][kc], kh, s[j], 0, 0, 0);
-                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[0][kc], kl, s[j], 0, 0, 0);
-                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[1][kc], km, s[j], 0, 0, 0);
-                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[1][kc], kh, s[j], 0, 0, 0);
-                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[0][kc], km, s[j], 0, 0, 0);
-                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qp[0][kc], kh, s[j], 0, 0, 0);
+                const fa_f16x8 kh = *reinterpret_cast<const fa_f16x8*>(Kp + at);
+                const fa_f16x8 kl = *reinterpret_cast<const fa_f16x8*>(Kp + FB_KPLANE + at);
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[kc], kh, s[j], 0, 0, 0);
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[kc], kl, s[j], 0, 0, 0);
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[kc], kh, s[j], 0, 0, 0);
             }
         }
         __syncthreads();   // every wave has read the K planes; P tiles reuse them
@@ -759,7 +825,7 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const uint32_t p = b * LH_ATTN_BLOCK + 16 * j + l16;
-                const float v = p <= limit[r] ? s[j][r] * FA_SCALE_LOG2 : -__builtin_inff();
+                const float v = p <= limit[r] ? s[j][r] * fk[j] * fq[r] : -__builtin_inff();
                 s[j][r] = v;
                 mx = fmaxf(mx, v);
             }
@@ -880,7 +946,7 @@ k_attn_mfma_bf16(const float* __restrict__ q, const float* __restrict__ kcache,
     }
 }
 
-// Merge of k_attn_mfma_bf16's KV splits (tolerance path): per (token, head)
+// Merge of k_attn_mfma's KV splits (tolerance path): per (token, head)
 // M = max m_z, f_z = exp2(m_z - M) (base-2 maxima), out = (sum f_z O_z) / (sum f_z l_z) with
 // the sums in split order. A split whose positions are all masked for the row
 // holds m = -inf, l = 0, O = 0 and contributes nothing; split 0 always holds
@@ -973,7 +1039,7 @@ extern "C" int lh_launch_attention_mfma(const float* q, const float* kcache_laye
     const uint32_t by_length = nb;
     splits = splits < by_length ? splits : by_length;
     splits = splits ? splits : 1;
-    hipLaunchKernelGGL(lh::k_attn_mfma_bf16, dim3(tiles * LH_KV_HEADS * splits), dim3(512), 0, s,
+    hipLaunchKernelGGL(lh::k_attn_mfma, dim3(tiles * LH_KV_HEADS * splits), dim3(512), 0, s,
         q, kcache_layer, vcache_layer, length, count, capacity, PM, PT, PA, out, xs, xs_tokens,
         xs_scale);
     if (splits > 1) {

@@ -239,6 +239,18 @@ __device__ __forceinline__ uint32_t f16_bits(float v)
     return __builtin_bit_cast(uint16_t, (_Float16)v);
 }
 
+// Four consecutive scaled values into the two FP16 planes of xs (plane stride
+// `plane` elements), one 8-byte store per plane; `at` is a multiple of 4.
+__device__ __forceinline__ void store_f16x2_4(uint16_t* xs, size_t plane, size_t at, float4 v)
+{
+    float ra, rb, rc, rd;
+    const uint32_t a = f16_hi(v.x, ra), b = f16_hi(v.y, rb), c = f16_hi(v.z, rc),
+                   d = f16_hi(v.w, rd);
+    *reinterpret_cast<uint2*>(xs + at) = make_uint2(a | (b << 16), c | (d << 16));
+    *reinterpret_cast<uint2*>(xs + plane + at) = make_uint2(
+        f16_bits(ra) | (f16_bits(rb) << 16), f16_bits(rc) | (f16_bits(rd) << 16));
+}
+
 // Two adjacent scaled values into the two FP16 planes of xs, one 4-byte
 // store per plane; `at` is even.
 __device__ __forceinline__ void store_f16x2_2(uint16_t* xs, size_t plane, size_t at, float a,
