@@ -396,19 +396,19 @@ __device__ __forceinline__ void fp8x16_to_f16x8x2(u32x4 u, f16x8& lo, f16x8& hi)
     hi = __builtin_bit_cast(f16x8, b);
 }
 
-// One 64-column stage of a wave's 64 tokens x 64 weight rows: A fragments
+// One 64-column stage of a wave's 64 tokens x 16 NF weight rows: A fragments
 // (mf, p, h) from the stage's LDS buffer, read one (p, h) group of four ahead
-// of its MFMAs; each fragment feeds the four weight fragments of w (this
+// of its MFMAs; each fragment feeds the NF weight fragments of w (this
 // lane's 16 FP8 codes of rows 16 nf + lane % 16, columns 16 (lane / 16) ..
 // +15 of the stage).
-template <int P>
-__device__ __forceinline__ void gemm_stage(const uint8_t* buf, const u32x4 (&w)[4], uint32_t lane,
-    floatx4 (&acc)[4][4])
+template <int P, int NF>
+__device__ __forceinline__ void gemm_stage(const uint8_t* buf, const u32x4 (&w)[NF], uint32_t lane,
+    floatx4 (&acc)[4][NF])
 {
     using V = typename std::conditional<P == PLANES_BF16, bf16x8, f16x8>::type;
-    V b[4][2];
+    V b[NF][2];
 #pragma unroll
-    for (int nf = 0; nf < 4; nf++) {
+    for (int nf = 0; nf < NF; nf++) {
         if constexpr (P == PLANES_BF16) {
             fp8x16_to_bf16x8x2(w[nf], b[nf][0], b[nf][1]);
         } else {
@@ -440,7 +440,7 @@ __device__ __forceinline__ void gemm_stage(const uint8_t* buf, const u32x4 (&w)[
 #pragma unroll
         for (int mf = 0; mf < 4; mf++) {
 #pragma unroll
-            for (int nf = 0; nf < 4; nf++) {
+            for (int nf = 0; nf < NF; nf++) {
                 if constexpr (P == PLANES_BF16) {
                     acc[mf][nf] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac[mf],
                         b[nf][j / P], acc[mf][nf], 0, 0, 0);
@@ -458,12 +458,13 @@ __device__ __forceinline__ void gemm_stage(const uint8_t* buf, const u32x4 (&w)[
     }
 }
 
-__device__ __forceinline__ void zero_tile(floatx4 (&acc)[4][4])
+template <int NF>
+__device__ __forceinline__ void zero_tile(floatx4 (&acc)[4][NF])
 {
 #pragma unroll
     for (int mf = 0; mf < 4; mf++) {
 #pragma unroll
-        for (int nf = 0; nf < 4; nf++) {
+        for (int nf = 0; nf < NF; nf++) {
             acc[mf][nf] = floatx4{0.f, 0.f, 0.f, 0.f};
         }
     }
@@ -472,7 +473,8 @@ __device__ __forceinline__ void zero_tile(floatx4 (&acc)[4][4])
 // The wave's 64 x 64 tile into o[m][n0 + ..] for token rows m0.. < count.
 // D layout of v_mfma_f32_16x16x32_{bf16,f16}: lane l holds rows 4*(l/16) + r,
 // column l%16 of each 16x16 tile.
-__device__ __forceinline__ void store_tile(const floatx4 (&acc)[4][4], float* __restrict__ o,
+template <int NF>
+__device__ __forceinline__ void store_tile(const floatx4 (&acc)[4][NF], float* __restrict__ o,
     uint32_t N, uint32_t m0, uint32_t n0, uint32_t count, uint32_t lane)
 {
     const uint32_t g = lane >> 4, l16 = lane & 15;
@@ -483,7 +485,7 @@ __device__ __forceinline__ void store_tile(const floatx4 (&acc)[4][4], float* __
             const uint32_t m = m0 + 16 * mf + 4 * g + r;
             if (m < count) {
 #pragma unroll
-                for (int nf = 0; nf < 4; nf++) {
+                for (int nf = 0; nf < NF; nf++) {
                     o[(size_t)m * N + n0 + 16 * nf + l16] = acc[mf][nf][r];
                 }
             }
@@ -492,9 +494,11 @@ __device__ __forceinline__ void store_tile(const floatx4 (&acc)[4][4], float* __
 }
 
 // P activation planes (PLANES_BF16 or PLANES_F16) of the same layout
-// xs[p][m][k]. grid: n_tiles * m_tiles * splits workgroups of 256 threads, two
-// resident per CU; (n_tiles * splits) a multiple of 8. W0 holds rows [0, boundary), W1
-// rows [boundary, N) (gate|up as two tensors); boundary a multiple of 256.
+// xs[p][m][k]. Each wave owns 16 NF weight rows, the workgroup 64 NF (256 or
+// 192). grid: n_tiles * m_tiles * splits workgroups of 256 threads, two
+// resident per CU; (n_tiles * splits) a multiple of 8. W0 holds rows
+// [0, boundary), W1 rows [boundary, N) (gate|up as two tensors); boundary a
+// multiple of 64 NF.
 // out: P[s][m][n] with split stride stride_tokens * N; token rows >= count
 // are not written (their activation rows, < m_tiles * 64 <= stride_tokens,
 // are read).
@@ -503,12 +507,13 @@ __device__ __forceinline__ void store_tile(const floatx4 (&acc)[4][4], float* __
 // 1/gscale[m][s] (row stride `splits`; the attention's output for the o
 // projection): the split's products are multiplied by gscale[m][s] (exact)
 // before the store, so the partials leave unscaled.
-template <int P>
+template <int P, int NF>
 __device__ __forceinline__ void gemm_tile(const uint8_t* __restrict__ W0,
     const uint8_t* __restrict__ W1, uint32_t boundary, uint32_t N, uint32_t K,
     const uint16_t* __restrict__ xs, uint32_t stride_tokens, uint32_t count, uint32_t m_tiles,
     uint32_t splits, const float* __restrict__ gscale, float* __restrict__ out)
 {
+    constexpr uint32_t WN = 16 * NF, TN = 4 * WN;   // weight rows per wave, per workgroup
     static_assert(P == PLANES_BF16 || P == PLANES_F16, "plane format");
     constexpr uint32_t A_FRAGS = 4 * P * 2;   // 1 KB activation fragments per stage
     constexpr uint32_t PW = A_FRAGS / 4;      // fragments each wave loads
@@ -523,7 +528,7 @@ __device__ __forceinline__ void gemm_tile(const uint8_t* __restrict__ W0,
     const uint32_t kps = K / splits, k0 = s * kps, steps = kps / BK;
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t g = lane >> 4, l16 = lane & 15;
-    const uint32_t m0 = mt * GM, n0 = nt * GN + wave * 64;
+    const uint32_t m0 = mt * GM, n0 = nt * TN + wave * WN;
     const uint8_t* Wt = n0 < boundary ? W0 + (size_t)n0 * K : W1 + (size_t)(n0 - boundary) * K;
     const uint8_t* wrow = Wt + (size_t)l16 * K + k0 + 16 * g;
     const size_t plane = (size_t)stride_tokens * K;
@@ -544,48 +549,48 @@ __device__ __forceinline__ void gemm_tile(const uint8_t* __restrict__ W0,
                 16, 0, 0);
         }
     };
-    u32x4 wr[4];
+    u32x4 wr[NF];
     auto load_w = [&](uint32_t dk) {
 #pragma unroll
-        for (int nf = 0; nf < 4; nf++) {
+        for (int nf = 0; nf < NF; nf++) {
             wr[nf] = *reinterpret_cast<const u32x4*>(wrow + (size_t)16 * nf * K + dk);
         }
     };
-    floatx4 acc[4][4];
-    zero_tile(acc);
+    floatx4 acc[4][NF];
+    zero_tile<NF>(acc);
     // Double-buffered stages: the next stage's activation (direct to LDS) and
     // weight loads are issued after the barrier that ends every read of the
     // LDS buffer they overwrite, and complete (s_waitcnt 0 + barrier) before
     // its MFMAs.
-    u32x4 wc[4];
+    u32x4 wc[NF];
     load_a(0, As0);
     load_w(0);
     for (uint32_t st = 0; st < steps; st += 2) {
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
 #pragma unroll
-        for (int nf = 0; nf < 4; nf++) {
+        for (int nf = 0; nf < NF; nf++) {
             wc[nf] = wr[nf];
         }
         if (st + 1 < steps) {
             load_a((st + 1) * BK, As1);
             load_w((st + 1) * BK);
         }
-        gemm_stage<P>(As0, wc, lane, acc);
+        gemm_stage<P, NF>(As0, wc, lane, acc);
         if (st + 1 >= steps) {
             break;
         }
         __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
 #pragma unroll
-        for (int nf = 0; nf < 4; nf++) {
+        for (int nf = 0; nf < NF; nf++) {
             wc[nf] = wr[nf];
         }
         if (st + 2 < steps) {
             load_a((st + 2) * BK, As0);
             load_w((st + 2) * BK);
         }
-        gemm_stage<P>(As1, wc, lane, acc);
+        gemm_stage<P, NF>(As1, wc, lane, acc);
     }
     if (gscale) {
         // Rows past count read a stale factor and are not stored.
@@ -595,13 +600,13 @@ __device__ __forceinline__ void gemm_tile(const uint8_t* __restrict__ W0,
             for (int r = 0; r < 4; r++) {
                 const float f = gscale[(size_t)(m0 + 16 * mf + 4 * g + r) * splits + s];
 #pragma unroll
-                for (int nf = 0; nf < 4; nf++) {
+                for (int nf = 0; nf < NF; nf++) {
                     acc[mf][nf][r] *= f;
                 }
             }
         }
     }
-    store_tile(acc, out + (size_t)s * stride_tokens * N, N, m0, nt * GN + wave * 64, count, lane);
+    store_tile<NF>(acc, out + (size_t)s * stride_tokens * N, N, m0, n0, count, lane);
 }
 
 // gemm_tile over a stream-K partition: grid 8 * gpx * m_tiles workgroups of
@@ -678,7 +683,7 @@ __device__ __forceinline__ void gemm_stream_tile(const uint8_t* __restrict__ W0,
         }
     };
     floatx4 acc[4][4];
-    zero_tile(acc);
+    zero_tile<4>(acc);
     // A column's partial leaves after its last stage or the range's last unit.
     auto finish = [&](uint32_t u) {
         const uint32_t nt = u / stages, st = u - nt * stages;
@@ -701,9 +706,9 @@ __device__ __forceinline__ void gemm_stream_tile(const uint8_t* __restrict__ W0,
         }
         if (last) {
             const uint32_t slot = G - stream_group(nt * stages, units, groups);
-            store_tile(acc, out + (size_t)slot * stride_tokens * N, N, m0, nt * GN + wave * 64,
+            store_tile<4>(acc, out + (size_t)slot * stride_tokens * N, N, m0, nt * GN + wave * 64,
                 count, lane);
-            zero_tile(acc);
+            zero_tile<4>(acc);
         }
     };
     // The same double-buffered stages as gemm_tile, over units.
@@ -721,7 +726,7 @@ __device__ __forceinline__ void gemm_stream_tile(const uint8_t* __restrict__ W0,
             load_a(u + 1, As1);
             load_w(u + 1);
         }
-        gemm_stage<P>(As0, wc, lane, acc);
+        gemm_stage<P, 4>(As0, wc, lane, acc);
         finish(u);
         if (u + 1 >= u1) {
             break;
@@ -736,7 +741,7 @@ __device__ __forceinline__ void gemm_stream_tile(const uint8_t* __restrict__ W0,
             load_a(u + 2, As0);
             load_w(u + 2);
         }
-        gemm_stage<P>(As1, wc, lane, acc);
+        gemm_stage<P, 4>(As1, wc, lane, acc);
         finish(u + 1);
     }
 }
@@ -748,7 +753,19 @@ k_gemm_bf16(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint
     uint32_t N, uint32_t K, const uint16_t* __restrict__ xs, uint32_t stride_tokens,
     uint32_t count, uint32_t m_tiles, uint32_t splits, float* __restrict__ out)
 {
-    gemm_tile<PLANES_BF16>(W0, W1, boundary, N, K, xs, stride_tokens, count, m_tiles, splits,
+    gemm_tile<PLANES_BF16, 4>(W0, W1, boundary, N, K, xs, stride_tokens, count, m_tiles, splits,
+        nullptr, out);
+}
+
+// 192-row workgroup tiles (48 rows per wave): q|k|v at 4 K splits and o at
+// 8 make 512 workgroups, every two-per-CU slot, where 256-row tiles leave a
+// quarter of them empty.
+__global__ void __launch_bounds__(256, 2)
+k_gemm_bf16_n3(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint32_t boundary,
+    uint32_t N, uint32_t K, const uint16_t* __restrict__ xs, uint32_t stride_tokens,
+    uint32_t count, uint32_t m_tiles, uint32_t splits, float* __restrict__ out)
+{
+    gemm_tile<PLANES_BF16, 3>(W0, W1, boundary, N, K, xs, stride_tokens, count, m_tiles, splits,
         nullptr, out);
 }
 
@@ -758,7 +775,17 @@ k_gemm_f16(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint3
     uint32_t count, uint32_t m_tiles, uint32_t splits, const float* __restrict__ gscale,
     float* __restrict__ out)
 {
-    gemm_tile<PLANES_F16>(W0, W1, boundary, N, K, xs, stride_tokens, count, m_tiles, splits,
+    gemm_tile<PLANES_F16, 4>(W0, W1, boundary, N, K, xs, stride_tokens, count, m_tiles, splits,
+        gscale, out);
+}
+
+__global__ void __launch_bounds__(256, 2)
+k_gemm_f16_n3(const uint8_t* __restrict__ W0, const uint8_t* __restrict__ W1, uint32_t boundary,
+    uint32_t N, uint32_t K, const uint16_t* __restrict__ xs, uint32_t stride_tokens,
+    uint32_t count, uint32_t m_tiles, uint32_t splits, const float* __restrict__ gscale,
+    float* __restrict__ out)
+{
+    gemm_tile<PLANES_F16, 3>(W0, W1, boundary, N, K, xs, stride_tokens, count, m_tiles, splits,
         gscale, out);
 }
 
@@ -946,21 +973,23 @@ static int residual_norm_split(const float* partial, uint32_t splits, uint32_t s
 // multiple of 64*splits, (N/256 * splits) a multiple of 8.
 static int gemm(int planes, const uint8_t* W0, const uint8_t* W1, uint32_t boundary, uint32_t N,
     uint32_t K, const uint16_t* xs, uint32_t stride, uint32_t count, uint32_t splits, float* out,
-    hipStream_t s, const float* gscale = nullptr)
+    hipStream_t s, const float* gscale = nullptr, uint32_t nf = 4)
 {
-    const uint32_t n_tiles = N / GN;
+    const uint32_t tn = 64 * nf;   // weight rows per workgroup
+    const uint32_t n_tiles = N / tn;
     const uint32_t m_tiles = (count + GM - 1) / GM;
-    if (!count || !splits || N % GN || (n_tiles * splits) % 8 || K % (BK * splits) ||
-        boundary % GN || m_tiles * GM > stride ||
+    if (!count || !splits || (nf != 3 && nf != 4) || N % tn || (n_tiles * splits) % 8 ||
+        K % (BK * splits) || boundary % tn || m_tiles * GM > stride ||
         (size_t)splits * stride * N > partial_floats(stride)) {
         lh_set_error("gemm: unsupported shape N=%u K=%u splits=%u", N, K, splits);
         return -1;
     }
+    const dim3 grid(n_tiles * m_tiles * splits);
     if (planes == PLANES_BF16) {
-        hipLaunchKernelGGL(k_gemm_bf16, dim3(n_tiles * m_tiles * splits), dim3(256), 0, s,
+        hipLaunchKernelGGL(nf == 4 ? k_gemm_bf16 : k_gemm_bf16_n3, grid, dim3(256), 0, s,
             W0, W1 ? W1 : W0, boundary, N, K, xs, stride, count, m_tiles, splits, out);
     } else {
-        hipLaunchKernelGGL(k_gemm_f16, dim3(n_tiles * m_tiles * splits), dim3(256), 0, s,
+        hipLaunchKernelGGL(nf == 4 ? k_gemm_f16 : k_gemm_f16_n3, grid, dim3(256), 0, s,
             W0, W1 ? W1 : W0, boundary, N, K, xs, stride, count, m_tiles, splits, gscale, out);
     }
     return launched_ok("gemm");
@@ -1075,7 +1104,8 @@ extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, floa
     const uint32_t sq = 4;
     if ((!input_split &&
             residual_norm_split(NULL, 0, B, 1.0f, d_x, w->input_norm, xs, NULL, n, s)) ||
-        gemm(PLANES_BF16, w->qkv, NULL, LH_QKV_ROWS, LH_QKV_ROWS, LH_HIDDEN, xs, B, n, sq, P, s) ||
+        gemm(PLANES_BF16, w->qkv, NULL, LH_QKV_ROWS, LH_QKV_ROWS, LH_HIDDEN, xs, B, n, sq, P, s,
+            nullptr, 3) ||
         with_splits(sq, "qkv epilogue", [&](auto S) {
             hipLaunchKernelGGL(k_qkv_epilogue<decltype(S)::value>, dim3(n, 3), dim3(256), 0, s,
                 P, (size_t)B * LH_QKV_ROWS, make_float3(w->scale[0], w->scale[1], w->scale[2]),
@@ -1093,7 +1123,7 @@ extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, floa
             n, C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_attn, xs, B, scale_b, s) ||
         launched_ok("attention") ||
         gemm(PLANES_F16, w->o, NULL, LH_HIDDEN, LH_HIDDEN, LH_QUERY, xs, B, n, so, P, s,
-            scale_b) ||
+            scale_b, 3) ||
         residual_norm_split(P, so, B, w->scale[3], d_x, w->post_norm, xs, scale_a, n, s)) {
         return -1;
     }
