@@ -21,8 +21,9 @@ tests/golden/make_long_golden.py (device-mirror schedule):
   within MPS_TOL (1e-2) of each call's logit range of the precise path's, and
   it selects the fixture's id wherever the precise top-2 gap exceeds twice its
   largest logit error there (no id can flip otherwise). Over the 1104 calls
-  the largest error measured on MI355X is 4.7e-3 of the range and the median
-  about 1e-4; two of the 1032 ids flip, both at gaps below twice the error.
+  the largest error measured on MI355X is 2.7e-3 of the range and the median
+  about 1.2e-4, with no id flipped (builds with another prefill summation
+  order flipped two of the 1032, both at gaps below twice the error).
 """
 import hashlib
 import json
