@@ -446,10 +446,14 @@ extern "C" int lh_launch_embed(const uint16_t* E, const lh_step_params* params, 
 // 4*kvh + w % 4 over the tile's 16-token half w / 4, so the four GQA heads and
 // both halves share every K/V block staged in LDS (one staging serves 32
 // tokens), one workgroup per CU. Per 64-position block:
-//   S[16 x 64] = Q[16 x 128] K^T, Q in registers;
-//   online softmax per token row in the base-2 domain (v_exp_f32), causal mask
-//   p <= length + t;
-//   O[16 x 128] += P[16 x 64] V through a per-wave P tile in LDS.
+//   S^T[64 x 16] = K[64 x 128] Q^T, Q in registers; a lane holds one
+//     token's column (16 positions, the other three lane groups the rest);
+//   online softmax per token in the base-2 domain (v_exp_f32), causal mask
+//     p <= length + t; the row statistics reduce over the lane's own values
+//     and two permlane swaps;
+//   O^T[128 x 16] += V^T[128 x 64] P^T: the lane's column of P^T is
+//     exactly its PV B operand (k slots = the positions of its S^T rows),
+//     so P never leaves the registers.
 // out = O / l. grid tiles * 8 * splits (1-D, fa_coords), block 512. With
 // splits > 1 split z takes a contiguous range of the tile's blocks and writes
 // its unnormalized (max, sum, O) rows as part z of PM/PT/PA (partial stride
@@ -457,11 +461,12 @@ extern "C" int lh_launch_embed(const uint16_t* E, const lh_step_params* params, 
 // output goes to xs as the o projection's two FP16 planes (plane stride
 // xs_tokens * 4096, one power of two per (token, kv head) in xs_scale)
 // instead of FP32 rows of out.
-// Measured at 256 tokens after a 4096-token prefix: 94 us (104 us with QK^T
-// over three exact BF16 planes of Q and K, six products: 3.1k of a block's
-// cycles went to QK^T at the matrix cores' rate for two waves per SIMD). Per
-// block and workgroup before that change: about 2.0k cycles of plane split,
-// 3.1k of QK^T, 2.0k of PV and 2.5k of barrier skew. Earlier: V's
+// Measured at 256 tokens after a 4096-token prefix: 88 us (94 us with
+// S = Q K^T and P through a per-wave LDS tile, whose reuse of the K planes
+// cost a third barrier per block: per block about 1.5k cycles of barrier
+// skew, 1.5k of staging, 1.0k of the second barrier, 2.1k of QK^T, 1.0k of
+// the third barrier, 1.7k of softmax and P tile, 1.6k of PV; 104 us with
+// QK^T over three exact BF16 planes of Q and K, six products). Earlier: V's
 // transposed planes and the P tiles in 128-byte rows with an XOR swizzle
 // (16-way bank conflicts on the staging writes, 5.3k cycles of split) and
 // the softmax's row reductions through LDS swizzles, 129 us; 16-token
@@ -482,34 +487,8 @@ constexpr float FA_SCALE_LOG2 = 0.12751743074062763f;
 
 typedef float fa_floatx4 __attribute__((ext_vector_type(4)));
 
-// Maximum and sum over each aligned group of 16 lanes, in every lane of the
-// group: rotations by 8, 4, 2, 1 within the 16-lane row (DPP row_ror, VALU
-// only). Each lane sums in its own order, so the sums of a group may differ
-// in the last bits (tolerance path only).
-template <int R>
-__device__ __forceinline__ float row_ror(float v)
-{
-    return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x120 + R, 0xf, 0xf, false));
-}
-
-__device__ __forceinline__ float quad16_max(float v)
-{
-    v = fmaxf(v, row_ror<8>(v));
-    v = fmaxf(v, row_ror<4>(v));
-    v = fmaxf(v, row_ror<2>(v));
-    return fmaxf(v, row_ror<1>(v));
-}
-
-__device__ __forceinline__ float quad16_sum(float v)
-{
-    v = v + row_ror<8>(v);
-    v = v + row_ror<4>(v);
-    v = v + row_ror<2>(v);
-    return v + row_ror<1>(v);
-}
-
-// Maximum over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four lane groups that
-// hold one MFMA operand row), in all four: v_permlane16_swap /
+// Maximum (and sum) over lanes l, l ^ 16, l ^ 32, l ^ 48 (the four lane
+// groups that hold one MFMA operand row or D column), in all four: v_permlane16_swap /
 // v_permlane32_swap of a register with itself hands every lane its
 // partner's value in one of the two results.
 __device__ __forceinline__ float col4_max(float v)
@@ -520,6 +499,16 @@ __device__ __forceinline__ float col4_max(float v)
     const uint32_t x = __float_as_uint(w);
     const auto b = __builtin_amdgcn_permlane32_swap(x, x, false, false);
     return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+
+__device__ __forceinline__ float col4_sum(float v)
+{
+    const uint32_t u = __float_as_uint(v);
+    const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+    const float w = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+    const uint32_t x = __float_as_uint(w);
+    const auto b = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
 // Workgroup coordinates of the matrix-core attention: a 1-D grid of
@@ -551,23 +540,20 @@ __device__ __forceinline__ FaCoords fa_coords(uint32_t tiles)
 //     stays near 2^-16.
 // Every 16-bit product is exact in FP32; accumulation is the hardware's FP32.
 // Workgroup and grid as described above.
-// LDS (85 KiB): the block's K planes [2][64 pos][128 dims] (in a three-plane
-// region), each 16-byte chunk of a row XOR-swizzled by the row index, the 64
-// per-position factors 2^-ek, and V planes transposed [2][128 dims][64 pos]
-// in 144-byte rows, so the MFMA operand reads and the staging writes are
-// conflict-free; after the scores each wave's P planes [2][16 tokens][64 pos]
-// (144-byte rows) reuse the K region.
+// LDS (69 KiB): the block's K planes [2][64 pos][128 dims], each 16-byte
+// chunk of a row XOR-swizzled by the row index, the 64 per-position factors
+// 2^-ek, and V planes transposed [2][128 dims][64 pos] in 144-byte rows, so
+// the MFMA operand reads and the staging writes are conflict-free.
 typedef __bf16 fa_bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 fa_f16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t fa_u32x4 __attribute__((ext_vector_type(4)));
 
-// Transposed V and P rows hold 64 positions (128 bytes) padded to 144 bytes:
+// Transposed V rows hold 64 positions (128 bytes) padded to 144 bytes:
 // 16 consecutive rows then start 36 banks apart, which spreads the operand
 // reads and the staging writes over all 64 banks.
 constexpr uint32_t FB_ROW = 144;
 constexpr uint32_t FB_KPLANE = LH_ATTN_BLOCK * LH_HEAD_DIM * 2;   // bytes per K plane
 constexpr uint32_t FB_VPLANE = LH_HEAD_DIM * FB_ROW;              // bytes per V plane
-constexpr uint32_t FB_PPLANE = FA_TQ * FB_ROW;                    // bytes per P plane
 
 // Byte offset of (row r, element e) in a K plane: rows of 256 bytes, chunk
 // e / 8 XOR (r & 15).
@@ -580,12 +566,6 @@ __device__ __forceinline__ uint32_t fb_k_at(uint32_t r, uint32_t e)
 __device__ __forceinline__ uint32_t fb_v_at(uint32_t d, uint32_t r)
 {
     return d * FB_ROW + r * 2;
-}
-
-// Byte offset of (token t, position r) in a P plane.
-__device__ __forceinline__ uint32_t fb_p_at(uint32_t t, uint32_t r)
-{
-    return t * FB_ROW + r * 2;
 }
 
 __device__ __forceinline__ uint32_t fb_hi(float x)
@@ -618,11 +598,9 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
     float* __restrict__ PM, float* __restrict__ PT, float* __restrict__ PA, float* __restrict__ out,
     uint16_t* __restrict__ xs, uint32_t xs_tokens, float* __restrict__ xs_scale)
 {
-    // K uses two of Kp's three planes; the P tiles need all three.
-    __shared__ __attribute__((aligned(16))) uint8_t Kp[3 * FB_KPLANE];
+    __shared__ __attribute__((aligned(16))) uint8_t Kp[2 * FB_KPLANE];
     __shared__ __attribute__((aligned(16))) uint8_t Vp[2 * FB_VPLANE];
     __shared__ float sk[LH_ATTN_BLOCK];
-    static_assert(8 * 2 * FB_PPLANE <= 3 * FB_KPLANE, "P planes fit the K planes");
     const FaCoords fc = fa_coords((count + 2 * FA_TQ - 1) / (2 * FA_TQ));
     const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const uint32_t t0 = 2 * fc.t0 + FA_TQ * (wave >> 2), kvh = fc.kvh;
@@ -632,13 +610,14 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
     // first subtile's last token (clamped) and stores nothing.
     const uint32_t t0c = t0 < count ? t0 : t0 - FA_TQ;
     const uint32_t last = (t0c + FA_TQ < count ? t0c + FA_TQ : count) - 1;   // last real token
-    // Q operand of k-chunk kc: lane (token l16, group g) holds dims
-    // 32 kc + 8g .. +7, as two FP16 planes of the row scaled by 2^eq (its
-    // largest magnitude into [2^14, 2^15)). fq[r] = 2^-eq * log2(e) /
-    // sqrt(128) for the S rows 4g + r this lane holds.
+    // Q operand of k-chunk kc (the B operand of S^T = K Q^T): lane (token
+    // l16, group g) holds dims 32 kc + 8g .. +7, as two FP16 planes of the
+    // row scaled by 2^eq (its largest magnitude into [2^14, 2^15)). fq =
+    // 2^-eq * log2(e) / sqrt(128) for the lane's token, whose S^T column the
+    // lane also holds.
     const uint32_t tq = t0 + l16 <= last ? t0 + l16 : last;
     fa_f16x8 qh[4], ql[4];
-    float fq[4];
+    float fq;
     {
         const float4* src = reinterpret_cast<const float4*>(
             q + (size_t)tq * LH_QUERY + head * LH_HEAD_DIM + 8 * g);
@@ -655,12 +634,7 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
         }
         const int eq = row_exponent(col4_max(mx));
         const float f = exp2i(eq);
-        const float fs = exp2i(-eq) * FA_SCALE_LOG2;
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
-            fq[r] = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (4 * g + r),
-                __float_as_int(fs)));
-        }
+        fq = exp2i(-eq) * FA_SCALE_LOG2;
 #pragma unroll
         for (int kc = 0; kc < 4; kc++) {
             uint2 h0, l0, h1, l1;
@@ -670,19 +644,11 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
             ql[kc] = __builtin_bit_cast(fa_f16x8, fa_u32x4{l0.x, l0.y, l1.x, l1.y});
         }
     }
-    uint32_t limit[4];
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const uint32_t t = t0 + 4 * g + r;
-        limit[r] = length + (t <= last ? t : last);   // last visible position
-    }
-    float m[4], l[4];
+    const uint32_t limit = length + tq;   // the lane's token's last visible position
+    // Online-softmax state of the lane's token (replicated over its four
+    // lane groups) and O^T tiles i: dims 16 i + 4g + r of the lane's token.
+    float m = -__builtin_inff(), l = 0.0f;
     fa_floatx4 o[8];
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        m[r] = -__builtin_inff();
-        l[r] = 0.0f;
-    }
 #pragma unroll
     for (int i = 0; i < 8; i++) {
         o[i] = fa_floatx4{0.f, 0.f, 0.f, 0.f};
@@ -697,7 +663,6 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
     const uint32_t b_begin = z * per < nb ? z * per : nb;
     const uint32_t b_end = b_begin + per < nb ? b_begin + per : nb;
     const size_t head_base = lh_kv_index(capacity, 0, kvh, 0);
-    uint8_t* pw = Kp + wave * 2 * FB_PPLANE;
     // Raw K and V of block b in registers, the next block's issued before
     // this block's MFMAs. K: thread tid holds float4 words tid + 256 i of the
     // tile (lh_ktile_word order); V: rows 2 rp and 2 rp + 1, float4 column
@@ -747,7 +712,7 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
     const uint32_t visible = length + last_wg;
     const fa_floatx4 zero = fa_floatx4{0.f, 0.f, 0.f, 0.f};
     for (uint32_t b = b_begin; b < b_end; b++) {
-        __syncthreads();   // the previous block's planes and P tiles are consumed
+        __syncthreads();   // the previous block's planes are consumed
         {
             // K: the position's largest magnitude over its eight lanes (a
             // DPP quad, then the other 32-lane half), its power of two 2^ek
@@ -797,13 +762,12 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
         if (b + 1 < b_end) {
             load_block(b + 1);   // in flight during this block's MFMAs
         }
-        // S tiles j = 0..3: positions 16j + l16; k-chunk kc: dims 32kc + 8g .. +7.
+        // S^T tiles j = 0..3: rows positions 16j + 4g + r, columns tokens l16
+        // (A operand K: row 16j + l16, dims 32kc + 8g .. +7).
         fa_floatx4 s[4];
-        float fk[4];   // 2^-ek of this lane's S columns
 #pragma unroll
         for (int j = 0; j < 4; j++) {
             s[j] = zero;
-            fk[j] = sk[16 * j + l16];
         }
 #pragma unroll
         for (int kc = 0; kc < 4; kc++) {
@@ -812,68 +776,82 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
                 const uint32_t at = fb_k_at(16 * j + l16, 32 * kc + 8 * g);
                 const fa_f16x8 kh = *reinterpret_cast<const fa_f16x8*>(Kp + at);
                 const fa_f16x8 kl = *reinterpret_cast<const fa_f16x8*>(Kp + FB_KPLANE + at);
-                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ql[kc], kh, s[j], 0, 0, 0);
-                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[kc], kl, s[j], 0, 0, 0);
-                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(qh[kc], kh, s[j], 0, 0, 0);
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[kc], s[j], 0, 0, 0);
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[kc], s[j], 0, 0, 0);
+                s[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[kc], s[j], 0, 0, 0);
             }
         }
-        __syncthreads();   // every wave has read the K planes; P tiles reuse them
-        // Scale, causal mask, online softmax; P planes to this wave's tile.
-#pragma unroll
-        for (int r = 0; r < 4; r++) {
+        // Scale (2^-ek of the row's position, fq of the token), causal mask,
+        // online softmax of the lane's token over its 16 values and its three
+        // other lane groups; P^T as the PV B operand of position chunk pc:
+        // k slots 0..3 = positions 32 pc + 4g + r (tile j = 2 pc), slots 4..7
+        // = 32 pc + 16 + 4g + r (tile j = 2 pc + 1).
+        fa_bf16x8 ph[2], pm[2];
+        {
+            float v[16];
             float mx = -__builtin_inff();
 #pragma unroll
             for (int j = 0; j < 4; j++) {
-                const uint32_t p = b * LH_ATTN_BLOCK + 16 * j + l16;
-                const float v = p <= limit[r] ? s[j][r] * fk[j] * fq[r] : -__builtin_inff();
-                s[j][r] = v;
-                mx = fmaxf(mx, v);
+                const fa_floatx4 fk = *reinterpret_cast<const fa_floatx4*>(sk + 16 * j + 4 * g);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const uint32_t p = b * LH_ATTN_BLOCK + 16 * j + 4 * g + r;
+                    const float x = p <= limit ? s[j][r] * fk[r] * fq : -__builtin_inff();
+                    v[4 * j + r] = x;
+                    mx = fmaxf(mx, x);
+                }
             }
-            mx = quad16_max(mx);
-            // A split can start past a row's last visible position: keep
-            // the row empty (no exp of -inf - -inf).
-            const float m_new = fmaxf(m[r], mx);
+            mx = col4_max(mx);
+            // A split can start past a token's last visible position: keep
+            // its row empty (no exp of -inf - -inf).
+            const float m_new = fmaxf(m, mx);
             const bool empty = m_new == -__builtin_inff();
-            const float alpha = empty ? 1.0f : __builtin_amdgcn_exp2f(m[r] - m_new);
+            const float alpha = empty ? 1.0f : __builtin_amdgcn_exp2f(m - m_new);
             float sum = 0.0f;
 #pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const float e = empty ? 0.0f : __builtin_amdgcn_exp2f(s[j][r] - m_new);
-                sum = sum + e;
-                uint32_t h, mm;
-                fb_split2(e, h, mm);
-                const uint32_t at = fb_p_at(4 * g + r, 16 * j + l16);
-                *reinterpret_cast<uint16_t*>(pw + at) = (uint16_t)h;
-                *reinterpret_cast<uint16_t*>(pw + FB_PPLANE + at) = (uint16_t)mm;
+            for (int pc = 0; pc < 2; pc++) {
+                fa_u32x4 hi, mid;
+#pragma unroll
+                for (int k = 0; k < 8; k += 2) {
+                    const float e0 = empty ? 0.0f : __builtin_amdgcn_exp2f(v[8 * pc + k] - m_new);
+                    const float e1 = empty ? 0.0f : __builtin_amdgcn_exp2f(v[8 * pc + k + 1] - m_new);
+                    sum = sum + e0;
+                    sum = sum + e1;
+                    uint32_t h0, m0, h1, m1;
+                    fb_split2(e0, h0, m0);
+                    fb_split2(e1, h1, m1);
+                    hi[k / 2] = h0 | (h1 << 16);
+                    mid[k / 2] = m0 | (m1 << 16);
+                }
+                ph[pc] = __builtin_bit_cast(fa_bf16x8, hi);
+                pm[pc] = __builtin_bit_cast(fa_bf16x8, mid);
             }
-            l[r] = l[r] * alpha + quad16_sum(sum);
-            m[r] = m_new;
+            l = l * alpha + col4_sum(sum);
+            m = m_new;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                o[i][r] = o[i][r] * alpha;
+                o[i] = o[i] * alpha;
             }
         }
-        // O += P V. A operand of position chunk pc: lane (token l16, group g)
-        // holds P[l16][32 pc + 8g .. +7]; B: V rows 32 pc + 8g .. +7 of dim
-        // 16 i + l16. The wave reads back only its own P tile, and a wave's
-        // LDS accesses complete in order.
-        fa_bf16x8 ph[2], pm[2];
-#pragma unroll
-        for (int pc = 0; pc < 2; pc++) {
-            const uint32_t at = fb_p_at(l16, 32 * pc + 8 * g);
-            ph[pc] = *reinterpret_cast<const fa_bf16x8*>(pw + at);
-            pm[pc] = *reinterpret_cast<const fa_bf16x8*>(pw + FB_PPLANE + at);
-        }
+        // O^T += V^T P^T: A operand of dim tile i: lane (dim 16 i + l16, group
+        // g) holds V at positions 32 pc + 4g .. +3 and 32 pc + 16 + 4g .. +3
+        // (two 8-byte reads per plane), the slots of P^T above.
 #pragma unroll
         for (int i = 0; i < 8; i++) {
+            const uint32_t d = 16 * i + l16;
 #pragma unroll
             for (int pc = 0; pc < 2; pc++) {
-                const uint32_t at = fb_v_at(16 * i + l16, 32 * pc + 8 * g);
-                const fa_bf16x8 vh = *reinterpret_cast<const fa_bf16x8*>(Vp + at);
-                const fa_bf16x8 vm = *reinterpret_cast<const fa_bf16x8*>(Vp + FB_VPLANE + at);
-                o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pm[pc], vh, o[i], 0, 0, 0);
-                o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph[pc], vm, o[i], 0, 0, 0);
-                o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ph[pc], vh, o[i], 0, 0, 0);
+                const uint32_t a0 = fb_v_at(d, 32 * pc + 4 * g);
+                const uint32_t a1 = fb_v_at(d, 32 * pc + 16 + 4 * g);
+                const uint2 h0 = *reinterpret_cast<const uint2*>(Vp + a0);
+                const uint2 h1 = *reinterpret_cast<const uint2*>(Vp + a1);
+                const uint2 m0 = *reinterpret_cast<const uint2*>(Vp + FB_VPLANE + a0);
+                const uint2 m1 = *reinterpret_cast<const uint2*>(Vp + FB_VPLANE + a1);
+                const fa_bf16x8 vh = __builtin_bit_cast(fa_bf16x8, fa_u32x4{h0.x, h0.y, h1.x, h1.y});
+                const fa_bf16x8 vm = __builtin_bit_cast(fa_bf16x8, fa_u32x4{m0.x, m0.y, m1.x, m1.y});
+                o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vm, ph[pc], o[i], 0, 0, 0);
+                o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pm[pc], o[i], 0, 0, 0);
+                o[i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph[pc], o[i], 0, 0, 0);
             }
         }
     }
@@ -884,64 +862,58 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
     // meet in LDS before any wave leaves.
     __shared__ float gmax[2 * FA_TQ][4];
     if (splits == 1 && xs) {
+        float mr = 0.0f;
 #pragma unroll
-        for (int r = 0; r < 4; r++) {
-            float mr = 0.0f;
-#pragma unroll
-            for (int i = 0; i < 8; i++) {
-                mr = fmaxf(mr, fabsf(o[i][r] / l[r]));
-            }
-            mr = quad16_max(mr);
-            if (l16 == 0) {
-                gmax[FA_TQ * (wave >> 2) + 4 * g + r][wave & 3] = mr;
-            }
+        for (int i = 0; i < 8; i++) {
+            mr = fmaxf(mr, fmaxf(fmaxf(fabsf(o[i].x), fabsf(o[i].y)),
+                                 fmaxf(fabsf(o[i].z), fabsf(o[i].w))));
+        }
+        mr = col4_max(mr) / l;
+        if (g == 0) {
+            gmax[FA_TQ * (wave >> 2) + l16][wave & 3] = mr;
         }
         __syncthreads();
     }
-    if (t0 >= count) {
+    // The lane's token and its O^T values: dims 16 i + 4g .. +3.
+    const uint32_t t = t0 + l16;
+    if (t0 >= count || t > last) {
         return;
     }
     const uint32_t nbc = capacity / LH_ATTN_BLOCK;
-#pragma unroll
-    for (int r = 0; r < 4; r++) {
-        const uint32_t t = t0 + 4 * g + r;
-        if (t > last) {
-            continue;
-        }
-        if (splits == 1) {
-            const size_t at = (size_t)t * LH_QUERY + head * LH_HEAD_DIM + l16;
-            if (xs) {
-                const float* gm = gmax[FA_TQ * (wave >> 2) + 4 * g + r];
-                const int e = row_exponent(fmaxf(fmaxf(gm[0], gm[1]), fmaxf(gm[2], gm[3])));
-                if (l16 == 0 && (wave & 3) == 0) {
-                    xs_scale[t * LH_KV_HEADS + kvh] = exp2i(-e);
-                }
-                const float f = exp2i(e);
-                const size_t plane = (size_t)xs_tokens * LH_QUERY;
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    float rest;
-                    const size_t xa = xs_at(t, head * LH_HEAD_DIM + l16 + 16 * i, LH_QUERY);
-                    xs[xa] = (uint16_t)f16_hi(o[i][r] / l[r] * f, rest);
-                    xs[plane + xa] = (uint16_t)f16_bits(rest);
-                }
-            } else {
-#pragma unroll
-                for (int i = 0; i < 8; i++) {
-                    out[at + 16 * i] = o[i][r] / l[r];
-                }
+    if (splits == 1) {
+        const float inv = 1.0f / l;
+        if (xs) {
+            const float* gm = gmax[FA_TQ * (wave >> 2) + l16];
+            const int e = row_exponent(fmaxf(fmaxf(gm[0], gm[1]), fmaxf(gm[2], gm[3])));
+            if (g == 0 && (wave & 3) == 0) {
+                xs_scale[t * LH_KV_HEADS + kvh] = exp2i(-e);
             }
-        } else {
-            const size_t part = ((size_t)t * LH_HEADS + head) * nbc + z;
-            if (l16 == 0) {
-                PM[part] = m[r];
-                PT[part] = l[r];
-            }
-            float* dst = PA + part * LH_HEAD_DIM + l16;
+            const float f = exp2i(e);
+            const size_t plane = (size_t)xs_tokens * LH_QUERY;
 #pragma unroll
             for (int i = 0; i < 8; i++) {
-                dst[16 * i] = o[i][r];
+                const fa_floatx4 v = o[i] * (inv * f);
+                store_f16x2_4(xs, plane, xs_at(t, head * LH_HEAD_DIM + 16 * i + 4 * g, LH_QUERY),
+                    make_float4(v.x, v.y, v.z, v.w));
             }
+        } else {
+            float* dst = out + (size_t)t * LH_QUERY + head * LH_HEAD_DIM + 4 * g;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                const fa_floatx4 v = o[i] * inv;
+                *reinterpret_cast<float4*>(dst + 16 * i) = make_float4(v.x, v.y, v.z, v.w);
+            }
+        }
+    } else {
+        const size_t part = ((size_t)t * LH_HEADS + head) * nbc + z;
+        if (g == 0) {
+            PM[part] = m;
+            PT[part] = l;
+        }
+        float* dst = PA + part * LH_HEAD_DIM + 4 * g;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            *reinterpret_cast<float4*>(dst + 16 * i) = make_float4(o[i].x, o[i].y, o[i].z, o[i].w);
         }
     }
 }
