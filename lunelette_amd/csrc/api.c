@@ -5,6 +5,7 @@
 #include "lh_internal.h"
 
 #include <stdarg.h>
+#include <stdatomic.h>
 #include <stdio.h>
 
 static _Thread_local char last_error[512];
@@ -31,12 +32,36 @@ static int ok(hipError_t status, const char *what)
     return 0;
 }
 
-lh_allocation_counter lh_allocations;
+static atomic_uint allocation_fail_at;  /* 1-based allocation to fail; 0 never */
+static atomic_uint allocation_count;    /* allocations since the counter was armed */
+static atomic_long allocation_live;     /* allocations not yet freed */
+
+void lh_allocations_arm(unsigned nth)
+{
+    atomic_store_explicit(&allocation_count, 0, memory_order_relaxed);
+    atomic_store_explicit(&allocation_fail_at, nth, memory_order_relaxed);
+}
+
+unsigned lh_allocations_count(void)
+{
+    return atomic_load_explicit(&allocation_count, memory_order_relaxed);
+}
+
+long lh_allocations_live(void)
+{
+    return atomic_load_explicit(&allocation_live, memory_order_relaxed);
+}
 
 static int forced_failure(void)
 {
-    lh_allocations.count++;
-    return lh_allocations.fail_at && lh_allocations.count == lh_allocations.fail_at;
+    unsigned n = atomic_fetch_add_explicit(&allocation_count, 1, memory_order_relaxed) + 1;
+    unsigned at = atomic_load_explicit(&allocation_fail_at, memory_order_relaxed);
+    return at && n == at;
+}
+
+static void count_live(long delta)
+{
+    atomic_fetch_add_explicit(&allocation_live, delta, memory_order_relaxed);
 }
 
 hipError_t lh_dev_malloc(void **ptr, size_t bytes)
@@ -47,7 +72,7 @@ hipError_t lh_dev_malloc(void **ptr, size_t bytes)
     }
     hipError_t status = hipMalloc(ptr, bytes ? bytes : 16);
     if (status == hipSuccess) {
-        lh_allocations.live++;
+        count_live(1);
     } else {
         *ptr = NULL;
     }
@@ -62,7 +87,7 @@ hipError_t lh_host_malloc(void **ptr, size_t bytes, unsigned flags)
     }
     hipError_t status = hipHostMalloc(ptr, bytes ? bytes : 16, flags);
     if (status == hipSuccess) {
-        lh_allocations.live++;
+        count_live(1);
     } else {
         *ptr = NULL;
     }
@@ -73,7 +98,7 @@ void lh_dev_free(void *ptr)
 {
     if (ptr) {
         (void)hipFree(ptr);
-        lh_allocations.live--;
+        count_live(-1);
     }
 }
 
@@ -81,7 +106,7 @@ void lh_host_free(void *ptr)
 {
     if (ptr) {
         (void)hipHostFree(ptr);
-        lh_allocations.live--;
+        count_live(-1);
     }
 }
 

@@ -67,20 +67,20 @@ int lh_launch_expf(const float *x, float *out, size_t n, hipStream_t s);
 void lh_set_error(const char *format, ...);
 
 /* Every device and pinned-host allocation of the library goes through these
- * (host_util.c). They count allocations and frees, and fail the fail_at-th
- * allocation after the counter was armed: the host-forced allocation failure
- * of the reference's tests (tests/test_metal.m:888-954). Only the test-seam
- * library (test_seams.c, not part of the shipped library) arms it. */
+ * (api.c). They count allocations and frees (relaxed atomics: contexts may be
+ * created and destroyed on different threads), and fail the nth allocation
+ * after the counter was armed: the host-forced allocation failure of the
+ * reference's tests (tests/test_metal.m:888-954). Only the test-seam library
+ * (test_seams.c, not part of the shipped library) arms it. */
 hipError_t lh_dev_malloc(void **ptr, size_t bytes);
 hipError_t lh_host_malloc(void **ptr, size_t bytes, unsigned flags);
 void lh_dev_free(void *ptr);
 void lh_host_free(void *ptr);
-typedef struct {
-    unsigned fail_at;   /* 1-based index of the allocation to fail; 0 never */
-    unsigned count;     /* allocations since the counter was armed */
-    long live;          /* allocations not yet freed */
-} lh_allocation_counter;
-extern lh_allocation_counter lh_allocations;
+/* Arms the counter: the nth allocation from now fails (1-based; 0 never). */
+void lh_allocations_arm(unsigned nth);
+/* Allocations since the counter was armed, and allocations not yet freed. */
+unsigned lh_allocations_count(void);
+long lh_allocations_live(void);
 
 /* Host-forced execution faults of one runtime context (runtime.c), set only
  * by the test-seam library: the analogue of the reference's mocked command

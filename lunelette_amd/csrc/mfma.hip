@@ -493,6 +493,33 @@ __device__ __forceinline__ void store_tile(const floatx4 (&acc)[4][NF], float* _
     }
 }
 
+// store_tile, or with add the tile added to what the same lanes stored there
+// before (each element is read back only by the lane that wrote it).
+template <int NF>
+__device__ __forceinline__ void fold_tile(const floatx4 (&acc)[4][NF], float* __restrict__ o,
+    uint32_t N, uint32_t m0, uint32_t n0, uint32_t count, uint32_t lane, bool add)
+{
+    if (!add) {
+        store_tile<NF>(acc, o, N, m0, n0, count, lane);
+        return;
+    }
+    const uint32_t g = lane >> 4, l16 = lane & 15;
+#pragma unroll
+    for (int mf = 0; mf < 4; mf++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+            const uint32_t m = m0 + 16 * mf + 4 * g + r;
+            if (m < count) {
+#pragma unroll
+                for (int nf = 0; nf < NF; nf++) {
+                    float* const e = o + (size_t)m * N + n0 + 16 * nf + l16;
+                    *e = *e + acc[mf][nf][r];
+                }
+            }
+        }
+    }
+}
+
 // P activation planes (PLANES_BF16 or PLANES_F16) of the same layout
 // xs[p][m][k]. Each wave owns 16 NF weight rows, the workgroup 64 NF (256 or
 // 192). grid: n_tiles * m_tiles * splits workgroups of 256 threads, two
@@ -627,6 +654,15 @@ __device__ __forceinline__ void gemm_tile(const uint8_t* __restrict__ W0,
 // granule and by gscale[m][j] before it is stored, so the partials are
 // unscaled. The factors are powers of two (exact products); the workgroup's
 // 64 x GRANULES factors are staged in LDS before the first stage.
+// The accumulator holds at most about 2^38 in its granule's units (576
+// products of a plane value below 2^15 and a weight below 2^9), so a ratio
+// above 2^64 could overflow it (a granule whose largest value is more than
+// 2^64 below its predecessor's, e.g. SiLU of very negative gates). Where a
+// lane's rows meet such a ratio, its wave folds the unscaled accumulator into
+// the column's partial in memory instead and restarts from zero; the column's
+// last store then adds to what was folded (each lane re-reads only what it
+// wrote itself).
+constexpr float WIDE_RATIO = 0x1p64f;
 constexpr uint32_t GRANULES = 16;
 static_assert(GRANULES == DOWN_SPLITS, "the down input's scale granules");
 
@@ -684,30 +720,50 @@ __device__ __forceinline__ void gemm_stream_tile(const uint8_t* __restrict__ W0,
     };
     floatx4 acc[4][4];
     zero_tile<4>(acc);
+    // Whether this wave has folded part of the current column into memory.
+    bool folded = false;
     // A column's partial leaves after its last stage or the range's last unit.
     auto finish = [&](uint32_t u) {
         const uint32_t nt = u / stages, st = u - nt * stages;
         const bool last = u + 1 == u1 || st + 1 == stages;
+        float* const dst = out + (size_t)(G - stream_group(nt * stages, units, groups)) *
+            stride_tokens * N;
         if (gscale && (last || (st + 1) % gstages == 0)) {
             const uint32_t j = st / gstages;
             const float* gf = reinterpret_cast<const float*>(gs);
+            bool wide = false;
+            if (!last) {
+#pragma unroll
+                for (int mf = 0; mf < 4; mf++) {
+#pragma unroll
+                    for (int r = 0; r < 4; r++) {
+                        const float* row = gf + (16 * mf + 4 * g + r) * GRANULES;
+                        wide = wide || row[j] > WIDE_RATIO * row[j + 1];
+                    }
+                }
+                wide = __builtin_amdgcn_ballot_w64(wide) != 0;
+            }
 #pragma unroll
             for (int mf = 0; mf < 4; mf++) {
 #pragma unroll
                 for (int r = 0; r < 4; r++) {
                     const float* row = gf + (16 * mf + 4 * g + r) * GRANULES;
-                    const float f = last ? row[j] : row[j] / row[j + 1];
+                    const float f = last || wide ? row[j] : row[j] / row[j + 1];
 #pragma unroll
                     for (int nf = 0; nf < 4; nf++) {
                         acc[mf][nf][r] *= f;
                     }
                 }
             }
+            if (wide) {
+                fold_tile<4>(acc, dst, N, m0, nt * GN + wave * 64, count, lane, folded);
+                folded = true;
+                zero_tile<4>(acc);
+            }
         }
         if (last) {
-            const uint32_t slot = G - stream_group(nt * stages, units, groups);
-            store_tile<4>(acc, out + (size_t)slot * stride_tokens * N, N, m0, nt * GN + wave * 64,
-                count, lane);
+            fold_tile<4>(acc, dst, N, m0, nt * GN + wave * 64, count, lane, folded);
+            folded = false;
             zero_tile<4>(acc);
         }
     };

@@ -28,16 +28,15 @@ int lunelette_metal_test_set_logit(struct lunelette_metal *context, size_t index
 
 void lunelette_metal_test_fail_allocation(unsigned nth)
 {
-    lh_allocations.fail_at = nth;
-    lh_allocations.count = 0;
+    lh_allocations_arm(nth);
 }
 
 unsigned lunelette_metal_test_allocations(void)
 {
-    return lh_allocations.count;
+    return lh_allocations_count();
 }
 
 long lunelette_metal_test_live_allocations(void)
 {
-    return lh_allocations.live;
+    return lh_allocations_live();
 }

@@ -14,7 +14,8 @@
  * 1 attention residual skipped, 2 post-norm fed x instead of x+o,
  * 3 query factor on K instead of Q, 4 V rotated before caching,
  * 5 head on row 0 instead of the last row, 6 K cached unrotated,
- * 7 MLP residual added to the layer input instead of x+o. */
+ * 7 MLP residual added to the layer input instead of x+o,
+ * 8 query factor dropped (neither Q nor K scaled). */
 #ifndef ORC_PLANT
 #define ORC_PLANT 0
 #endif
@@ -56,7 +57,7 @@ void orc_layer_forward(int schedule, orc_model *model, size_t layer, float *x,
     orc_matvec(schedule, ORC_W_FP8, w->q, w->scale[0], xn, q, Q, H, count);
     orc_matvec(schedule, ORC_W_FP8, w->k, w->scale[1], xn, k, KV, H, count);
     orc_matvec(schedule, ORC_W_FP8, w->v, w->scale[2], xn, v, KV, H, count);
-    orc_rope(q, cosine, sine, ORC_PLANT == 3 ? NULL : factor, rq, Q, count);
+    orc_rope(q, cosine, sine, ORC_PLANT == 3 || ORC_PLANT == 8 ? NULL : factor, rq, Q, count);
     orc_rope(k, cosine, sine, ORC_PLANT == 3 ? factor : NULL, rk, KV, count);
     if (ORC_PLANT == 4) {
         memcpy(attn, v, count * KV * sizeof(float));

@@ -77,6 +77,35 @@ def load_path(path):
     return l
 
 
+PLANTS = {1: "attention residual skipped", 2: "post-norm fed x instead of x+o",
+          3: "query factor on K instead of Q", 4: "V rotated before caching",
+          5: "head on row 0", 6: "K cached unrotated", 7: "MLP residual on the layer input",
+          8: "query factor dropped"}
+
+
+def build_planted(plants, directory):
+    """Oracle builds with one planted composition mistake each (orc_model.c
+    compiled with -DORC_PLANT=n), compiled in parallel into `directory`;
+    returns {n: library}."""
+    import subprocess
+    src = os.path.join(ROOT, "oracle")
+    procs = {}
+    for n in plants:
+        lib = os.path.join(str(directory), "liboracle_plant%d.so" % n)
+        cmd = ["gcc", "-std=c11", "-O3", "-march=x86-64-v3", "-ffp-contract=off",
+               "-fno-math-errno", "-fopenmp", "-fPIC", "-shared", "-DORC_PLANT=%d" % n,
+               os.path.join(src, "orc_basic.c"), os.path.join(src, "orc_kernels.c"),
+               os.path.join(src, "orc_model.c"), "-o", lib, "-lm"]
+        procs[n] = (subprocess.Popen(cmd, stderr=subprocess.PIPE), lib)
+    libs = {}
+    for n, (proc, lib) in procs.items():
+        _, err = proc.communicate()
+        if proc.returncode != 0:
+            raise RuntimeError(err.decode())
+        libs[n] = load_path(lib)
+    return libs
+
+
 def load_ref():
     """The reference's own C (safetensors container, checkpoint contract, FP8/BF16
     decode, YaRN, greedy), or None."""

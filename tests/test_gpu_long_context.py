@@ -18,12 +18,16 @@ tests/golden/make_long_golden.py (device-mirror schedule):
   precise path selects the fixture's 8 x 129 ids. The matrix-core path runs
   the same workload in lockstep with the precise path, both fed the fixture's
   ids (so one near-tie cannot change every later context): its logits stay
-  within MPS_TOL (1e-2) of each call's logit range of the precise path's, and
-  it selects the fixture's id wherever the precise top-2 gap exceeds twice its
-  largest logit error there (no id can flip otherwise). Over the 1104 calls
-  the largest error measured on MI355X is 2.7e-3 of the range and the median
-  about 1.2e-4, with no id flipped (builds with another prefill summation
-  order flipped two of the 1032, both at gaps below twice the error).
+  within MPS_TOL (5e-3) of each call's logit range of the precise path's, the
+  median over the calls within MPS_MEDIAN_TOL (5e-4), and it selects the
+  fixture's id wherever the precise top-2 gap exceeds twice its largest logit
+  error there (no id can flip otherwise). Over the 1104 calls the largest
+  error measured on MI355X is 2.7e-3 of the range and the median about
+  1.2e-4, with no id flipped (builds with another prefill summation order
+  flipped two of the 1032, both at gaps below twice the error). The bound is
+  looser than the 1e-3 of the 2-layer and config-4 workloads because after a
+  16K-token matrix-core prefill the 26-layer stack amplifies the prefill's
+  rounding through near-tie softmax rows; those errors move no selected id.
 """
 import hashlib
 import json
@@ -68,7 +72,8 @@ def test_attention_mfma_long_prefix(gpu, length, count):
     assert np.max(np.abs(got - want)) < 2e-4
 
 
-MPS_TOL = 1e-2
+MPS_TOL = 5e-3
+MPS_MEDIAN_TOL = 5e-4
 
 
 def run_workload(fx, prefill_mode, turns, forced=None):
@@ -166,6 +171,8 @@ def test_long_reuse_26layer_mps_lockstep(gpu):
                     selected, gap, err)
             selected += 1
     assert selected == len(want)
-    print("mps lockstep: %d calls, largest error %.3g of the logit range, %d near-tie flips %s"
-          % (call + 1, worst, len(flips), flips))
+    errors = [e for v in by_kind.values() for e in v]
+    print("mps lockstep: %d calls, largest error %.3g of the logit range (median %.3g), "
+          "%d near-tie flips %s" % (call + 1, worst, float(np.median(errors)), len(flips), flips))
+    assert float(np.median(errors)) <= MPS_MEDIAN_TOL
     print("mps lockstep errors by kind:", {k: (max(v), float(np.median(v))) for k, v in by_kind.items()})

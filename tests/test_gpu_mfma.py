@@ -197,6 +197,47 @@ def test_mfma_layer_down_input_range(gpu, shift):
     assert np.median(np.abs(gx - wx) / np.maximum(np.abs(wx), 1e-30)) < 1e-5
 
 
+def test_mfma_layer_down_granule_gap(gpu):
+    """Adjacent 576-column granules of the down input whose largest values
+    lie more than 2^100 apart: every gate row of granules 5 and 11 is the code
+    -1.0 and the MLP input is positive, so those gates sit near -80 and
+    SiLU(gate) * up near 2^-100 there, against about 2^17 in the granules
+    before them. A stream-K segment that crosses such a boundary must not
+    carry its accumulator over by the ratio of the granules' scales (it would
+    overflow FP32); the layer stays finite and within the config-3 tolerance
+    of the oracle."""
+    from test_gpu_layer import oracle_layer, run_layer
+    host = dict(syn.layer(SEED, 3))
+    length, count, capacity = 64, 192, 256
+    rng = np.random.default_rng(77)
+    x = (np.abs(rng.normal(size=count * 3072)) + 0.5).astype(np.float32)
+    # o's output 2^-40 of its usual size: the MLP input stays x (positive).
+    host["scale_o"] = math.ldexp(1.0, -46)
+    gate = np.array(host["gate"])
+    tiny = np.r_[5 * 576:6 * 576, 11 * 576:12 * 576]
+    gate[tiny] = 0xB8
+    host["gate"] = gate
+    xx = x.reshape(count, 3072).astype(np.float64)
+    gamma = syn.bf16_to_f32(host["post_norm"]).astype(np.float64)
+    xn = xx / np.sqrt(np.mean(xx * xx, axis=1, keepdims=True) + 1e-5) * gamma
+    host["scale_gate"] = float(np.float32(80.0 / np.median(xn.sum(axis=1))))
+    dec = gpu_util.decode_table().astype(np.float64)
+    g = host["scale_gate"] * (xn @ dec[gate].T)
+    u = host["scale_up"] * (xn @ dec[host["up"]].T)
+    silu = g * np.exp(-np.logaddexp(0.0, -g))
+    y = np.abs(silu * u).reshape(count, 16, 576).max(axis=2)
+    assert np.all(np.log2(y[:, 4] / y[:, 5]) > 100) and np.all(np.log2(y[:, 10] / y[:, 11]) > 100)
+    kpm = syn.normal_f32(SEED, 9302, length * 1024).reshape(length, 1024)
+    vpm = syn.normal_f32(SEED, 9303, length * 1024).reshape(length, 1024)
+    got = run_layer(gpu, host, x, kpm, vpm, length, count, capacity, lh.PATH_MFMA)
+    want = oracle_layer(host, x, kpm, vpm, length, count, capacity, MIRROR)
+    gx, wx = got[0].reshape(count, 3072), want[0].reshape(count, 3072)
+    assert np.isfinite(gx).all()
+    rowmax = np.max(np.abs(wx), axis=1, keepdims=True)
+    assert np.max(np.abs(gx - wx) / rowmax) < 1e-3
+    assert np.median(np.abs(gx - wx) / np.maximum(np.abs(wx), 1e-30)) < 1e-5
+
+
 @pytest.mark.parametrize("tail", [np.inf, np.nan], ids=["inf", "nan"])
 @pytest.mark.parametrize("length,count,capacity", [(60, 3, 256), (256, 37, 4352),
                                                    (4000, 256, 4352)])

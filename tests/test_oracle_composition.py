@@ -25,11 +25,9 @@ a BF16 N(0,1) embedding) come from the library's seeded generators. The
 per-tensor scales are this test's own small powers of two, so that scores have
 a standard deviation near 2 and the softmax stays soft: a composition slip then
 moves the result by far more than rounding does. Both oracle schedules must agree with float64 to
-1e-5 of each row's max-abs. Seven planted composition mistakes, compiled into
+1e-5 of each row's max-abs. Eight planted composition mistakes, compiled into
 oracle variants with -DORC_PLANT=n, must each fail the same comparison.
 """
-import os
-import subprocess
 
 import numpy as np
 import pytest
@@ -46,9 +44,7 @@ SCALES = {"q": 2.0 ** -12, "k": 2.0 ** -12, "v": 2.0 ** -12, "o": 2.0 ** -11,
 EPS = float(np.float32(1e-5))
 SCORE_SCALE = 0.08838834764831845
 TOL = 1e-5
-PLANTS = {1: "attention residual skipped", 2: "post-norm fed x instead of x+o",
-          3: "query factor on K instead of Q", 4: "V rotated before caching",
-          5: "head on row 0", 6: "K cached unrotated", 7: "MLP residual on the layer input"}
+PLANTS = oracle_lib.PLANTS
 
 
 def e4m3_f64():
@@ -297,29 +293,14 @@ def test_oracle_composition_matches_float64(schedule, which, case_start, case_lo
 @pytest.fixture(scope="module")
 def planted(tmp_path_factory):
     """Oracle builds with one planted composition mistake each."""
-    src = os.path.join(oracle_lib.ROOT, "oracle")
-    out = tmp_path_factory.mktemp("planted")
-    procs = {}
-    for n in PLANTS:
-        lib = str(out / ("liboracle_plant%d.so" % n))
-        cmd = ["gcc", "-std=c11", "-O2", "-march=x86-64-v3", "-ffp-contract=off",
-               "-fno-math-errno", "-fopenmp", "-fPIC", "-shared", "-DORC_PLANT=%d" % n,
-               os.path.join(src, "orc_basic.c"), os.path.join(src, "orc_kernels.c"),
-               os.path.join(src, "orc_model.c"), "-o", lib, "-lm"]
-        procs[n] = (subprocess.Popen(cmd, stderr=subprocess.PIPE), lib)
-    libs = {}
-    for n, (proc, lib) in procs.items():
-        _, err = proc.communicate()
-        assert proc.returncode == 0, err.decode()
-        libs[n] = oracle_lib.load_path(lib)
-    return libs
+    return oracle_lib.build_planted(sorted(PLANTS), tmp_path_factory.mktemp("planted"))
 
 
 @pytest.mark.parametrize("plant", sorted(PLANTS), ids=lambda n: PLANTS[n].replace(" ", "_"))
 def test_planted_composition_mistake_fails(plant, planted, case_start, case_long):
     # Each mistake must miss the float64 restatement by at least 100x the
     # tolerance on one of the two cases (the query factor only differs from 1
-    # at positions >= 16384, so plant 3 shows on the long case alone).
+    # at positions >= 16384, so plants 3 and 8 show on the long case alone).
     worst = 0.0
     for case in (case_start, case_long):
         worst = max(worst, *case.errors(MIRROR, lib=planted[plant], layers=False).values())
