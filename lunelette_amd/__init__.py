@@ -110,6 +110,9 @@ def test_lib():
         _proto(l, "lunelette_metal_test_fail_allocation", None, ctypes.c_uint)
         _proto(l, "lunelette_metal_test_allocations", ctypes.c_uint)
         _proto(l, "lunelette_metal_test_live_allocations", ctypes.c_long)
+        _proto(l, "lunelette_metal_test_fail_host_allocation", None, ctypes.c_uint)
+        _proto(l, "lunelette_metal_test_host_allocations", ctypes.c_uint)
+        _proto(l, "lunelette_metal_test_live_host_allocations", ctypes.c_long)
         _test_lib = l
     return _test_lib
 

@@ -8,6 +8,7 @@
  * of one text), measured, and written to the caller's array only when it fits
  * the 256-id context, so a failure leaves ids and count untouched. */
 #include "lunelette_chat.h"
+#include "lh_host_alloc.h"
 
 #include <stdio.h>
 #include <stdlib.h>
@@ -90,7 +91,7 @@ int lunelette_chat_prompt(const lunelette_tokenizer *tokenizer, const char *prom
     status = 0;
 release:
     for (size_t i = 0; i < segments; i++) {
-        free(plan[i].ids);
+        lh_free(plan[i].ids);
     }
     return status;
 }

@@ -2,6 +2,7 @@
  * the reference's include/generation.h:38-71. */
 #include "lunelette_generation.h"
 #include "lh_scan.h"
+#include "lh_host_alloc.h"
 
 #include <math.h>
 #include <stdint.h>
@@ -114,12 +115,12 @@ int lunelette_generate_with_logits_capacity(lunelette_logits_fn next, void *cont
     int64_t *prefix = NULL;
     float *scratch = NULL;
     if (stop < 0) {
-        prefix = malloc(context_limit * sizeof *prefix);
-        scratch = malloc(LUNELETTE_VOCAB_SIZE * sizeof *scratch);
+        prefix = lh_malloc(context_limit * sizeof *prefix);
+        scratch = lh_malloc(LUNELETTE_VOCAB_SIZE * sizeof *scratch);
         if (!prefix || !scratch) {
             say(error, capacity, "generation: scratch allocation failed");
-            free(prefix);
-            free(scratch);
+            lh_free(prefix);
+            lh_free(scratch);
             return -1;
         }
         memcpy(prefix, prompt, count * sizeof *prefix);
@@ -142,8 +143,8 @@ int lunelette_generate_with_logits_capacity(lunelette_logits_fn next, void *cont
         staged.tokens[staged.count++] = last;
         stop = stop_rule(last, staged.count, length, context_limit, config);
     }
-    free(prefix);
-    free(scratch);
+    lh_free(prefix);
+    lh_free(scratch);
     if (stop < 0) {
         return -1;
     }

@@ -33,6 +33,12 @@ void lunelette_metal_test_fail_allocation(unsigned nth);
 /* Allocations since the counter was armed, and allocations not yet freed. */
 unsigned lunelette_metal_test_allocations(void);
 long lunelette_metal_test_live_allocations(void);
+/* The same for the host heap allocations of the generation loop, tokenizer
+ * and chat framing (lh_host_alloc.h): the nth from now on fails (0: none). A
+ * block handed to a caller (token ids, text) stays counted as live. */
+void lunelette_metal_test_fail_host_allocation(unsigned nth);
+unsigned lunelette_metal_test_host_allocations(void);
+long lunelette_metal_test_live_host_allocations(void);
 
 #ifdef __cplusplus
 }

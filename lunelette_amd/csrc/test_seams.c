@@ -2,6 +2,7 @@
  * the shipped liblunelette_hip.so neither contains nor exports them. */
 #include "lh_test_seams.h"
 #include "lh_internal.h"
+#include "lh_host_alloc.h"
 
 int lunelette_metal_test_inject(struct lunelette_metal *context, int what)
 {
@@ -39,4 +40,19 @@ unsigned lunelette_metal_test_allocations(void)
 long lunelette_metal_test_live_allocations(void)
 {
     return lh_allocations_live();
+}
+
+void lunelette_metal_test_fail_host_allocation(unsigned nth)
+{
+    lh_host_allocations_arm(nth);
+}
+
+unsigned lunelette_metal_test_host_allocations(void)
+{
+    return lh_host_allocations_count();
+}
+
+long lunelette_metal_test_live_host_allocations(void)
+{
+    return lh_host_allocations_live();
 }

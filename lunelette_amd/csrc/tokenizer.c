@@ -19,6 +19,7 @@
 #define _POSIX_C_SOURCE 200809L
 #include "lunelette_tokenizer.h"
 #include "lh_unicode_classes.h"
+#include "lh_host_alloc.h"
 
 #include <stdarg.h>
 #include <stdio.h>
@@ -112,6 +113,7 @@ typedef struct {
     size_t length, at;
     jnode *node;               /* node 0 is the missing-node sentinel */
     uint32_t count, capacity;
+    int out_of_memory;         /* a node array could not grow */
 } jdoc;
 
 static void j_space(jdoc *d)
@@ -135,8 +137,9 @@ static uint32_t j_new(jdoc *d, char kind)
         if (capacity > J_MAX_NODES) {
             capacity = J_MAX_NODES;
         }
-        jnode *grown = realloc(d->node, (size_t)capacity * sizeof(*grown));
+        jnode *grown = lh_realloc(d->node, (size_t)capacity * sizeof(*grown));
         if (!grown) {
+            d->out_of_memory = 1;
             return 0;
         }
         d->node = grown;
@@ -401,13 +404,27 @@ static uint32_t j_value(jdoc *d, int depth)
 
 static void j_free(jdoc *d)
 {
-    free(d->data);
-    free(d->node);
+    lh_free(d->data);
+    lh_free(d->node);
     memset(d, 0, sizeof(*d));
 }
 
-/* Reads a whole file of at most 32 MiB holding exactly one value. */
+/* Reads a whole file of at most 32 MiB holding exactly one value: 1, or 0
+ * (unreadable, not JSON, past a limit), or -1 when memory ran out. */
+static int j_parse(const char *path, jdoc *d);
+
 static int j_read(const char *path, jdoc *d)
+{
+    const int ok = j_parse(path, d);
+    if (ok) {
+        return 1;
+    }
+    const int out_of_memory = d->out_of_memory;
+    j_free(d);
+    return out_of_memory ? -1 : 0;
+}
+
+static int j_parse(const char *path, jdoc *d)
 {
     memset(d, 0, sizeof(*d));
     FILE *f = fopen(path, "rb");
@@ -423,26 +440,18 @@ static int j_read(const char *path, jdoc *d)
         return 0;
     }
     d->length = (size_t)size;
-    d->data = malloc(d->length + 1);
+    d->data = lh_malloc(d->length + 1);
+    d->out_of_memory = !d->data;
     const int read_ok = d->data && fread(d->data, 1, d->length, f) == d->length && !ferror(f);
     fclose(f);
     if (read_ok) {
         j_new(d, 0);                       /* the sentinel, node 0 */
     }
-    if (!read_ok || d->count != 1) {
-        j_free(d);
-        return 0;
-    }
-    if (j_value(d, 0) != 1) {
-        j_free(d);
+    if (!read_ok || d->count != 1 || j_value(d, 0) != 1) {
         return 0;
     }
     j_space(d);
-    if (d->at != d->length) {
-        j_free(d);
-        return 0;
-    }
-    return 1;
+    return d->at == d->length;
 }
 
 /* Value of key in the object node (0 when absent or not an object). */
@@ -582,8 +591,8 @@ static int b64_decode(const jdoc *d, uint32_t node, unsigned char *out, size_t *
 void lunelette_tokenizer_close(lunelette_tokenizer *t)
 {
     if (t) {
-        free(t->arena);
-        free(t);
+        lh_free(t->arena);
+        lh_free(t);
     }
 }
 
@@ -592,11 +601,11 @@ void lunelette_tokenizer_close(lunelette_tokenizer *t)
 static int load_vocab(const jdoc *d, uint32_t vocab, lunelette_tokenizer *t, char *error,
     size_t size)
 {
-    uint32_t *node_of = calloc(TK_ORDINARY, sizeof(*node_of));
-    uint32_t *length_of = calloc(TK_ORDINARY, sizeof(*length_of));
+    uint32_t *node_of = lh_calloc(TK_ORDINARY, sizeof(*node_of));
+    uint32_t *length_of = lh_calloc(TK_ORDINARY, sizeof(*length_of));
     int ok = 0;
     if (!node_of || !length_of) {
-        fail(error, size, "tokenizer: allocation failed");
+        fail(error, size, "tokenizer open: out of memory");
         goto done;
     }
     unsigned entries = 0;
@@ -607,12 +616,12 @@ static int load_vocab(const jdoc *d, uint32_t vocab, lunelette_tokenizer *t, cha
         const uint32_t bytes = j_field(d, e, "token_bytes");
         if (!j_u32(d, j_field(d, e, "rank"), &rank) || rank >= TK_ORDINARY || node_of[rank] ||
             !b64_decode(d, bytes, NULL, &n)) {
-            fail(error, size, "tokenizer: vocab entry %u invalid rank/base64/duplicate rank",
+            fail(error, size, "tokenizer open: vocabulary entry %u has a bad rank, bad base64 or a repeated rank",
                 entries);
             goto done;
         }
         if (total > TK_MAX_VOCAB_BYTES - n) {
-            fail(error, size, "tokenizer: vocab bytes exceed 16 MiB");
+            fail(error, size, "tokenizer open: token bytes total more than 16 MiB");
             goto done;
         }
         node_of[rank] = bytes;
@@ -620,12 +629,12 @@ static int load_vocab(const jdoc *d, uint32_t vocab, lunelette_tokenizer *t, cha
         total += n;
     }
     if (entries != TK_ORDINARY) {
-        fail(error, size, "tokenizer: expected 130072 ordinary ranks, got %u", entries);
+        fail(error, size, "tokenizer open: %u ordinary ranks where the format has 130072", entries);
         goto done;
     }
-    t->arena = malloc(total ? total : 1);
+    t->arena = lh_malloc(total ? total : 1);
     if (!t->arena) {
-        fail(error, size, "tokenizer: allocation failed");
+        fail(error, size, "tokenizer open: out of memory");
         goto done;
     }
     t->start[0] = 0;
@@ -634,7 +643,7 @@ static int load_vocab(const jdoc *d, uint32_t vocab, lunelette_tokenizer *t, cha
         b64_decode(d, node_of[r], t->arena + t->start[r], &n);
         t->start[r + 1] = t->start[r] + (uint32_t)n;
         if (tk_find(t, t->arena + t->start[r], n) != TK_NONE) {
-            fail(error, size, "tokenizer: rank %u duplicate bytes", r);
+            fail(error, size, "tokenizer open: rank %u repeats the bytes of a lower rank", r);
             goto done;
         }
         tk_insert(t, r);
@@ -642,14 +651,14 @@ static int load_vocab(const jdoc *d, uint32_t vocab, lunelette_tokenizer *t, cha
     for (unsigned byte = 0; byte < 256; byte++) {
         const unsigned char b = (unsigned char)byte;
         if (tk_find(t, &b, 1) == TK_NONE) {
-            fail(error, size, "tokenizer: missing byte token %u", byte);
+            fail(error, size, "tokenizer open: no single-byte token for byte %u", byte);
             goto done;
         }
     }
     ok = 1;
 done:
-    free(node_of);
-    free(length_of);
+    lh_free(node_of);
+    lh_free(length_of);
     return ok;
 }
 
@@ -665,13 +674,13 @@ static int check_specials(const jdoc *d, uint32_t specials, char *error, size_t 
         if (!j_u32(d, j_field(d, e, "rank"), &rank) || rank >= TK_SPECIALS || spelling[rank] ||
             !text || d->node[text].kind != '"' || !d->node[text].length || !control ||
             (d->node[control].kind != 't' && d->node[control].kind != 'f')) {
-            return fail(error, size, "tokenizer: invalid/duplicate special rank or string");
+            return fail(error, size, "tokenizer open: a special token has a bad or repeated rank or spelling");
         }
         for (unsigned r = 0; r < TK_SPECIALS; r++) {
             const uint32_t other = spelling[r];
             if (other && d->node[other].length == d->node[text].length &&
                 !memcmp(d->node[other].text, d->node[text].text, d->node[text].length)) {
-                return fail(error, size, "tokenizer: duplicate special spelling");
+                return fail(error, size, "tokenizer open: two special tokens share a spelling");
             }
         }
         spelling[rank] = text;
@@ -686,20 +695,24 @@ static int check_specials(const jdoc *d, uint32_t specials, char *error, size_t 
         framed &= j_is_string(d, spelling[framing[i].rank], framing[i].text);
     }
     return framed ? 1 :
-        fail(error, size, "tokenizer: expected 1000 specials and supported framing IDs");
+        fail(error, size, "tokenizer open: the special tokens are not the 1000 of the format with its framing ids");
 }
 
 int lunelette_tokenizer_open(const char *path, lunelette_tokenizer **out, char *error,
     size_t error_size)
 {
     if (!out) {
-        return fail(error, error_size, "tokenizer: NULL output pointer");
+        return fail(error, error_size, "tokenizer open: no place for the handle");
     }
     *out = NULL;
     jdoc d;
-    if (!path || !j_read(path, &d)) {
-        return fail(error, error_size, "tokenizer %s: invalid JSON, I/O, or parser limit "
-            "(32 MiB, depth 32, 1500000 nodes)", path ? path : "(null)");
+    const int read = path ? j_read(path, &d) : 0;
+    if (read < 0) {
+        return fail(error, error_size, "tokenizer open %s: out of memory", path);
+    }
+    if (!read) {
+        return fail(error, error_size, "tokenizer open %s: unreadable, not JSON, or past the reader's "
+            "limits (32 MiB, nesting 32, 1500000 values)", path ? path : "(null)");
     }
     lunelette_tokenizer *t = NULL;
     int ok = 0;
@@ -709,24 +722,25 @@ int lunelette_tokenizer_open(const char *path, lunelette_tokenizer **out, char *
         !j_is_u32(&d, config, "num_vocab_tokens", LUNELETTE_TOKENIZER_VOCAB_SIZE) ||
         !j_is_u32(&d, config, "default_vocab_size", LUNELETTE_TOKENIZER_VOCAB_SIZE) ||
         !j_is_u32(&d, config, "default_num_special_tokens", TK_SPECIALS)) {
-        fail(error, error_size, "tokenizer %s: unsupported Tekken13 config/pattern", path);
+        fail(error, error_size, "tokenizer open %s: config is not the Tekken v13 one this reader knows "
+            "(version, pattern or vocabulary sizes)", path);
         goto done;
     }
     const uint32_t vocab = j_field(&d, 1, "vocab"), specials = j_field(&d, 1, "special_tokens");
     if (!vocab || d.node[vocab].kind != '[') {
-        fail(error, error_size, "tokenizer: missing vocab array");
+        fail(error, error_size, "tokenizer open: the file has no vocab list");
         goto done;
     }
-    t = calloc(1, sizeof(*t));
+    t = lh_calloc(1, sizeof(*t));
     if (!t) {
-        fail(error, error_size, "tokenizer: allocation failed");
+        fail(error, error_size, "tokenizer open: out of memory");
         goto done;
     }
     if (!load_vocab(&d, vocab, t, error, error_size)) {
         goto done;
     }
     if (!specials || d.node[specials].kind != '[') {
-        fail(error, error_size, "tokenizer: missing special_tokens array");
+        fail(error, error_size, "tokenizer open: the file has no special_tokens list");
         goto done;
     }
     ok = check_specials(&d, specials, error, error_size);
@@ -869,7 +883,7 @@ static size_t piece_end(const tk_char *c, size_t n, size_t s)
 static tk_char *decode_text(const unsigned char *text, size_t length, size_t *count,
     size_t *bad_at)
 {
-    tk_char *chars = malloc((length + 1) * sizeof(*chars));
+    tk_char *chars = lh_malloc((length + 1) * sizeof(*chars));
     if (!chars) {
         *bad_at = (size_t)-1;
         return NULL;
@@ -879,7 +893,7 @@ static tk_char *decode_text(const unsigned char *text, size_t length, size_t *co
         unsigned cp;
         const size_t width = utf8_scalar(text + at, length - at, &cp);
         if (!width) {
-            free(chars);
+            lh_free(chars);
             *bad_at = at;
             return NULL;
         }
@@ -908,13 +922,13 @@ long lunelette_tokenizer_split(const unsigned char *text, size_t length, size_t 
     for (size_t s = 0; s < n;) {
         const size_t e = piece_end(chars, n, s);
         if (e <= s || e > n || (size_t)pieces == capacity) {
-            free(chars);
+            lh_free(chars);
             return -1;
         }
         ends[pieces++] = chars[e].offset;
         s = e;
     }
-    free(chars);
+    lh_free(chars);
     return pieces;
 }
 
@@ -978,10 +992,10 @@ static int merge_piece(const lunelette_tokenizer *t, const unsigned char *b, siz
     if (!n) {
         return 1;
     }
-    size_t *end = malloc(n * sizeof(*end)), *next = malloc(n * sizeof(*next));
-    size_t *prev = malloc(n * sizeof(*prev));
-    uint32_t *stamp = calloc(n, sizeof(*stamp));
-    merge_entry *heap = malloc(3 * n * sizeof(*heap));
+    size_t *end = lh_malloc(n * sizeof(*end)), *next = lh_malloc(n * sizeof(*next));
+    size_t *prev = lh_malloc(n * sizeof(*prev));
+    uint32_t *stamp = lh_calloc(n, sizeof(*stamp));
+    merge_entry *heap = lh_malloc(3 * n * sizeof(*heap));
     int ok = end && next && prev && stamp && heap;
     if (ok) {
         size_t queued = 0;
@@ -1029,11 +1043,11 @@ static int merge_piece(const lunelette_tokenizer *t, const unsigned char *b, siz
             out[(*count)++] = tk_find(t, b + i, end[i] - i) + TK_SPECIALS;
         }
     }
-    free(end);
-    free(next);
-    free(prev);
-    free(stamp);
-    free(heap);
+    lh_free(end);
+    lh_free(next);
+    lh_free(prev);
+    lh_free(stamp);
+    lh_free(heap);
     return ok;
 }
 
@@ -1059,17 +1073,17 @@ int lunelette_tokenizer_encode_with_limit(const lunelette_tokenizer *t,
     if (!t || !ids || !count || (!text && length) ||
         (input_limit != LUNELETTE_TOKENIZER_MAX_INPUT &&
          input_limit != LUNELETTE_TOKENIZER_LONG_INPUT) || length > input_limit) {
-        return fail(error, error_size, "tokenizer encode: invalid arguments or input exceeds "
+        return fail(error, error_size, "tokenizer encode: bad arguments, or the text is longer than "
             "%u bytes", input_limit == LUNELETTE_TOKENIZER_LONG_INPUT ?
             LUNELETTE_TOKENIZER_LONG_INPUT : LUNELETTE_TOKENIZER_MAX_INPUT);
     }
     size_t n, bad;
     tk_char *chars = decode_text(text, length, &n, &bad);
     if (!chars) {
-        return bad == (size_t)-1 ? fail(error, error_size, "tokenizer encode: allocation failed") :
+        return bad == (size_t)-1 ? fail(error, error_size, "tokenizer encode: out of memory") :
             fail(error, error_size, "tokenizer encode: invalid UTF-8 at byte %zu", bad);
     }
-    uint32_t *result = malloc((length ? length : 1) * sizeof(*result));
+    uint32_t *result = lh_malloc((length ? length : 1) * sizeof(*result));
     size_t produced = 0;
     int ok = result != NULL;
     for (size_t s = 0; ok && s < n;) {
@@ -1082,10 +1096,10 @@ int lunelette_tokenizer_encode_with_limit(const lunelette_tokenizer *t,
             &produced);
         s = e;
     }
-    free(chars);
+    lh_free(chars);
     if (!ok) {
-        free(result);
-        return fail(error, error_size, "tokenizer encode: allocation failed");
+        lh_free(result);
+        return fail(error, error_size, "tokenizer encode: out of memory");
     }
     *ids = result;
     *count = produced;
@@ -1102,24 +1116,24 @@ int lunelette_tokenizer_decode(const lunelette_tokenizer *t, const uint32_t *ids
         *length = 0;
     }
     if (!t || !bytes || !length || (!ids && count) || count > LUNELETTE_TOKENIZER_MAX_INPUT) {
-        return fail(error, error_size, "tokenizer decode: invalid arguments or more than 4096 IDs");
+        return fail(error, error_size, "tokenizer decode: bad arguments or more than 4096 ids");
     }
     size_t total = 0;
     for (size_t i = 0; i < count; i++) {
         if (ids[i] < TK_SPECIALS || ids[i] >= LUNELETTE_TOKENIZER_VOCAB_SIZE) {
-            return fail(error, error_size, "tokenizer decode: ID %u at %zu is special or out of "
-                "range", ids[i], i);
+            return fail(error, error_size, "tokenizer decode: id %u at %zu is a special token or "
+                "outside the vocabulary", ids[i], i);
         }
         const uint32_t r = ids[i] - TK_SPECIALS;
         const size_t n = t->start[r + 1] - t->start[r];
         if (n > TK_MAX_DECODE - total) {
-            return fail(error, error_size, "tokenizer decode: output exceeds 4 MiB");
+            return fail(error, error_size, "tokenizer decode: the text would pass 4 MiB");
         }
         total += n;
     }
-    unsigned char *result = malloc(total + 1);
+    unsigned char *result = lh_malloc(total + 1);
     if (!result) {
-        return fail(error, error_size, "tokenizer decode: allocation failed");
+        return fail(error, error_size, "tokenizer decode: out of memory");
     }
     size_t at = 0;
     for (size_t i = 0; i < count; i++) {

@@ -27,7 +27,7 @@ from lunelette_amd.session import LEGACY, MORE, REUSE_OFF, REUSE_ON, Session
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 CSRC = os.path.join(ROOT, "lunelette_amd", "csrc")
 SOURCES = [os.path.join(CSRC, "session.c"), os.path.join(CSRC, "generation.c"),
-           os.path.join(ROOT, "tests", "support", "stub_runtime.c")]
+           os.path.join(CSRC, "host_alloc.c"), os.path.join(ROOT, "tests", "support", "stub_runtime.c")]
 VOCAB = lh.VOCAB
 GREEDY = 22177   # the stub's tied maximum: the lower id wins
 

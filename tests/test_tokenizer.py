@@ -13,13 +13,15 @@ Oracles:
 Cases restated from tests/test_tokenizer.c:21-74 (JSON grammar and limits),
 :78-95 and :98-201 (round trips, limits, invalid UTF-8 and ids, the fixture's
 merges), tests/test_tokenizer.c:262-279 (defective files) and
-tests/test_chat.c:27-61. Allocation-failure injection
-(tests/test_tokenizer_alloc.c) needs a malloc hook in the library and is not
-restated.
+tests/test_chat.c:27-61. Allocation failure (tests/test_tokenizer_alloc.c)
+through the test library's host allocation seam, at every allocation of open,
+encode (32768 bytes), decode and chat framing rather than the first three.
 """
 import ctypes
 import os
 import random
+
+import numpy as np
 
 import pytest
 import regex
@@ -374,3 +376,69 @@ def test_unicode18_text_matches_reference_tokenizer(tmp_path, libraries):
     assert boundaries_differ > 100
     for _, t in opened:
         t.close()
+
+
+def each_allocation_failure(seams, attempt):
+    """Runs attempt() with the nth host allocation failing, n = 1, 2, ...,
+    until one run allocates no more than n - 1 times and succeeds. Every
+    failing run must free all it allocated. Returns the successful result and
+    the number of allocations it made."""
+    base = seams.lunelette_metal_test_live_host_allocations()
+    nth = 1
+    while True:
+        assert nth < 100000, "no run succeeded"
+        seams.lunelette_metal_test_fail_host_allocation(nth)
+        try:
+            result = attempt()
+        except ValueError as e:
+            assert "out of memory" in str(e), (nth, str(e))
+            assert seams.lunelette_metal_test_live_host_allocations() == base, nth
+            nth += 1
+            continue
+        finally:
+            made = seams.lunelette_metal_test_host_allocations()
+        seams.lunelette_metal_test_fail_host_allocation(0)
+        assert made == nth - 1, (made, nth)
+        return result, made
+
+
+def test_allocation_failures_clean_up(synthetic, libraries):
+    seams = lh.test_lib()
+    lh.declare_tokenizer(seams)
+    reference = dict(libraries).get("reference")
+    try:
+        tok, made = each_allocation_failure(seams, lambda: Tokenizer(synthetic, seams))
+        assert made >= 4
+        live = seams.lunelette_metal_test_live_host_allocations()
+        text = b"a" * LONG_INPUT    # the reference test's input
+        ids, made = each_allocation_failure(seams, lambda: tok.encode(text, limit=LONG_INPUT))
+        assert made >= 3
+        # The returned ids are counted until the caller frees them (with free).
+        assert seams.lunelette_metal_test_live_host_allocations() == live + 1
+        if reference is not None:
+            with Tokenizer(synthetic, reference) as ref:
+                assert ids == ref.encode(text, limit=LONG_INPUT)
+        mixed = "Grüße, 東京 — ok?\n\t 12345 " * 40
+        ids, _ = each_allocation_failure(seams, lambda: tok.encode(mixed))
+        raw, _ = each_allocation_failure(seams, lambda: tok.decode(ids))
+        assert raw == mixed.encode()
+        framed, _ = each_allocation_failure(seams, lambda: chat(seams, tok, mixed[:60]))
+        assert framed[0] == 1 and len(framed) > 20
+        with pytest.raises(ValueError, match="invalid UTF-8 at byte %d" % (LONG_INPUT - 1)):
+            tok.encode(text[:-1] + b"\x80", limit=LONG_INPUT)
+        tok.close()
+    finally:
+        seams.lunelette_metal_test_fail_host_allocation(0)
+
+
+def chat(library, tok, prompt):
+    """Ids of lunelette_chat_prompt; ValueError with its diagnostic."""
+    ids = np.full(256, -7, np.int64)
+    count = ctypes.c_size_t(999)
+    err = ctypes.create_string_buffer(512)
+    if library.lunelette_chat_prompt(tok.handle, prompt.encode(), None, 0,
+                                     ids.ctypes.data_as(lh.c_int64_p), ctypes.byref(count),
+                                     err, 512):
+        assert count.value == 999 and np.all(ids == -7)
+        raise ValueError(err.value.decode())
+    return ids[:count.value].tolist()
