@@ -11,6 +11,14 @@ if HERE not in sys.path:
     sys.path.insert(0, HERE)
 
 
+# A sanitized build of the library (tests/support/host_sanitize.py) in place
+# of the shipped and test builds, for the sanitizer run of the host tests.
+SANITIZED = os.environ.get("LH_SANITIZED_LIBRARY")
+if SANITIZED:
+    import lunelette_amd
+    lunelette_amd.LIBRARY = lunelette_amd.TEST_LIBRARY = SANITIZED
+
+
 def pytest_configure(config):
     # Temporary files (checkpoint containers) stay inside the repository tree.
     if not config.option.basetemp:

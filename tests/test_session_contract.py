@@ -35,9 +35,13 @@ GREEDY = 22177   # the stub's tied maximum: the lower id wins
 @pytest.fixture(scope="module")
 def stub_build(tmp_path_factory):
     out = str(tmp_path_factory.mktemp("session") / "libsession_stub.so")
+    sanitize = []
+    if os.environ.get("LH_SANITIZED_LIBRARY"):
+        from support import host_sanitize
+        sanitize = host_sanitize.FLAGS
     subprocess.run(["gcc", "-std=c11", "-O2", "-fPIC", "-shared", "-Wall", "-Wextra", "-Werror",
-                    "-I" + os.path.join(ROOT, "include"), "-I" + CSRC] + SOURCES + ["-o", out],
-                   check=True)
+                    "-I" + os.path.join(ROOT, "include"), "-I" + CSRC] + sanitize + SOURCES +
+                   ["-o", out], check=True)
     return out
 
 
