@@ -59,6 +59,12 @@ PREFILL_PLANES = {"qkv": (3, "3 x bf16 (exact split of fp32)"),
                   "o": (2, "2 x fp16 + per-(token, kv head) power-of-two scale (~22 bits)"),
                   "gate_up": (2, "2 x fp16 + per-token power-of-two scale (~22 bits)"),
                   "down": (2, "2 x fp16 + per-(token, K split) power-of-two scale (~22 bits)")}
+# Matrix-core prefill attention: operand formats of its two products.
+PREFILL_ATTENTION = {
+    "attention_qk": "Q and K as 2 x fp16 planes (power of two per (token, head) for Q, per "
+                    "position for K, ~22 bits); products ql.kh + qh.kl + qh.kh; fp32 accumulation",
+    "attention_pv": "P and V as 2 x bf16 planes truncated (16 bits); products pm.vh + ph.vm + "
+                    "ph.vh; fp32 accumulation"}
 # Algorithmic bytes per decode-step launch (weights + activations read/written).
 FP8_BYTES = {"qkv_rope": 6144 * 3072, "o_residual": 3072 * 4096,
              "gateup_silu": 2 * 9216 * 3072, "down_residual": 3072 * 9216}
@@ -359,20 +365,79 @@ def agreement(got, want):
     return next((i for i in range(n) if got[i] != want[i]), n)
 
 
-def precise_stream(lh, Runtime, seed, prompt, steps):
-    """Greedy ids of the bench workload on the bit-exact path: the 512-token
-    prompt prefilled in two 256-token chunks by PREFILL_CUSTOM (the decode
-    kernels with a token dimension), then steps - 1 decodes. Untimed."""
-    rt = Runtime(seed=seed, layers=26, context=4352, block=256, prefill=lh.PREFILL_CUSTOM,
+def lockstep_streams(lh, Runtime, seed, prompt, steps):
+    """The bench workload on the bit-exact path (the 512-token prompt
+    prefilled in two 256-token chunks by PREFILL_CUSTOM, the decode kernels
+    with a token dimension, then steps - 1 decodes) and, in lockstep with it,
+    on the matrix-core path fed the same ids. Returns the bit-exact path's
+    greedy ids and, over every call, the matrix-core path's largest logit
+    error as a fraction of the precise logits' range, its median, and the
+    calls whose greedy id differs (with the precise top-2 gap there as a
+    fraction of the range). Untimed."""
+    exact = Runtime(seed=seed, layers=26, context=4352, block=256, prefill=lh.PREFILL_CUSTOM,
+                    strategy=lh.COMPACT_FP8_ARITHMETIC)
+    mps = Runtime(seed=seed, layers=26, context=4352, block=256, prefill=lh.PREFILL_MPS,
+                  strategy=lh.COMPACT_FP8_ARITHMETIC)
+    try:
+        errors, flips = [], []
+
+        def compare(a, b, call):
+            span = float(a.max() - a.min())
+            errors.append(float(np.max(np.abs(b - a))) / span)
+            if exact.greedy() != mps.greedy():
+                top = np.partition(a, -2)[-2:]
+                flips.append({"call": call, "gap_over_range": float(top[1] - top[0]) / span})
+
+        exact.prefill(prompt[:256], copy=False)
+        mps.prefill(prompt[:256], copy=False)
+        compare(exact.append(prompt[256:]), mps.append(prompt[256:]), 0)
+        tokens = [exact.greedy()]
+        for call in range(1, steps):
+            a = exact.decode(tokens[-1])
+            compare(a, mps.decode(tokens[-1]), call)
+            tokens.append(exact.greedy())
+        worst = int(np.argmax(errors))
+        return tokens, {"calls": len(errors), "max_err_over_range": max(errors),
+                        "worst_call": worst,
+                        "median_err_over_range": float(np.median(errors)),
+                        "calls_over_1e-3": int(np.sum(np.array(errors) > 1e-3)),
+                        "greedy_differs": flips}
+    finally:
+        exact.close()
+        mps.close()
+
+
+def decode_near_capacity(lh, Runtime, seed, steps, prefill_mode):
+    """Decode at the metric's context: a seeded prompt of 4352 - steps tokens
+    prefilled in 256-token chunks (untimed), then `steps` greedy decode calls,
+    timed like `value`, whose positions end at 4351 (the last attends 4352
+    positions)."""
+    from lunelette_amd import synthetic as syn
+    length = 4352 - steps
+    prompt = syn.tokens(seed, 4, length)
+    rt = Runtime(seed=seed, layers=26, context=4352, block=256, prefill=prefill_mode,
                  strategy=lh.COMPACT_FP8_ARITHMETIC)
     try:
-        rt.prefill(prompt[:256], copy=False)
-        rt.append(prompt[256:], copy=False)
-        tokens = [rt.greedy()]
-        for _ in range(steps - 1):
-            rt.decode(tokens[-1], copy=False)
-            tokens.append(rt.greedy())
-        return tokens
+        for begin in range(0, length, 256):
+            ids = prompt[begin:begin + 256]
+            if begin == 0:
+                rt.prefill(ids, copy=False)
+            else:
+                rt.append(ids, copy=False)
+        token = rt.greedy()
+        lh.check(lh.lib().lh_device_synchronize())
+        device_ms = 0.0
+        t = time.perf_counter()
+        for _ in range(steps):
+            rt.decode(token, copy=False)
+            device_ms += rt.last_device_ms()
+            token = rt.greedy()
+        lh.check(lh.lib().lh_device_synchronize())
+        wall = time.perf_counter() - t
+        return {"decode_tok_s": round(steps / wall, 2),
+                "ms_per_step": round(wall * 1e3 / steps, 4),
+                "device_ms_per_step": round(device_ms / steps, 4),
+                "positions": [length, 4351], "prompt": length}
     finally:
         rt.close()
 
@@ -502,6 +567,8 @@ def cpu_baseline(syn, seed, budget_s=10.0):
 
     steps, many = run(share, 16)
     steps1, one = run(1, 4)
+    configs = cpu_configs(syn, seed, o, oracle_lib, layers, model, share)
+    configs["seconds_total"] = round(time.time() - t0, 1)
     return {"value": many, "unit": "tok/s", "cores": share,
             "kind": "port",
             "sample": "%d greedy decode steps of the 26-layer model at L=%d..%d on %d threads "
@@ -510,7 +577,60 @@ def cpu_baseline(syn, seed, budget_s=10.0):
                           steps, prefix + 1, prefix + steps, share,
                           os.environ.get("OMP_PROC_BIND"), steps1),
             "value_1thread": one, "host_cpus": START_AFFINITY, "online_cpus": os.cpu_count(),
-            "cpu_model": cpu_model()}
+            "cpu_model": cpu_model(), "configs": configs}
+
+
+def cpu_configs(syn, seed, o, oracle_lib, layers, model, share, budget_s=1.0):
+    """The oracle's reference-literal schedule on the other BASELINE configs,
+    each bounded to about budget_s of repeats: the FP8 linear 9216x3072 (1
+    thread and the host share), one decode layer at position 4351, one
+    256-token prefill layer after a 4096-token prefix, and one decode step of
+    the 26-layer model at L = 16001 (capacity 17920, KV prefix seeded)."""
+    def repeat(fn):
+        n, t = 0, time.time()
+        while n == 0 or time.time() - t < budget_s:
+            fn()
+            n += 1
+        return (time.time() - t) / n, n
+
+    out = {}
+    w = syn.fp8(seed, 500, 9216, 3072)
+    x = syn.normal_f32(seed, 501, 3072)
+    nbytes = 9216 * 3072 + 4 * (3072 + 9216)
+    lin = {}
+    for threads in (1, share):
+        o.orc_set_threads(threads)
+        sec, n = repeat(lambda: oracle_lib.matvec(oracle_lib.REF, 0, w, 0.0125, x, 9216, 3072))
+        lin["us_%dthreads" % threads] = round(sec * 1e6, 1)
+        lin["GBps_%dthreads" % threads] = round(nbytes / sec / 1e9, 2)
+    out["fp8_linear_9216x3072"] = lin
+    o.orc_set_threads(share)
+    one = oracle_lib.HostModel(np.zeros(1, np.uint16), np.zeros(1, np.uint16), [layers[0]], 4352)
+    one.keys[:] = model.keys[:one.keys.size]
+    one.values[:] = model.values[:one.values.size]
+    xd = syn.normal_f32(seed, 9001, 3072)
+    sec, n = repeat(lambda: one.layer_forward(oracle_lib.REF, 0, xd.copy(), 4351, 1))
+    out["decode_layer_pos4351"] = {"us": round(sec * 1e6, 1), "repeats": n,
+                                   "threads": share}
+    xp = syn.normal_f32(seed, 9202, 256 * 3072)
+    t = time.time()
+    one.layer_forward(oracle_lib.REF, 0, xp.copy(), 4096, 256)
+    sec = time.time() - t
+    out["prefill_layer_256_after_4096"] = {"s": round(sec, 3), "tok_s": round(256 / sec, 1),
+                                           "threads": share}
+    long = oracle_lib.HostModel(syn.embedding(seed).reshape(-1), syn.final_norm(seed), layers,
+                                17920)
+    per_layer = 8 * 17920 * 128
+    block = syn.normal_f32(seed, 9400, per_layer)
+    for i in range(26):
+        long.keys[i * per_layer:(i + 1) * per_layer] = block
+        long.values[i * per_layer:(i + 1) * per_layer] = block[::-1]
+    t = time.time()
+    long.forward(oracle_lib.REF, [7], 16000)
+    sec = time.time() - t
+    out["long_decode_L16001"] = {"tok_s": round(1 / sec, 3), "steps": 1, "threads": share}
+    del long
+    return out
 
 
 def main():
@@ -613,13 +733,24 @@ def main():
         # cache equal to the oracle's up to rounding (a near-tie can flip).
         want = fx["tokens_mirror"]
         n = min(len(tokens), len(want))
-        exact = precise_stream(lh, Runtime, args.seed, prompt, n)
+        exact, lockstep = lockstep_streams(lh, Runtime, args.seed, prompt, len(want))
         out["tokens_match_fixture"] = agreement(exact, want)
         out["tokens_match_fixture_mps_prefill"] = agreement(tokens, want)
         out["tokens_compared"] = n
+        out["tokens_compared_precise"] = len(want)
+        out["mps_vs_precise_logits"] = lockstep
         log("token stream: precise prefill %d/%d equal the oracle's, matrix-core prefill %d/%d"
-            % (out["tokens_match_fixture"], n, out["tokens_match_fixture_mps_prefill"], n))
-    out["config"]["prefill_activations"] = {k: v[1] for k, v in PREFILL_PLANES.items()}
+            % (out["tokens_match_fixture"], len(want), out["tokens_match_fixture_mps_prefill"], n))
+        log("matrix-core vs precise logits over %d calls: max %.3g, median %.3g of the range, "
+            "%d greedy differences" % (lockstep["calls"], lockstep["max_err_over_range"],
+                                       lockstep["median_err_over_range"],
+                                       len(lockstep["greedy_differs"])))
+    if args.steps < 4352:
+        out["decode_near_capacity"] = decode_near_capacity(lh, Runtime, args.seed, args.steps,
+                                                           prefill_mode)
+        log("decode near capacity: %s" % out["decode_near_capacity"])
+    out["config"]["prefill_activations"] = dict({k: v[1] for k, v in PREFILL_PLANES.items()},
+                                                **PREFILL_ATTENTION)
     if not args.no_operators:
         ops, floors = time_operators(lh, syn, args.seed, args.op_repeats)
         fp8_us = sum(ops[k] for k in FP8_BYTES)
