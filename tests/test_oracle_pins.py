@@ -181,3 +181,22 @@ def test_silu_schedules_close(oracle):
         for fn in (oracle.orc_silu_ref, oracle.orc_silu_mirror):
             assert abs(fn(float(v)) - exact) <= 2e-6 * max(1.0, abs(exact))
     assert oracle.orc_silu_mirror(-1e4) == 0.0 and math.copysign(1, oracle.orc_silu_mirror(-1e4)) < 0
+
+
+def test_schedule_envelope_fixture_consistent():
+    """tests/golden/schedule_envelope_c4352_26layer.json (the oracle's two
+    exact FP32 schedules in lockstep on the config-4 workload) belongs to the
+    stream fixture's workload: same seed and first ids, one entry per call,
+    and the reordering alone moves a few calls past 1e-3 of the logit range
+    while the median call stays near 1e-5."""
+    with open(os.path.join(GOLDEN, "schedule_envelope_c4352_26layer.json")) as f:
+        env = json.load(f)
+    with open(os.path.join(GOLDEN, "stream_c4352_26layer.json")) as f:
+        stream = json.load(f)
+    assert env["seed"] == stream["seed"] and env["calls"] == stream["decode"]
+    assert env["tokens_mirror_first"] == stream["tokens_mirror"][:8]
+    errors = np.array(env["err_over_range"])
+    assert errors.size == env["calls"] == len(env["gap_over_range"])
+    assert env["max_err_over_range"] == errors.max() and env["worst_call"] == errors.argmax()
+    assert env["calls_over_1e-3"] == int(np.sum(errors > 1e-3)) >= 1
+    assert env["median_err_over_range"] < 1e-4
