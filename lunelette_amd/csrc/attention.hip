@@ -918,6 +918,403 @@ k_attn_mfma(const float* __restrict__ q, const float* __restrict__ kcache,
     }
 }
 
+// The wide variant for long prefixes (k_attn_mfma_wide): 64-token
+// workgroups, each wave running two 16-token subtiles over every staged
+// block, so each block is split into planes once per 64 tokens. The two
+// passes' Q planes and O accumulators double the per-wave state; the raw
+// K/V tiles therefore come to LDS by direct loads (136 KiB of LDS) instead of
+// through registers, and each K and V fragment read from LDS feeds both
+// passes. Measured (attention + merge, 256 tokens): 88.5 against 95.8 us
+// after a 4096-token prefix, 148 against 170 us after 8192, 255 against 304
+// us after 16128; slower on short prefixes (28.6 against 22.5 us with no
+// prefix: half the workgroups) and for 64 tokens, where the launcher keeps
+// k_attn_mfma.
+constexpr uint32_t WIDE_PASSES = 2;                          // subtiles per wave
+constexpr uint32_t WIDE_WG = 2 * WIDE_PASSES * FA_TQ;        // tokens per workgroup
+constexpr uint32_t WIDE_MIN_LENGTH = 2048;                   // prefix from which it pays
+constexpr uint32_t WIDE_MIN_COUNT = 128;                     // tokens from which it pays
+
+__global__ void __launch_bounds__(512, 1)
+k_attn_mfma_wide(const float* __restrict__ q, const float* __restrict__ kcache,
+    const float* __restrict__ vcache, uint32_t length, uint32_t count, uint32_t capacity,
+    float* __restrict__ PM, float* __restrict__ PT, float* __restrict__ PA, float* __restrict__ out,
+    uint16_t* __restrict__ xs, uint32_t xs_tokens, float* __restrict__ xs_scale)
+{
+    __shared__ __attribute__((aligned(16))) uint8_t Kp[2 * FB_KPLANE];
+    __shared__ __attribute__((aligned(16))) uint8_t Vp[2 * FB_VPLANE];
+    __shared__ float sk[LH_ATTN_BLOCK];
+    const FaCoords fc = fa_coords((count + WIDE_WG - 1) / WIDE_WG);
+    const uint32_t tid = threadIdx.x, kvh = fc.kvh;
+    uint32_t lane = tid & 63, wave = tid >> 6;
+    uint32_t g = lane >> 4, l16 = lane & 15;
+    uint32_t head = kvh * 4 + (wave & 3);
+    // The workgroup's WIDE_WG tokens start at tw; wave w runs 16-token subtiles
+    // 2 pass + w / 4 in passes 0 and 1 over every staged block.
+    const uint32_t tw = fc.t0 * (WIDE_WG / FA_TQ);
+    const uint32_t last_wg = (tw + WIDE_WG < count ? tw + WIDE_WG : count) - 1;
+    // A subtile can lie past count: it then runs on the last real subtile's
+    // tokens (clamped) and stores nothing.
+    const uint32_t last_sub = (count - 1) / FA_TQ * FA_TQ;
+    uint32_t t0[WIDE_PASSES], last[WIDE_PASSES];
+    // The lane's token in pass ps (clamped to the subtile's last real token).
+    auto tq_of = [&](int ps) { return t0[ps] + l16 <= last[ps] ? t0[ps] + l16 : last[ps]; };
+    // Q operand of k-chunk kc (the B operand of S^T = K Q^T): lane (token
+    // l16, group g) holds dims 32 kc + 8g .. +7, as two FP16 planes of the
+    // row scaled by 2^eq (its largest magnitude into [2^14, 2^15)). fq =
+    // 2^-eq * log2(e) / sqrt(128) for the lane's token, whose S^T column the
+    // lane also holds.
+    fa_f16x8 qh[WIDE_PASSES][4], ql[WIDE_PASSES][4];
+    float fq[WIDE_PASSES];
+    // Online-softmax state of the lane's token (replicated over its four
+    // lane groups) and O^T tiles i: dims 16 i + 4g + r of the lane's token.
+    float m[WIDE_PASSES], l[WIDE_PASSES];
+    fa_floatx4 o[WIDE_PASSES][8];
+#pragma unroll
+    for (int ps = 0; ps < WIDE_PASSES; ps++) {
+        t0[ps] = tw + FA_TQ * (2 * ps + (wave >> 2));
+        const uint32_t t0c = t0[ps] < count ? t0[ps] : last_sub;
+        last[ps] = (t0c + FA_TQ < count ? t0c + FA_TQ : count) - 1;   // last real token
+        const uint32_t tq = t0[ps] + l16 <= last[ps] ? t0[ps] + l16 : last[ps];
+        const float4* src = reinterpret_cast<const float4*>(
+            q + (size_t)tq * LH_QUERY + head * LH_HEAD_DIM + 8 * g);
+        float4 a[4], b[4];
+        float mx = 0.0f;
+#pragma unroll
+        for (int kc = 0; kc < 4; kc++) {
+            a[kc] = src[8 * kc];
+            b[kc] = src[8 * kc + 1];
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(a[kc].x), fabsf(a[kc].y)),
+                                 fmaxf(fabsf(a[kc].z), fabsf(a[kc].w))));
+            mx = fmaxf(mx, fmaxf(fmaxf(fabsf(b[kc].x), fabsf(b[kc].y)),
+                                 fmaxf(fabsf(b[kc].z), fabsf(b[kc].w))));
+        }
+        const int eq = row_exponent(col4_max(mx));
+        const float f = exp2i(eq);
+        fq[ps] = exp2i(-eq) * FA_SCALE_LOG2;
+#pragma unroll
+        for (int kc = 0; kc < 4; kc++) {
+            uint2 h0, l0, h1, l1;
+            f16_planes4(a[kc], f, h0, l0);
+            f16_planes4(b[kc], f, h1, l1);
+            qh[ps][kc] = __builtin_bit_cast(fa_f16x8, fa_u32x4{h0.x, h0.y, h1.x, h1.y});
+            ql[ps][kc] = __builtin_bit_cast(fa_f16x8, fa_u32x4{l0.x, l0.y, l1.x, l1.y});
+        }
+        m[ps] = -__builtin_inff();
+        l[ps] = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            o[ps][i] = fa_floatx4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+    // The block range and the staging's visible rows follow the workgroup's
+    // last token (all subtiles share every barrier and every staged block).
+    const uint32_t nb = (length + last_wg + 1 + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
+    const uint32_t splits = fc.splits, z = fc.z;
+    const uint32_t per = (nb + splits - 1) / splits;
+    const uint32_t b_begin = z * per < nb ? z * per : nb;
+    const uint32_t b_end = b_begin + per < nb ? b_begin + per : nb;
+    const size_t head_base = lh_kv_index(capacity, 0, kvh, 0);
+    // Raw K and V of block b go to LDS by direct loads (the next block's
+    // issued once this block's staging has read them, in flight during its
+    // MFMAs): the tiles as they lie in the cache, K in lh_ktile_word order,
+    // V row-major. Wave w, load i copies the 1 KiB chunk 8i + w of each.
+    // V staging item j (0..7) of thread tid: lane l of wave w takes dim
+    // 16 (j % 8) + l % 16 and positions r0, r0 + 1 with r0 = 2 (4 w + l / 16),
+    // so the packed-pair writes of the transposed planes land on 64 distinct
+    // banks.
+    auto v_item = [&](int j, uint32_t& d, uint32_t& r0) {
+        d = 16 * j + (lane & 15);
+        r0 = 2 * (4 * wave + (lane >> 4));
+    };
+    // K: wave w takes positions 8w .. 8w+7 of the block; lane l holds
+    // position kp = 8w + (l % 32) / 4, quarter kq = l % 4, dims
+    // 32 kq + 4 (2i + l / 32) .. +3 for i = 0..3, so the eight lanes of a
+    // position hold all its 128 dims.
+    const uint32_t kp = 8 * wave + ((lane & 31) >> 2), kq = lane & 3, khalf = lane >> 5;
+    __shared__ __attribute__((aligned(16))) fa_floatx4 Kraw[LH_ATTN_BLOCK * LH_HEAD_DIM / 4];
+    __shared__ __attribute__((aligned(16))) fa_floatx4 Vraw[LH_ATTN_BLOCK * LH_HEAD_DIM / 4];
+    auto load_block = [&](uint32_t b) {
+        const fa_floatx4* kb = reinterpret_cast<const fa_floatx4*>(
+            kcache + head_base + (size_t)b * LH_ATTN_BLOCK * LH_HEAD_DIM);
+        const fa_floatx4* vb = reinterpret_cast<const fa_floatx4*>(
+            vcache + head_base + (size_t)b * LH_ATTN_BLOCK * LH_HEAD_DIM);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const uint32_t c = 8 * i + wave;
+            __builtin_amdgcn_global_load_lds(kb + 64 * c + lane, Kraw + 64 * c, 16, 0, 0);
+            __builtin_amdgcn_global_load_lds(vb + 64 * c + lane, Vraw + 64 * c, 16, 0, 0);
+        }
+    };
+    if (b_begin < b_end) {
+        load_block(b_begin);
+    }
+    // Rows past the tile's last visible position hold whatever an earlier
+    // sequence (or a failed step) left in the cache; they are staged as zeros
+    // (0 * Inf would be NaN in P.V).
+    const uint32_t visible = length + last_wg;
+    const fa_floatx4 zero = fa_floatx4{0.f, 0.f, 0.f, 0.f};
+    for (uint32_t b = b_begin; b < b_end; b++) {
+        // Block b's raw tiles have landed (each wave waits for its own direct
+        // loads) and the previous block's planes are consumed.
+        __builtin_amdgcn_s_waitcnt(0x0f70);
+        __syncthreads();
+        {
+            fa_floatx4 kr[4];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                kr[i] = Kraw[lh_ktile_word(kp, kq, 2 * i + khalf)];
+            }
+            // K: the position's largest magnitude over its eight lanes (a
+            // DPP quad, then the other 32-lane half), its power of two 2^ek
+            // (into [2^14, 2^15)), and the two FP16 planes; sk[p] = 2^-ek.
+            const bool kvis = b * LH_ATTN_BLOCK + kp <= visible;
+            float mx = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                kr[i] = kvis ? kr[i] : zero;
+                mx = fmaxf(mx, fmaxf(fmaxf(fabsf(kr[i].x), fabsf(kr[i].y)),
+                                     fmaxf(fabsf(kr[i].z), fabsf(kr[i].w))));
+            }
+            mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mx), 0xB1, 0xf,
+                0xf, false)));   // quad_perm [1,0,3,2]
+            mx = fmaxf(mx, __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(mx), 0x4E, 0xf,
+                0xf, false)));   // quad_perm [2,3,0,1]
+            const uint32_t mu = __float_as_uint(mx);
+            const auto p32 = __builtin_amdgcn_permlane32_swap(mu, mu, false, false);
+            const int ek = row_exponent(fmaxf(__uint_as_float(p32[0]), __uint_as_float(p32[1])));
+            if ((lane & 35) == 0) {
+                // The position again from the thread id (a register held for
+                // it across the loop would spill).
+                uint32_t t = threadIdx.x;
+                asm volatile("" : "+v"(t));
+                sk[8 * (t >> 6) + ((t & 31) >> 2)] = exp2i(-ek);
+            }
+            const float f = exp2i(ek);
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                uint2 h, lo;
+                f16_planes4(make_float4(kr[i].x, kr[i].y, kr[i].z, kr[i].w), f, h, lo);
+                const uint32_t at = fb_k_at(kp, 32 * kq + 4 * (2 * i + khalf));
+                *reinterpret_cast<uint2*>(Kp + at) = h;
+                *reinterpret_cast<uint2*>(Kp + FB_KPLANE + at) = lo;
+            }
+        }
+        const float* vf = reinterpret_cast<const float*>(Vraw);
+#pragma unroll
+        for (int j = 0; j < 8; j++) {
+            uint32_t d, r0;
+            v_item(j, d, r0);
+            const float v0 = b * LH_ATTN_BLOCK + r0 <= visible ? vf[r0 * LH_HEAD_DIM + d] : 0.0f;
+            const float v1 = b * LH_ATTN_BLOCK + r0 + 1 <= visible ?
+                vf[(r0 + 1) * LH_HEAD_DIM + d] : 0.0f;
+            uint32_t h0, m0, h1, m1;
+            fb_split2(v0, h0, m0);
+            fb_split2(v1, h1, m1);
+            const uint32_t at = fb_v_at(d, r0);
+            *reinterpret_cast<uint32_t*>(Vp + at) = h0 | (h1 << 16);
+            *reinterpret_cast<uint32_t*>(Vp + FB_VPLANE + at) = m0 | (m1 << 16);
+        }
+        __syncthreads();
+        if (b + 1 < b_end) {
+            load_block(b + 1);   // in flight during this block's MFMAs
+        }
+        // S^T tiles j = 0..3 of each pass: rows positions 16j + 4g + r,
+        // columns tokens l16 (A operand K: row 16j + l16, dims 32kc + 8g ..
+        // +7, read once for both passes).
+        fa_floatx4 s[WIDE_PASSES][4];
+#pragma unroll
+        for (int ps = 0; ps < WIDE_PASSES; ps++) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                s[ps][j] = zero;
+            }
+        }
+#pragma unroll
+        for (int kc = 0; kc < 4; kc++) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const uint32_t at = fb_k_at(16 * j + l16, 32 * kc + 8 * g);
+                const fa_f16x8 kh = *reinterpret_cast<const fa_f16x8*>(Kp + at);
+                const fa_f16x8 kl = *reinterpret_cast<const fa_f16x8*>(Kp + FB_KPLANE + at);
+#pragma unroll
+                for (int ps = 0; ps < WIDE_PASSES; ps++) {
+                    s[ps][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kl, qh[ps][kc], s[ps][j], 0, 0, 0);
+                    s[ps][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, ql[ps][kc], s[ps][j], 0, 0, 0);
+                    s[ps][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kh, qh[ps][kc], s[ps][j], 0, 0, 0);
+                }
+            }
+        }
+        // Scale (2^-ek of the row's position, fq of the token), causal mask,
+        // online softmax of the lane's token over its 16 values and its three
+        // other lane groups; P^T as the PV B operand of position chunk pc:
+        // k slots 0..3 = positions 32 pc + 4g + r (tile j = 2 pc), slots 4..7
+        // = 32 pc + 16 + 4g + r (tile j = 2 pc + 1).
+        fa_bf16x8 ph[WIDE_PASSES][2], pm[WIDE_PASSES][2];
+#pragma unroll
+        for (int ps = 0; ps < WIDE_PASSES; ps++) {
+            // The scaled, masked scores in place (s[ps] holds them from here).
+            float mx = -__builtin_inff();
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const fa_floatx4 fk = *reinterpret_cast<const fa_floatx4*>(sk + 16 * j + 4 * g);
+#pragma unroll
+                for (int r = 0; r < 4; r++) {
+                    const uint32_t p = b * LH_ATTN_BLOCK + 16 * j + 4 * g + r;
+                    const float x = p <= length + tq_of(ps) ? s[ps][j][r] * fk[r] * fq[ps] :
+                        -__builtin_inff();
+                    s[ps][j][r] = x;
+                    mx = fmaxf(mx, x);
+                }
+            }
+            mx = col4_max(mx);
+            // A split can start past a token's last visible position: keep
+            // its row empty (no exp of -inf - -inf).
+            const float m_new = fmaxf(m[ps], mx);
+            const bool empty = m_new == -__builtin_inff();
+            const float alpha = empty ? 1.0f : __builtin_amdgcn_exp2f(m[ps] - m_new);
+            float sum = 0.0f;
+#pragma unroll
+            for (int pc = 0; pc < 2; pc++) {
+                fa_u32x4 hi, mid;
+#pragma unroll
+                for (int k = 0; k < 8; k += 2) {
+                    const float x0 = s[ps][2 * pc + k / 4][k % 4];
+                    const float x1 = s[ps][2 * pc + (k + 1) / 4][(k + 1) % 4];
+                    const float e0 = empty ? 0.0f : __builtin_amdgcn_exp2f(x0 - m_new);
+                    const float e1 = empty ? 0.0f : __builtin_amdgcn_exp2f(x1 - m_new);
+                    sum = sum + e0;
+                    sum = sum + e1;
+                    uint32_t h0, m0, h1, m1;
+                    fb_split2(e0, h0, m0);
+                    fb_split2(e1, h1, m1);
+                    hi[k / 2] = h0 | (h1 << 16);
+                    mid[k / 2] = m0 | (m1 << 16);
+                }
+                ph[ps][pc] = __builtin_bit_cast(fa_bf16x8, hi);
+                pm[ps][pc] = __builtin_bit_cast(fa_bf16x8, mid);
+            }
+            l[ps] = l[ps] * alpha + col4_sum(sum);
+            m[ps] = m_new;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                o[ps][i] = o[ps][i] * alpha;
+            }
+        }
+        // O^T += V^T P^T: A operand of dim tile i: lane (dim 16 i + l16, group
+        // g) holds V at positions 32 pc + 4g .. +3 and 32 pc + 16 + 4g .. +3
+        // (two 8-byte reads per plane, read once for both passes), the slots
+        // of P^T above.
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+            const uint32_t d = 16 * i + l16;
+#pragma unroll
+            for (int pc = 0; pc < 2; pc++) {
+                const uint32_t a0 = fb_v_at(d, 32 * pc + 4 * g);
+                const uint32_t a1 = fb_v_at(d, 32 * pc + 16 + 4 * g);
+                const uint2 h0 = *reinterpret_cast<const uint2*>(Vp + a0);
+                const uint2 h1 = *reinterpret_cast<const uint2*>(Vp + a1);
+                const uint2 m0 = *reinterpret_cast<const uint2*>(Vp + FB_VPLANE + a0);
+                const uint2 m1 = *reinterpret_cast<const uint2*>(Vp + FB_VPLANE + a1);
+                const fa_bf16x8 vh = __builtin_bit_cast(fa_bf16x8, fa_u32x4{h0.x, h0.y, h1.x, h1.y});
+                const fa_bf16x8 vm = __builtin_bit_cast(fa_bf16x8, fa_u32x4{m0.x, m0.y, m1.x, m1.y});
+#pragma unroll
+                for (int ps = 0; ps < WIDE_PASSES; ps++) {
+                    o[ps][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vm, ph[ps][pc], o[ps][i], 0, 0, 0);
+                    o[ps][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, pm[ps][pc], o[ps][i], 0, 0, 0);
+                    o[ps][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(vh, ph[ps][pc], o[ps][i], 0, 0, 0);
+                }
+            }
+        }
+    }
+    // Output planes (one split): each token's four query heads of this kv
+    // head (512 columns, one K split of the o projection) share one power of
+    // two 2^e, their largest magnitude into [2^14, 2^15), before the split
+    // into two FP16 planes; xs_scale[t][kv head] = 2^-e. The heads' maxima
+    // meet in LDS before any wave leaves.
+    // The lane's coordinates again (held across the block loop they would
+    // spill: the loop needs every register).
+    {
+        uint32_t tid_e = threadIdx.x;
+        asm volatile("" : "+v"(tid_e));
+        lane = tid_e & 63;
+        g = lane >> 4;
+        l16 = lane & 15;
+        const uint32_t wave_e = __builtin_amdgcn_readfirstlane(tid_e >> 6);
+#pragma unroll
+        for (int ps = 0; ps < WIDE_PASSES; ps++) {
+            t0[ps] = tw + FA_TQ * (2 * ps + (wave_e >> 2));
+            const uint32_t t0c = t0[ps] < count ? t0[ps] : last_sub;
+            last[ps] = (t0c + FA_TQ < count ? t0c + FA_TQ : count) - 1;
+        }
+        head = kvh * 4 + (wave_e & 3);
+        wave = wave_e;
+    }
+    __shared__ float gmax[WIDE_WG][4];
+    if (splits == 1 && xs) {
+#pragma unroll
+        for (int ps = 0; ps < WIDE_PASSES; ps++) {
+            float mr = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                mr = fmaxf(mr, fmaxf(fmaxf(fabsf(o[ps][i].x), fabsf(o[ps][i].y)),
+                                     fmaxf(fabsf(o[ps][i].z), fabsf(o[ps][i].w))));
+            }
+            mr = col4_max(mr) / l[ps];
+            if (g == 0) {
+                gmax[t0[ps] - tw + l16][wave & 3] = mr;
+            }
+        }
+        __syncthreads();
+    }
+    // The lane's token and its O^T values: dims 16 i + 4g .. +3.
+    const uint32_t nbc = capacity / LH_ATTN_BLOCK;
+#pragma unroll
+    for (int ps = 0; ps < WIDE_PASSES; ps++) {
+        const uint32_t t = t0[ps] + l16;
+        if (t0[ps] >= count || t > last[ps]) {
+            continue;
+        }
+        if (splits == 1) {
+            const float inv = 1.0f / l[ps];
+            if (xs) {
+                const float* gm = gmax[t0[ps] - tw + l16];
+                const int e = row_exponent(fmaxf(fmaxf(gm[0], gm[1]), fmaxf(gm[2], gm[3])));
+                if (g == 0 && (wave & 3) == 0) {
+                    xs_scale[t * LH_KV_HEADS + kvh] = exp2i(-e);
+                }
+                const float f = exp2i(e);
+                const size_t plane = (size_t)xs_tokens * LH_QUERY;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const fa_floatx4 v = o[ps][i] * (inv * f);
+                    store_f16x2_4(xs, plane,
+                        xs_at(t, head * LH_HEAD_DIM + 16 * i + 4 * g, LH_QUERY),
+                        make_float4(v.x, v.y, v.z, v.w));
+                }
+            } else {
+                float* dst = out + (size_t)t * LH_QUERY + head * LH_HEAD_DIM + 4 * g;
+#pragma unroll
+                for (int i = 0; i < 8; i++) {
+                    const fa_floatx4 v = o[ps][i] * inv;
+                    *reinterpret_cast<float4*>(dst + 16 * i) = make_float4(v.x, v.y, v.z, v.w);
+                }
+            }
+        } else {
+            const size_t part = ((size_t)t * LH_HEADS + head) * nbc + z;
+            if (g == 0) {
+                PM[part] = m[ps];
+                PT[part] = l[ps];
+            }
+            float* dst = PA + part * LH_HEAD_DIM + 4 * g;
+#pragma unroll
+            for (int i = 0; i < 8; i++) {
+                *reinterpret_cast<float4*>(dst + 16 * i) =
+                    make_float4(o[ps][i].x, o[ps][i].y, o[ps][i].z, o[ps][i].w);
+            }
+        }
+    }
+}
+
 // Merge of k_attn_mfma's KV splits (tolerance path): per (token, head)
 // M = max m_z, f_z = exp2(m_z - M) (base-2 maxima), out = (sum f_z O_z) / (sum f_z l_z) with
 // the sums in split order. A split whose positions are all masked for the row
@@ -1005,15 +1402,23 @@ extern "C" int lh_launch_attention_mfma(const float* q, const float* kcache_laye
     // per block of the longest tile (a 256-token chunk with no prefix runs 4
     // splits of one block: measured 2.7 us per layer faster than 2 splits of
     // two blocks, the merge included).
-    const uint32_t tiles = (count + 2 * lh::FA_TQ - 1) / (2 * lh::FA_TQ);
+    const bool wide = length >= lh::WIDE_MIN_LENGTH && count >= lh::WIDE_MIN_COUNT;
+    const uint32_t per_wg = wide ? lh::WIDE_WG : 2 * lh::FA_TQ;
+    const uint32_t tiles = (count + per_wg - 1) / per_wg;
     const uint32_t nb = (length + count + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
     uint32_t splits = 256 / (tiles * LH_KV_HEADS);
     const uint32_t by_length = nb;
     splits = splits < by_length ? splits : by_length;
     splits = splits ? splits : 1;
-    hipLaunchKernelGGL(lh::k_attn_mfma, dim3(tiles * LH_KV_HEADS * splits), dim3(512), 0, s,
-        q, kcache_layer, vcache_layer, length, count, capacity, PM, PT, PA, out, xs, xs_tokens,
-        xs_scale);
+    if (wide) {
+        hipLaunchKernelGGL(lh::k_attn_mfma_wide, dim3(tiles * LH_KV_HEADS * splits), dim3(512), 0,
+            s, q, kcache_layer, vcache_layer, length, count, capacity, PM, PT, PA, out, xs,
+            xs_tokens, xs_scale);
+    } else {
+        hipLaunchKernelGGL(lh::k_attn_mfma, dim3(tiles * LH_KV_HEADS * splits), dim3(512), 0, s,
+            q, kcache_layer, vcache_layer, length, count, capacity, PM, PT, PA, out, xs,
+            xs_tokens, xs_scale);
+    }
     if (splits > 1) {
         hipLaunchKernelGGL(lh::k_attn_merge, dim3(count * LH_HEADS / 4), dim3(256), 0, s, PM, PT,
             PA, capacity, splits, count, out, xs, xs_tokens, xs_scale);
