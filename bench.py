@@ -8,11 +8,16 @@ greedy decode runs for --steps tokens; a step is one decode call (all layers,
 the head, the 512 KiB of logits reaching host memory and host greedy
 selection). value = decode tokens/s; prefill tokens/s (the median of 5 timed
 512-token prefills from an empty cache) is reported beside it.
-After the timed calls the same workload runs untimed on the bit-exact path
-(precise prefill, then the same decode kernels), and its ids are compared with
-the oracle's token fixture (tokens_match_fixture = how many lead in
-agreement); tokens_match_fixture_mps_prefill compares the timed stream, whose
-matrix-core prefill leaves a KV cache equal to the oracle's up to rounding.
+After the timed calls the fixture's workload (1024 calls) runs untimed on the
+bit-exact path (precise prefill, then the same decode kernels) and, in
+lockstep with it and fed the same ids, on the matrix-core path: the bit-exact
+ids are compared with the oracle's token fixture (tokens_match_fixture = how
+many lead in agreement), and mps_vs_precise_logits gives the matrix-core
+path's logit error per call as a fraction of the logit range;
+tokens_match_fixture_mps_prefill compares the timed stream, whose matrix-core
+prefill leaves a KV cache equal to the oracle's up to rounding. Then decode at
+the metric's context: a 4352 - steps token prompt, then --steps timed decode
+calls ending at position 4351 (decode_near_capacity).
 
 Also measured, with HIP events on the stream the kernels run on:
 - each fused decode operator at position 4351 launched over 26 distinct layer
@@ -25,10 +30,11 @@ Also measured, with HIP events on the stream the kernels run on:
   prompt, 8 turns of restore + append 64 + decode 128), with its ids compared
   with the oracle's long fixture;
 - the CPU baseline: the oracle's reference-literal schedule on the host cores
-  over a bounded decode sample, with the host share of threads and with one.
+  over a bounded decode sample, with the host share of threads and with one,
+  and bounded samples of the other configurations (cpu_baseline.configs).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu-baseline]
-       [--no-operators] [--no-long]
+       [--no-operators] [--no-long] [--no-streams]
 """
 import argparse
 import ctypes
@@ -105,6 +111,10 @@ def parse():
     p.add_argument("--op-repeats", type=int, default=4)
     p.add_argument("--no-long", action="store_true",
                    help="skip the long-context prefix-reuse workload (about 10 s)")
+    p.add_argument("--no-streams", action="store_true",
+                   help="skip the untimed token-stream checks (the bit-exact and matrix-core "
+                        "paths in lockstep over the fixture's 1024 calls) and the decode near "
+                        "capacity, for profiler runs of the timed workload")
     return p.parse_args()
 
 
@@ -726,7 +736,7 @@ def main():
         "first_tokens": tokens[:8],
     }
     fx = fixture_tokens("stream_c4352_26layer.json")
-    if fx is not None and fx["seed"] == args.seed and args.prefill == "mps":
+    if fx is not None and fx["seed"] == args.seed and args.prefill == "mps" and not args.no_streams:
         # Token identity, after the timed region: the bit-exact path (precise
         # prefill, then the same decode kernels) against the oracle's stream,
         # and the timed stream itself, whose matrix-core prefill leaves a KV
@@ -745,7 +755,7 @@ def main():
             "%d greedy differences" % (lockstep["calls"], lockstep["max_err_over_range"],
                                        lockstep["median_err_over_range"],
                                        len(lockstep["greedy_differs"])))
-    if args.steps < 4352:
+    if args.steps < 4352 and not args.no_streams:
         out["decode_near_capacity"] = decode_near_capacity(lh, Runtime, args.seed, args.steps,
                                                            prefill_mode)
         log("decode near capacity: %s" % out["decode_near_capacity"])
