@@ -1320,7 +1320,11 @@ k_attn_mfma_wide(const float* __restrict__ q, const float* __restrict__ kcache,
 // the sums in split order. A split whose positions are all masked for the row
 // holds m = -inf, l = 0, O = 0 and contributes nothing; split 0 always holds
 // position 0, so M is finite. grid (count * 8), block 256: one wave per
-// (token, head), lane l owns dims 2l and 2l + 1.
+// (token, head), lane l owns dims 2l and 2l + 1. Every split's m, l and O
+// words are requested before the first is used (index clamped to the last
+// split, so MAXP >= parts loads stay in bounds): one memory round trip, where
+// a loop over a run-time split count waited for each split's loads in turn.
+template <uint32_t MAXP>
 __global__ void __launch_bounds__(256)
 k_attn_merge(const float* __restrict__ PM, const float* __restrict__ PT,
     const float* __restrict__ PA, uint32_t capacity, uint32_t parts, uint32_t count,
@@ -1345,18 +1349,32 @@ k_attn_merge(const float* __restrict__ PM, const float* __restrict__ PT,
     const float* pm = PM + (size_t)th * nbc;
     const float* pt = PT + (size_t)th * nbc;
     const float2* pa = reinterpret_cast<const float2*>(PA + (size_t)th * nbc * LH_HEAD_DIM) + lane;
+    float mz[MAXP], tz[MAXP];
+    float2 az[MAXP];
+#pragma unroll
+    for (uint32_t z = 0; z < MAXP; z++) {
+        const uint32_t c = z < parts ? z : parts - 1;
+        mz[z] = pm[c];
+        tz[z] = pt[c];
+        az[z] = pa[(size_t)c * (LH_HEAD_DIM / 2)];
+    }
     float M = -__builtin_inff();
-    for (uint32_t z = 0; z < parts; z++) {
-        M = fmaxf(M, pm[z]);
+#pragma unroll
+    for (uint32_t z = 0; z < MAXP; z++) {
+        if (z < parts) {
+            M = fmaxf(M, mz[z]);
+        }
     }
     float2 A = make_float2(0.0f, 0.0f);
     float T = 0.0f;
-    for (uint32_t z = 0; z < parts; z++) {
-        const float f = __builtin_amdgcn_exp2f(pm[z] - M);
-        const float2 a = pa[(size_t)z * (LH_HEAD_DIM / 2)];
-        A.x = __builtin_fmaf(f, a.x, A.x);
-        A.y = __builtin_fmaf(f, a.y, A.y);
-        T = __builtin_fmaf(f, pt[z], T);
+#pragma unroll
+    for (uint32_t z = 0; z < MAXP; z++) {
+        if (z < parts) {
+            const float f = __builtin_amdgcn_exp2f(mz[z] - M);
+            A.x = __builtin_fmaf(f, az[z].x, A.x);
+            A.y = __builtin_fmaf(f, az[z].y, A.y);
+            T = __builtin_fmaf(f, tz[z], T);
+        }
     }
     const uint32_t t = th / LH_HEADS, h = th % LH_HEADS;
     const size_t at = (size_t)t * LH_QUERY + h * LH_HEAD_DIM + 2 * lane;
@@ -1420,8 +1438,21 @@ extern "C" int lh_launch_attention_mfma(const float* q, const float* kcache_laye
             xs_tokens, xs_scale);
     }
     if (splits > 1) {
-        hipLaunchKernelGGL(lh::k_attn_merge, dim3(count * LH_HEADS / 4), dim3(256), 0, s, PM, PT,
-            PA, capacity, splits, count, out, xs, xs_tokens, xs_scale);
+        static_assert(256 / LH_KV_HEADS <= 32, "at most 32 splits");
+        const dim3 grid(count * LH_HEADS / 4);
+        if (splits <= 4) {
+            hipLaunchKernelGGL(lh::k_attn_merge<4>, grid, dim3(256), 0, s, PM, PT, PA, capacity,
+                splits, count, out, xs, xs_tokens, xs_scale);
+        } else if (splits <= 8) {
+            hipLaunchKernelGGL(lh::k_attn_merge<8>, grid, dim3(256), 0, s, PM, PT, PA, capacity,
+                splits, count, out, xs, xs_tokens, xs_scale);
+        } else if (splits <= 16) {
+            hipLaunchKernelGGL(lh::k_attn_merge<16>, grid, dim3(256), 0, s, PM, PT, PA, capacity,
+                splits, count, out, xs, xs_tokens, xs_scale);
+        } else {
+            hipLaunchKernelGGL(lh::k_attn_merge<32>, grid, dim3(256), 0, s, PM, PT, PA, capacity,
+                splits, count, out, xs, xs_tokens, xs_scale);
+        }
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
