@@ -139,11 +139,14 @@ def test_runtime_mps_prefill_then_decode(gpu, prompt):
 @pytest.mark.parametrize("length,count,capacity", [(0, 5, 256), (60, 3, 256), (0, 256, 256),
                                                    (256, 256, 4352), (1000, 17, 4352),
                                                    (4096, 256, 4352), (2048, 128, 4352),
-                                                   (2048, 130, 4352), (3001, 211, 4352)])
+                                                   (2048, 130, 4352), (3001, 211, 4352),
+                                                   (2000, 20, 4352)])
 def test_attention_mfma_vs_oracle(gpu, length, count, capacity):
     """From a 2048-token prefix and 128 tokens on, the wide kernel runs (64
     tokens per workgroup); 130 and 211 tokens leave subtiles past the last
-    token, and 2048 + 128 is the smallest such launch."""
+    token, and 2048 + 128 is the smallest such launch. The merge runs with
+    4 (256 tokens), 8 (the wide kernel at 256), 10 and 16 (1000 + 17) and 32
+    (2000 + 20) KV splits."""
     rng = np.random.default_rng(length + 7 * count)
     total = length + count
     q = (rng.normal(size=count * 4096) * 3).astype(np.float32)
