@@ -193,3 +193,23 @@ def test_attention_random_bitwise_and_tolerance(gpu):
         ref = oracle_lib.attention(REF, q, kpm.reshape(-1), vpm.reshape(-1), 128, 1024,
                                    length, count)
         assert np.max(np.abs(got - ref)) < 1e-4
+
+
+def test_attention_seeded_lengths_bitwise(gpu):
+    """Seeded random decode and small-chunk shapes across the whole 17920
+    capacity: partial last blocks at every offset, one to three combine
+    rounds (256 blocks each), bitwise the mirror schedule."""
+    rng = np.random.default_rng(20251202)
+    capacity = 17920
+    cases = [(int(rng.integers(0, capacity - 8)), int(rng.choice([1, 1, 1, 2, 5])))
+             for _ in range(20)]
+    cases += [(16383, 2), (16447, 1), (17900, 3)]
+    for length, count in cases:
+        total = length + count
+        q = (rng.normal(size=count * 4096) * 3).astype(np.float32)
+        kpm = rng.normal(size=(total, 1024)).astype(np.float32)
+        vpm = rng.normal(size=(total, 1024)).astype(np.float32)
+        got = attention_on_device(gpu, q, kpm, vpm, length, count, capacity)
+        mirror = oracle_lib.attention(MIRROR, q, kpm.reshape(-1), vpm.reshape(-1), 128, 1024,
+                                      length, count)
+        assert np.array_equal(bits(got), bits(mirror)), (length, count)
