@@ -268,3 +268,29 @@ def test_attention_ignores_stale_cache_rows(gpu, tail, length, count, capacity):
                                        capacity, tail=tail)
     assert np.all(np.isfinite(got))
     assert np.max(np.abs(got - clean)) < 2e-4
+
+
+def test_attention_mfma_seeded_shapes(gpu):
+    """Seeded random (prefix, chunk) shapes: both kernels (32-token tiles, and
+    64-token tiles from a 2048-token prefix and 128 tokens on), 1 to 32 KV
+    splits with ragged last splits, ragged token tiles; within 2e-4 of the
+    mirror."""
+    rng = np.random.default_rng(20251203)
+    capacity = 4352
+    for i in range(16):
+        if i % 2:   # the wide kernel's range
+            count = int(rng.integers(128, 161))
+            length = int(rng.integers(2048, capacity - count + 1))
+        else:
+            count = int(rng.integers(1, 161))
+            length = int(rng.integers(0, capacity - count + 1))
+        total = length + count
+        q = (rng.normal(size=count * 4096) * 3).astype(np.float32)
+        kpm = rng.normal(size=(total, 1024)).astype(np.float32)
+        vpm = rng.normal(size=(total, 1024)).astype(np.float32)
+        got = gpu_util.attention_on_device(gpu, gpu.lh_attention_mfma, q, kpm, vpm, length, count,
+                                           capacity)
+        mirror = oracle_lib.attention(MIRROR, q, kpm.reshape(-1), vpm.reshape(-1), 128, 1024,
+                                      length, count)
+        assert np.all(np.isfinite(got)), (length, count)
+        assert np.max(np.abs(got - mirror)) < 2e-4, (length, count)
