@@ -294,3 +294,25 @@ def test_attention_mfma_seeded_shapes(gpu):
                                       length, count)
         assert np.all(np.isfinite(got)), (length, count)
         assert np.max(np.abs(got - mirror)) < 2e-4, (length, count)
+
+
+def test_mfma_layer_seeded_shapes(gpu):
+    """Seeded random prefixes and chunk sizes through the whole matrix-core
+    layer (ragged 64-token tiles, every stream-K partition of gate|up and
+    down that those counts produce, short and long prefixes), within 1e-3 of
+    each row's largest magnitude of the mirror schedule."""
+    from test_gpu_layer import oracle_layer, run_layer
+    host = syn.layer(SEED, 2)
+    rng = np.random.default_rng(20251204)
+    capacity = 4352
+    for i in range(12):
+        count = int(rng.integers(2, 257))
+        length = int(rng.integers(0, capacity - count + 1))
+        x = syn.normal_f32(SEED, 9200 + i, count * 3072)
+        kpm = rng.normal(size=(length, 1024)).astype(np.float32)
+        vpm = rng.normal(size=(length, 1024)).astype(np.float32)
+        got = run_layer(gpu, host, x, kpm, vpm, length, count, capacity, lh.PATH_MFMA)
+        want = oracle_layer(host, x, kpm, vpm, length, count, capacity, MIRROR)
+        gx, wx = got[0].reshape(count, 3072), want[0].reshape(count, 3072)
+        err = np.max(np.abs(gx - wx) / np.max(np.abs(wx), axis=1, keepdims=True))
+        assert err < 1e-3, (length, count, err)
