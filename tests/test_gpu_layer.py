@@ -213,3 +213,11 @@ def test_attention_seeded_lengths_bitwise(gpu):
         mirror = oracle_lib.attention(MIRROR, q, kpm.reshape(-1), vpm.reshape(-1), 128, 1024,
                                       length, count)
         assert np.array_equal(bits(got), bits(mirror)), (length, count)
+
+
+def test_decode_layer_seeded_lengths(gpu, layer_host):
+    """Seeded random positions across the 17920 capacity (the query factor
+    above 16384 included), fused and lookup paths bitwise the mirror."""
+    rng = np.random.default_rng(20251205)
+    for length in [int(v) for v in rng.integers(0, 17919, size=8)]:
+        check_layer(gpu, layer_host, length, 1, 17920, [lh.PATH_FUSED, lh.PATH_LOOKUP])
