@@ -934,13 +934,17 @@ int lunelette_metal_read_kv(const lunelette_metal *context, size_t layer, int ki
     const float *base = (kind ? rt->d_values : rt->d_keys) + (size_t)layer * LH_KV_HEADS * C *
         LH_HEAD_DIM;
     if (kind) {
-        for (size_t p = 0; p < count; p++) {
-            for (size_t h = 0; h < LH_KV_HEADS; h++) {
-                const float *src = base + lh_kv_index(C, 0, (uint32_t)h, position + p);
-                if (hipMemcpy(out + p * LH_KV + h * LH_HEAD_DIM, src, LH_HEAD_DIM * sizeof(float),
-                        hipMemcpyDeviceToHost) != hipSuccess) {
-                    return -1;
-                }
+        /* V rows are contiguous per kv head: one strided copy per head into
+         * the position-major output. */
+        if (!count) {
+            return 0;
+        }
+        for (size_t h = 0; h < LH_KV_HEADS; h++) {
+            const float *src = base + lh_kv_index(C, 0, (uint32_t)h, position);
+            if (hipMemcpy2D(out + h * LH_HEAD_DIM, LH_KV * sizeof(float), src,
+                    LH_HEAD_DIM * sizeof(float), LH_HEAD_DIM * sizeof(float), count,
+                    hipMemcpyDeviceToHost) != hipSuccess) {
+                return -1;
             }
         }
         return 0;
