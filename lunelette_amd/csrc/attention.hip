@@ -1019,11 +1019,15 @@ k_attn_mfma_wide(const float* __restrict__ q, const float* __restrict__ kcache,
     // MFMAs): the tiles as they lie in the cache, K in lh_ktile_word order,
     // V row-major. Wave w, load i copies the 1 KiB chunk 8i + w of each.
     // V staging item j (0..7) of thread tid: lane l of wave w takes dim
-    // 16 (j % 8) + l % 16 and positions r0, r0 + 1 with r0 = 2 (4 w + l / 16),
-    // so the packed-pair writes of the transposed planes land on 64 distinct
-    // banks.
+    // 16 ((j + l / 16) % 8) + l % 16 and positions r0, r0 + 1 with
+    // r0 = 2 (4 w + l / 16). The four 16-lane groups of a wave read four
+    // different 16-dim blocks of the raw tile, so the reads of the row-major
+    // raw V land on 64 distinct banks (rows are 128 words apart, so without
+    // the rotation the groups' reads met on the same 16 banks); the
+    // packed-pair writes of the transposed planes land on 64 distinct banks
+    // either way (row d starts 36 d words in).
     auto v_item = [&](int j, uint32_t& d, uint32_t& r0) {
-        d = 16 * j + (lane & 15);
+        d = 16 * ((j + (lane >> 4)) & 7) + (lane & 15);
         r0 = 2 * (4 * wave + (lane >> 4));
     };
     // K: wave w takes positions 8w .. 8w+7 of the block; lane l holds
