@@ -19,9 +19,12 @@
 // position, quarter of the head dimension); V comes to registers meanwhile and
 // overwrites K's LDS region once the scores are done, for the P.V chains. A
 // workgroup holds 35 KiB of LDS and 85 registers, so four fit on a CU. Rows at
-// or past length+t+1 never enter arithmetic. The combine runs as its own kernel: the
-// kernel boundary publishes the partials device-wide, where an in-kernel
-// hand-off costs an L2 write-back or same-address atomics per workgroup.
+// or past length+t+1 never enter arithmetic. Up to 16 blocks, the last
+// workgroup of each (token, kv head) group to finish combines in the same
+// launch: the group runs on one XCD, so the hand-off needs no L2 write-back
+// (only the stores' acknowledgements and one L2 atomic per workgroup). Longer
+// grids run the combine as its own kernel, 128 workgroups wide, since one
+// workgroup's reads of every partial would outlast the launch it saves.
 #include "lh_device.h"
 #include "lh_internal.h"
 
@@ -32,16 +35,154 @@ namespace lh {
 constexpr uint32_t GROUP = 8;     // blocks chained per combine group
 constexpr uint32_t ROUND = 256;   // blocks per combine round (32 groups)
 
+// Arrival word of a fused launch's (token, kv head) group: eight 7-bit
+// fields, field x counting the group's workgroups that ran on XCD x.
+constexpr uint32_t ARRIVE_FIELD = 7;
+
+// Largest block count a fused launch combines: groups of eight blocks, the
+// even ones on lanes 0..31 and the odd ones on lanes 32..63 of the combining
+// workgroup's waves.
+#ifndef LH_ATTN_FUSED_MAX
+#define LH_ATTN_FUSED_MAX 16
+#endif
+constexpr uint32_t FUSED_MAX_BLOCKS = LH_ATTN_FUSED_MAX;
+
+// The hand-off of a fused launch. Each workgroup waits until its partial
+// stores are acknowledged (the vector L1 writes through, so they are in its
+// XCD's L2), then adds its arrival to its XCD's field of the group's word;
+// the workgroup that brings the fields' total to nblk returns the word to
+// zero for the next launch and combines the group's four heads from the
+// partials, which its XCD's L2 holds. That holds only when the whole group
+// ran on its XCD: otherwise the word shows it, and the combine writes NaN
+// (never a silently stale result). The arithmetic is k_attn_combine's,
+// operation for operation.
+__device__ __forceinline__ void attn_combine_last(const float* __restrict__ PM,
+    const float* __restrict__ PT, const float* __restrict__ PA,
+    unsigned long long* __restrict__ arrive,
+    float* __restrict__ out, uint32_t t, uint32_t kvh, uint32_t nblk, uint32_t nbc, uint32_t n)
+{
+    __shared__ uint32_t verdict;   // 0 not last, 1 last, 2 last but the group was split
+    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    unsigned long long* slot = arrive + (size_t)t * LH_KV_HEADS + kvh;
+    if (tid == 0) {
+        uint32_t xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 3)" : "=s"(xcc));
+        const unsigned long long inc = 1ull << (ARRIVE_FIELD * xcc);
+        const unsigned long long now =
+            __hip_atomic_fetch_add(slot, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + inc;
+        uint32_t arrived = 0;
+#pragma unroll
+        for (uint32_t x = 0; x < 8; x++) {
+            arrived += (uint32_t)(now >> (ARRIVE_FIELD * x)) & ((1u << ARRIVE_FIELD) - 1);
+        }
+        verdict = arrived != nblk ? 0u : now == (unsigned long long)nblk << (ARRIVE_FIELD * xcc) ? 1u : 2u;
+    }
+    __syncthreads();
+    const uint32_t seen = verdict;
+    if (!seen) {
+        return;
+    }
+    if (tid == 0) {
+        __hip_atomic_exchange(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    asm volatile("buffer_inv sc0" ::: "memory");   // partials from L2, never this CU's L1
+    const uint32_t nb = (n + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
+    const size_t th = (size_t)t * LH_HEADS + kvh * 4 + wave;
+    // Wave w combines head kvh * 4 + w alone: lane = (group gp = lane / 32,
+    // dims 4c .. 4c + 3 with c = lane % 32). Every load is issued first (the
+    // block maxima and sums with lane = block; the lane's four dims of its
+    // group's eight blocks, rows past nb clamped). A lane takes its blocks'
+    // factors and sums from the lanes that hold them (ds_bpermute), chains its
+    // group, and group 1's sums reach lanes 0..31 by a 32-lane swap. Blocks
+    // past nb are skipped by selects, so no branch follows the loads.
+    const uint32_t c = lane & 31, gp = lane >> 5;
+    constexpr uint32_t J = FUSED_MAX_BLOCKS / (2 * GROUP);   // groups per half-wave
+    const float* pm = PM + th * nbc;
+    const float* pt = PT + th * nbc;
+    const float mb = lane < nb ? pm[lane] : -__builtin_inff();
+    const float tb = lane < nb ? pt[lane] : 0.0f;
+    const float4* pa = reinterpret_cast<const float4*>(PA + th * nbc * LH_HEAD_DIM) + c;
+    float4 a[J][GROUP];
+#pragma unroll
+    for (uint32_t j = 0; j < J; j++) {
+#pragma unroll
+        for (uint32_t k = 0; k < GROUP; k++) {
+            const uint32_t bb = (gp + 2 * j) * GROUP + k;
+            a[j][k] = pa[(size_t)(bb < nb ? bb : nb - 1) * (LH_HEAD_DIM / 4)];
+        }
+    }
+    const float M = wave_max64(mb);
+    const int fl = __float_as_int(expf_cw(mb - M));
+    auto upper = [](float v) {   // lane l < 32 receives lane l + 32's v
+        const uint32_t u = __float_as_uint(v);
+        return __uint_as_float(__builtin_amdgcn_permlane32_swap(u, u, false, false)[1]);
+    };
+    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+    float T = 0.0f;
+#pragma unroll
+    for (uint32_t j = 0; j < J; j++) {
+        float4 S = make_float4(0.f, 0.f, 0.f, 0.f);
+        float U = 0.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < GROUP; k++) {
+            const uint32_t bb = (gp + 2 * j) * GROUP + k;
+            const float fb = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * bb, fl));
+            const float tk = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * bb, __float_as_int(tb)));
+            const bool in = bb < nb;
+            S.x = in ? __builtin_fmaf(fb, a[j][k].x, S.x) : S.x;
+            S.y = in ? __builtin_fmaf(fb, a[j][k].y, S.y) : S.y;
+            S.z = in ? __builtin_fmaf(fb, a[j][k].z, S.z) : S.z;
+            S.w = in ? __builtin_fmaf(fb, a[j][k].w, S.w) : S.w;
+            U = in ? __builtin_fmaf(fb, tk, U) : U;
+        }
+        // Lanes 0..31 add group 2j, then group 2j + 1 (from lane + 32), left
+        // to right after the groups before them.
+        const float4 S1 = make_float4(upper(S.x), upper(S.y), upper(S.z), upper(S.w));
+        const float U1 = upper(U);
+        const bool in0 = 2 * j * GROUP < nb, in1 = (2 * j + 1) * GROUP < nb;
+        if (j == 0) {
+            A = S;
+            T = U;
+        } else if (in0) {
+            A = make_float4(A.x + S.x, A.y + S.y, A.z + S.z, A.w + S.w);
+            T = T + U;
+        }
+        if (in1) {
+            A = make_float4(A.x + S1.x, A.y + S1.y, A.z + S1.z, A.w + S1.w);
+            T = T + U1;
+        }
+    }
+    if (lane < 32) {
+        float4 o = make_float4(A.x / T, A.y / T, A.z / T, A.w / T);
+        if (seen != 1) {
+            o = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""),
+                __builtin_nanf(""));
+        }
+        reinterpret_cast<float4*>(out + (size_t)t * LH_QUERY + (kvh * 4 + wave) * LH_HEAD_DIM)[c] = o;
+    }
+}
+
+// grid (8 * nblk * count): workgroup id = (t * nblk + b) * 8 + kvh, so every
+// block of a (token, kv head) group runs on one XCD (the dispatcher deals a
+// launch's workgroups to the 8 XCDs in turn, so ids that agree mod 8 share
+// one). FUSED: the last workgroup of a group to arrive combines the group's
+// four heads itself (k_attn_combine's schedule), reading the partials from
+// that XCD's L2.
+template <bool FUSED>
 __global__ void __launch_bounds__(256)
 k_attn_blocks(const float* __restrict__ q, const float* __restrict__ kcache,
     const float* __restrict__ vcache, const lh_step_params* __restrict__ params,
-    uint32_t capacity, float* __restrict__ PM, float* __restrict__ PT, float* __restrict__ PA)
+    uint32_t capacity, uint32_t nblk, float* __restrict__ PM, float* __restrict__ PT,
+    float* __restrict__ PA, unsigned long long* __restrict__ arrive, float* __restrict__ out)
 {
     // One 32 KiB tile region holds K for the scores, then V for the P.V chains.
     __shared__ float4 T[LH_ATTN_BLOCK * LH_HEAD_DIM / 4];
     __shared__ float4 qs[4][LH_HEAD_DIM / 4];
     __shared__ float S[4][LH_ATTN_BLOCK];
-    const uint32_t b = blockIdx.x, kvh = blockIdx.y, t = blockIdx.z;
+    const uint32_t kvh = blockIdx.x & 7, b = (blockIdx.x >> 3) % nblk,
+                   t = (blockIdx.x >> 3) / nblk;
     const uint64_t tile = lh_kv_index(capacity, 0, kvh, (uint64_t)b * LH_ATTN_BLOCK);
     const float4* kb = reinterpret_cast<const float4*>(kcache + tile);
     const float4* vb = reinterpret_cast<const float4*>(vcache + tile);
@@ -164,15 +305,17 @@ k_attn_blocks(const float* __restrict__ q, const float* __restrict__ kcache,
             a1 = __builtin_fmaf(ej, v.y, a1);
         }
     }
-    if (!valid) {
-        return;
-    }
     const size_t th = (size_t)t * LH_HEADS + kvh * 4 + wave;
-    if (lane == 0) {
-        PM[th * nbc + b] = m;
-        PT[th * nbc + b] = total;
+    if (valid) {
+        if (lane == 0) {
+            PM[th * nbc + b] = m;
+            PT[th * nbc + b] = total;
+        }
+        *reinterpret_cast<float2*>(PA + (th * nbc + b) * LH_HEAD_DIM + d0) = make_float2(a0, a1);
     }
-    *reinterpret_cast<float2*>(PA + (th * nbc + b) * LH_HEAD_DIM + d0) = make_float2(a0, a1);
+    if (FUSED) {
+        attn_combine_last(PM, PT, PA, arrive, out, t, kvh, nblk, nbc, n);
+    }
 }
 
 // grid (32 heads x 4 dimension quarters, count), 256 threads: thread
@@ -334,19 +477,101 @@ extern "C" int lh_launch_step_embed(const uint16_t* E, const float* yarn, int32_
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
+#ifndef LH_ATTN_FUSED_BLOCKS
+#define LH_ATTN_FUSED_BLOCKS LH_ATTN_FUSED_MAX   // largest block grid combined in the blocks kernel
+#endif
+static_assert(LH_ATTN_FUSED_BLOCKS <= lh::FUSED_MAX_BLOCKS, "fused combine capacity");
+
+// Whether a launch's workgroups whose ids agree mod 8 run on one XCD, per
+// device, as measured by lh_attention_xcd_probe (0 unknown, 1 yes, 2 no).
+static int xcd_dispatch[64];
+
+namespace lh {
+__global__ void k_xcd_probe(uint32_t* out)
+{
+    if (threadIdx.x == 0) {
+        uint32_t xcc;
+        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 3)" : "=s"(xcc));
+        out[blockIdx.x] = xcc;
+    }
+}
+}  // namespace lh
+
+// Once per device: runs launches of 1, 7, 64, 509 and 1467 workgroups, each
+// recording the XCD it ran on into d_words (at least 2048 words, left
+// zeroed), and records whether in every launch the workgroups whose ids agree
+// mod 8 ran on one XCD (the dispatcher deals workgroups to the XCDs in turn;
+// which XCD a launch starts on varies). *ok receives the verdict.
+// Synchronizes the stream when it probes.
+extern "C" int lh_attention_xcd_probe(uint32_t* d_words, size_t words, int* ok, hipStream_t s)
+{
+    static const uint32_t grids[] = {1, 7, 64, 509, 1467};
+    int device = -1;
+    if (!d_words || words < 2048 || hipGetDevice(&device) != hipSuccess || device < 0 ||
+        device >= 64) {
+        return -1;
+    }
+    const int known = __atomic_load_n(&xcd_dispatch[device], __ATOMIC_RELAXED);
+    if (known) {
+        *ok = known == 1;
+        return 0;
+    }
+    uint32_t host[2048];
+    size_t at = 0;
+    for (uint32_t g : grids) {
+        hipLaunchKernelGGL(lh::k_xcd_probe, dim3(g), dim3(64), 0, s, d_words + at);
+        at += g;
+    }
+    if (hipGetLastError() != hipSuccess ||
+        hipMemcpyAsync(host, d_words, at * sizeof(uint32_t), hipMemcpyDeviceToHost, s) != hipSuccess ||
+        hipMemsetAsync(d_words, 0, words * sizeof(uint32_t), s) != hipSuccess ||
+        hipStreamSynchronize(s) != hipSuccess) {
+        return -1;
+    }
+    int good = 1;
+    at = 0;
+    for (uint32_t g : grids) {
+        for (uint32_t i = 8; i < g; i++) {
+            good &= host[at + i] == host[at + i % 8];
+        }
+        at += g;
+    }
+    __atomic_store_n(&xcd_dispatch[device], good ? 1 : 2, __ATOMIC_RELAXED);
+    *ok = good;
+    return 0;
+}
+
+static bool fused_attention_ok()
+{
+    int device = -1;
+    return hipGetDevice(&device) == hipSuccess && device >= 0 && device < 64 &&
+        __atomic_load_n(&xcd_dispatch[device], __ATOMIC_RELAXED) == 1;
+}
+
 // The kernels read the step length from params (device memory); `length`
-// here must equal params->length and only sizes the block grid.
+// here must equal params->length and only sizes the block grid. With arrive
+// set (count * 8 zeroed 64-bit words, left zeroed) and a block grid of at most
+// LH_ATTN_FUSED_BLOCKS on a device whose dispatch the probe confirmed, one
+// launch does the blocks and the combine; otherwise two.
 extern "C" int lh_launch_attention(const float* q, const float* kcache_layer,
     const float* vcache_layer, const lh_step_params* params, uint32_t length, uint32_t count,
-    uint32_t capacity, float* PM, float* PT, float* PA, float* out, hipStream_t s)
+    uint32_t capacity, float* PM, float* PT, float* PA, unsigned long long* arrive, float* out,
+    hipStream_t s)
 {
     if (!count || capacity % LH_ATTN_BLOCK || length + count > capacity) {
         return -1;
     }
-    hipLaunchKernelGGL(k_attn_blocks, dim3(lh_attention_blocks(length, count), LH_KV_HEADS, count),
-        dim3(256), 0, s, q, kcache_layer, vcache_layer, params, capacity, PM, PT, PA);
-    hipLaunchKernelGGL(k_attn_combine, dim3(LH_HEADS * 4, count), dim3(256), 0, s, PM, PT, PA, params,
-        capacity, out);
+    const uint32_t nblk = lh_attention_blocks(length, count);
+    const dim3 grid(LH_KV_HEADS * nblk * count);
+    if (arrive && nblk <= LH_ATTN_FUSED_BLOCKS && fused_attention_ok()) {
+        hipLaunchKernelGGL(k_attn_blocks<true>, grid, dim3(256), 0, s, q, kcache_layer,
+            vcache_layer, params, capacity, nblk, PM, PT, PA, arrive, out);
+    } else {
+        hipLaunchKernelGGL(k_attn_blocks<false>, grid, dim3(256), 0, s, q, kcache_layer,
+            vcache_layer, params, capacity, nblk, PM, PT, PA, nullptr, nullptr);
+        hipLaunchKernelGGL(k_attn_combine, dim3(LH_HEADS * 4, count), dim3(256), 0, s, PM, PT, PA,
+            params, capacity, out);
+    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
@@ -417,7 +642,7 @@ extern "C" int lh_attention_noalloc(const float* d_q, const float* d_keys, const
         (uint32_t)count);
     if (hipGetLastError() != hipSuccess ||
         lh_launch_attention(d_q, d_keys, d_values, params, (uint32_t)length, (uint32_t)count,
-            (uint32_t)capacity, PM, PT, PA, d_out, s)) {
+            (uint32_t)capacity, PM, PT, PA, nullptr, d_out, s)) {
         lh_set_error("attention_noalloc: launch failed");
         return -1;
     }

@@ -17,6 +17,10 @@ static int check(hipError_t status, const char *what)
     return 0;
 }
 
+/* 64-bit arrival words of the fused attention launch: one per (token, kv
+ * head), and at least the XCD dispatch probe's 2048 32-bit words. */
+#define ARRIVE_WORDS(B) ((B) * LH_KV_HEADS > 1024 ? (B) * LH_KV_HEADS : 1024)
+
 static int alloc_device(void **out, size_t bytes, uint64_t *total)
 {
     *out = NULL;
@@ -57,7 +61,15 @@ lh_workspace *lh_workspace_create(size_t capacity, size_t block)
         alloc_device((void **)&ws->d_PM, B * LH_HEADS * nbc * sizeof(float), &ws->bytes) ||
         alloc_device((void **)&ws->d_PT, B * LH_HEADS * nbc * sizeof(float), &ws->bytes) ||
         alloc_device((void **)&ws->d_PA, B * LH_HEADS * nbc * LH_HEAD_DIM * sizeof(float),
-            &ws->bytes)) {
+            &ws->bytes) ||
+        alloc_device((void **)&ws->d_arrive, ARRIVE_WORDS(B) * 8, &ws->bytes) ||
+        check(hipMemset(ws->d_arrive, 0, ARRIVE_WORDS(B) * 8), "workspace clear")) {
+        lh_workspace_destroy(ws);
+        return NULL;
+    }
+    int fused = 0;
+    if (lh_attention_xcd_probe((uint32_t *)ws->d_arrive, 2 * ARRIVE_WORDS(B), &fused, NULL)) {
+        lh_set_error("workspace: XCD dispatch probe failed: %s", hipGetErrorString(hipGetLastError()));
         lh_workspace_destroy(ws);
         return NULL;
     }
@@ -71,7 +83,7 @@ void lh_workspace_destroy(lh_workspace *ws)
         return;
     }
     void *device[] = {ws->d_params, ws->d_q, ws->d_attn, ws->d_gated, ws->d_up, ws->d_xn,
-        ws->d_qraw, ws->d_kraw, ws->d_vraw, ws->d_PM, ws->d_PT, ws->d_PA,
+        ws->d_qraw, ws->d_kraw, ws->d_vraw, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_arrive,
         ws->d_split, ws->d_gemm, ws->d_yarn};
     for (size_t i = 0; i < sizeof device / sizeof device[0]; i++) {
         lh_dev_free(device[i]);
@@ -233,7 +245,7 @@ static int layer_unfused(const lh_layer_weights *w, float *x, float *keys, float
         launched(lh_launch_rope_append(ws->d_qraw, ws->d_kraw, ws->d_vraw, params, n, ws->d_q,
             keys, values, C, s), "rope/append") ||
         launched(lh_launch_attention(ws->d_q, keys, values, ws->d_params, (uint32_t)ws->length, n,
-            C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_attn, s),
+            C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_arrive, ws->d_attn, s),
             "attention") ||
         launched(lh_launch_matvec(kind, 0, wo, w->scale[3], ws->d_attn, x, x, LH_HIDDEN,
             LH_QUERY, n, s), "o") ||
@@ -259,7 +271,7 @@ static int layer_fused(const lh_layer_weights *w, float *x, float *keys, float *
     if (launched(lh_launch_qkv_rope(lookup, w->qkv, w->scale[0], w->scale[1], w->scale[2],
             w->input_norm, x, params, n, ws->d_q, keys, values, C, s), "qkv") ||
         launched(lh_launch_attention(ws->d_q, keys, values, ws->d_params, (uint32_t)ws->length, n,
-            C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_attn, s),
+            C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_arrive, ws->d_attn, s),
             "attention") ||
         launched(lh_launch_matvec(0, lookup, w->o, w->scale[3], ws->d_attn, x, x, LH_HIDDEN,
             LH_QUERY, n, s), "o") ||
@@ -287,7 +299,7 @@ int lh_layer_operator(int op, const lh_layer_weights *w, float *d_x, float *d_ke
             w->input_norm, d_x, ws->d_params, n, ws->d_q, d_keys, d_values, C, s), "qkv");
     case LH_OP_ATTENTION:
         return launched(lh_launch_attention(ws->d_q, d_keys, d_values, ws->d_params, (uint32_t)ws->length, n,
-            C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_attn, s),
+            C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_arrive, ws->d_attn, s),
             "attention");
     case LH_OP_O_RESIDUAL:
         return launched(lh_launch_matvec(0, 0, w->o, w->scale[3], ws->d_attn, d_x, d_x, LH_HIDDEN,
@@ -342,7 +354,7 @@ int lh_attention(const float *d_q, const float *d_keys, const float *d_values, l
     }
     return launched(lh_launch_attention(d_q, d_keys, d_values, ws->d_params,
         (uint32_t)ws->length, (uint32_t)ws->count, (uint32_t)ws->capacity, ws->d_PM, ws->d_PT,
-        ws->d_PA, d_out, (hipStream_t)stream), "attention");
+        ws->d_PA, ws->d_arrive, d_out, (hipStream_t)stream), "attention");
 }
 
 int lh_attention_mfma(const float *d_q, const float *d_keys, const float *d_values,

@@ -30,7 +30,11 @@ int lh_launch_rmsnorm(const float *gamma, const float *x, float *out, uint32_t w
  * params->length) sizes the block grid only. */
 int lh_launch_attention(const float *q, const float *kcache_layer, const float *vcache_layer,
     const lh_step_params *params, uint32_t length, uint32_t count, uint32_t capacity, float *PM,
-    float *PT, float *PA, float *out, hipStream_t s);
+    float *PT, float *PA, unsigned long long *arrive, float *out, hipStream_t s);
+/* Records once per device whether a launch's workgroups whose ids agree mod 8
+ * run on one XCD (five probe launches into d_words, at least 2048 words, left
+ * zeroed); *ok receives the verdict. A fused attention launch needs it. */
+int lh_attention_xcd_probe(uint32_t *d_words, size_t words, int *ok, hipStream_t s);
 /* Matrix-core attention for multi-token steps (tolerance path). With xs set
  * the output goes to the two scaled FP16 planes of xs (token stride
  * xs_tokens, the o projection's input) instead of FP32 rows of out, with

@@ -21,6 +21,7 @@ struct lh_workspace {
     float *d_qraw, *d_kraw, *d_vraw;
     float *d_PM, *d_PT;            /* [B][32][C/64] block maxima and sums */
     float *d_PA;                   /* [B][32][C/64][128] block P.V partials */
+    unsigned long long *d_arrive;  /* [max(B * 8, 1024)] arrival words of fused attention, zero between launches */
     float *d_yarn;                 /* [C][128]: cos[64], sin[64] per position (decode) */
     float *h_yarn;                 /* host copy of the same rows, filled on first use */
     uint8_t *h_yarn_ready;         /* [C]: row p of h_yarn holds lh_yarn(p) */

@@ -157,6 +157,25 @@ def test_attention_repeated_launches_one_workspace(gpu):
         gpu.lh_workspace_destroy(ws)
 
 
+def test_attention_fused_combine_boundary(gpu):
+    """Block grids of up to 16 blocks run as one launch whose last-arriving
+    workgroup per (token, kv head) combines (from its XCD's L2); 17 and more
+    as blocks + combine. Both sides of the boundary, single and multi-token
+    steps (one arrival word per token), bitwise the mirror."""
+    rng = np.random.default_rng(33)
+    capacity = 2048
+    for length, count in ((0, 1), (63, 1), (64, 1), (511, 1), (1023, 1), (1024, 1),
+                          (1000, 24), (1001, 24), (990, 32), (2000, 3)):
+        total = length + count
+        q = (rng.normal(size=count * 4096) * 3).astype(np.float32)
+        kpm = rng.normal(size=(total, 1024)).astype(np.float32)
+        vpm = rng.normal(size=(total, 1024)).astype(np.float32)
+        got = attention_on_device(gpu, q, kpm, vpm, length, count, capacity)
+        mirror = oracle_lib.attention(MIRROR, q, kpm.reshape(-1), vpm.reshape(-1), 128, 1024,
+                                      length, count)
+        assert np.array_equal(bits(got), bits(mirror)), (length, count)
+
+
 def test_long_causal_sentinel_through_kernels(gpu):
     """tests/test_metal.m:956-999: zero q and K, V rows of 1 except a 4352
     sentinel in the last row; query row 0 must mask it (1.0), row 1 must
