@@ -25,6 +25,7 @@
 // (only the stores' acknowledgements and one L2 atomic per workgroup). Longer
 // grids run the combine as its own kernel, 128 workgroups wide, since one
 // workgroup's reads of every partial would outlast the launch it saves.
+#include "lh_attention_blocks.h"
 #include "lh_device.h"
 #include "lh_internal.h"
 
@@ -32,137 +33,7 @@
 
 namespace lh {
 
-constexpr uint32_t GROUP = 8;     // blocks chained per combine group
 constexpr uint32_t ROUND = 256;   // blocks per combine round (32 groups)
-
-// Arrival word of a fused launch's (token, kv head) group: eight 7-bit
-// fields, field x counting the group's workgroups that ran on XCD x.
-constexpr uint32_t ARRIVE_FIELD = 7;
-
-// Largest block count a fused launch combines: groups of eight blocks, the
-// even ones on lanes 0..31 and the odd ones on lanes 32..63 of the combining
-// workgroup's waves.
-#ifndef LH_ATTN_FUSED_MAX
-#define LH_ATTN_FUSED_MAX 16
-#endif
-constexpr uint32_t FUSED_MAX_BLOCKS = LH_ATTN_FUSED_MAX;
-
-// The hand-off of a fused launch. Each workgroup waits until its partial
-// stores are acknowledged (the vector L1 writes through, so they are in its
-// XCD's L2), then adds its arrival to its XCD's field of the group's word;
-// the workgroup that brings the fields' total to nblk returns the word to
-// zero for the next launch and combines the group's four heads from the
-// partials, which its XCD's L2 holds. That holds only when the whole group
-// ran on its XCD: otherwise the word shows it, and the combine writes NaN
-// (never a silently stale result). The arithmetic is k_attn_combine's,
-// operation for operation.
-__device__ __forceinline__ void attn_combine_last(const float* __restrict__ PM,
-    const float* __restrict__ PT, const float* __restrict__ PA,
-    unsigned long long* __restrict__ arrive,
-    float* __restrict__ out, uint32_t t, uint32_t kvh, uint32_t nblk, uint32_t nbc, uint32_t n)
-{
-    __shared__ uint32_t verdict;   // 0 not last, 1 last, 2 last but the group was split
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
-    unsigned long long* slot = arrive + (size_t)t * LH_KV_HEADS + kvh;
-    if (tid == 0) {
-        uint32_t xcc;
-        asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID, 0, 3)" : "=s"(xcc));
-        const unsigned long long inc = 1ull << (ARRIVE_FIELD * xcc);
-        const unsigned long long now =
-            __hip_atomic_fetch_add(slot, inc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + inc;
-        uint32_t arrived = 0;
-#pragma unroll
-        for (uint32_t x = 0; x < 8; x++) {
-            arrived += (uint32_t)(now >> (ARRIVE_FIELD * x)) & ((1u << ARRIVE_FIELD) - 1);
-        }
-        verdict = arrived != nblk ? 0u : now == (unsigned long long)nblk << (ARRIVE_FIELD * xcc) ? 1u : 2u;
-    }
-    __syncthreads();
-    const uint32_t seen = verdict;
-    if (!seen) {
-        return;
-    }
-    if (tid == 0) {
-        __hip_atomic_exchange(slot, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    asm volatile("buffer_inv sc0" ::: "memory");   // partials from L2, never this CU's L1
-    const uint32_t nb = (n + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
-    const size_t th = (size_t)t * LH_HEADS + kvh * 4 + wave;
-    // Wave w combines head kvh * 4 + w alone: lane = (group gp = lane / 32,
-    // dims 4c .. 4c + 3 with c = lane % 32). Every load is issued first (the
-    // block maxima and sums with lane = block; the lane's four dims of its
-    // group's eight blocks, rows past nb clamped). A lane takes its blocks'
-    // factors and sums from the lanes that hold them (ds_bpermute), chains its
-    // group, and group 1's sums reach lanes 0..31 by a 32-lane swap. Blocks
-    // past nb are skipped by selects, so no branch follows the loads.
-    const uint32_t c = lane & 31, gp = lane >> 5;
-    constexpr uint32_t J = FUSED_MAX_BLOCKS / (2 * GROUP);   // groups per half-wave
-    const float* pm = PM + th * nbc;
-    const float* pt = PT + th * nbc;
-    const float mb = lane < nb ? pm[lane] : -__builtin_inff();
-    const float tb = lane < nb ? pt[lane] : 0.0f;
-    const float4* pa = reinterpret_cast<const float4*>(PA + th * nbc * LH_HEAD_DIM) + c;
-    float4 a[J][GROUP];
-#pragma unroll
-    for (uint32_t j = 0; j < J; j++) {
-#pragma unroll
-        for (uint32_t k = 0; k < GROUP; k++) {
-            const uint32_t bb = (gp + 2 * j) * GROUP + k;
-            a[j][k] = pa[(size_t)(bb < nb ? bb : nb - 1) * (LH_HEAD_DIM / 4)];
-        }
-    }
-    const float M = wave_max64(mb);
-    const int fl = __float_as_int(expf_cw(mb - M));
-    auto upper = [](float v) {   // lane l < 32 receives lane l + 32's v
-        const uint32_t u = __float_as_uint(v);
-        return __uint_as_float(__builtin_amdgcn_permlane32_swap(u, u, false, false)[1]);
-    };
-    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-    float T = 0.0f;
-#pragma unroll
-    for (uint32_t j = 0; j < J; j++) {
-        float4 S = make_float4(0.f, 0.f, 0.f, 0.f);
-        float U = 0.0f;
-#pragma unroll
-        for (uint32_t k = 0; k < GROUP; k++) {
-            const uint32_t bb = (gp + 2 * j) * GROUP + k;
-            const float fb = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * bb, fl));
-            const float tk = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * bb, __float_as_int(tb)));
-            const bool in = bb < nb;
-            S.x = in ? __builtin_fmaf(fb, a[j][k].x, S.x) : S.x;
-            S.y = in ? __builtin_fmaf(fb, a[j][k].y, S.y) : S.y;
-            S.z = in ? __builtin_fmaf(fb, a[j][k].z, S.z) : S.z;
-            S.w = in ? __builtin_fmaf(fb, a[j][k].w, S.w) : S.w;
-            U = in ? __builtin_fmaf(fb, tk, U) : U;
-        }
-        // Lanes 0..31 add group 2j, then group 2j + 1 (from lane + 32), left
-        // to right after the groups before them.
-        const float4 S1 = make_float4(upper(S.x), upper(S.y), upper(S.z), upper(S.w));
-        const float U1 = upper(U);
-        const bool in0 = 2 * j * GROUP < nb, in1 = (2 * j + 1) * GROUP < nb;
-        if (j == 0) {
-            A = S;
-            T = U;
-        } else if (in0) {
-            A = make_float4(A.x + S.x, A.y + S.y, A.z + S.z, A.w + S.w);
-            T = T + U;
-        }
-        if (in1) {
-            A = make_float4(A.x + S1.x, A.y + S1.y, A.z + S1.z, A.w + S1.w);
-            T = T + U1;
-        }
-    }
-    if (lane < 32) {
-        float4 o = make_float4(A.x / T, A.y / T, A.z / T, A.w / T);
-        if (seen != 1) {
-            o = make_float4(__builtin_nanf(""), __builtin_nanf(""), __builtin_nanf(""),
-                __builtin_nanf(""));
-        }
-        reinterpret_cast<float4*>(out + (size_t)t * LH_QUERY + (kvh * 4 + wave) * LH_HEAD_DIM)[c] = o;
-    }
-}
 
 // grid (8 * nblk * count): workgroup id = (t * nblk + b) * 8 + kvh, so every
 // block of a (token, kv head) group runs on one XCD (the dispatcher deals a
@@ -177,145 +48,11 @@ k_attn_blocks(const float* __restrict__ q, const float* __restrict__ kcache,
     uint32_t capacity, uint32_t nblk, float* __restrict__ PM, float* __restrict__ PT,
     float* __restrict__ PA, unsigned long long* __restrict__ arrive, float* __restrict__ out)
 {
-    // One 32 KiB tile region holds K for the scores, then V for the P.V chains.
-    __shared__ float4 T[LH_ATTN_BLOCK * LH_HEAD_DIM / 4];
-    __shared__ float4 qs[4][LH_HEAD_DIM / 4];
-    __shared__ float S[4][LH_ATTN_BLOCK];
+    __shared__ AttnShared sh;
     const uint32_t kvh = blockIdx.x & 7, b = (blockIdx.x >> 3) % nblk,
                    t = (blockIdx.x >> 3) / nblk;
-    const uint64_t tile = lh_kv_index(capacity, 0, kvh, (uint64_t)b * LH_ATTN_BLOCK);
-    const float4* kb = reinterpret_cast<const float4*>(kcache + tile);
-    const float4* vb = reinterpret_cast<const float4*>(vcache + tile);
-    const uint32_t tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-    // The tile loads do not wait for the step record: the launch grid covers
-    // ceil((length + count) / 64) blocks of a capacity that is a multiple of
-    // 64, so all 64 rows are in bounds; rows past the valid count are never
-    // used in arithmetic.
-    // Issue order: the four query rows (2 KiB) and the K tile go to LDS by
-    // direct loads, then the V tile to registers. Vector loads complete in
-    // issue order, so the scores wait for q and K only (an explicit vmcnt(8))
-    // and V lands while they run.
-    if (tid < 128) {
-        __builtin_amdgcn_global_load_lds(reinterpret_cast<const float4*>(
-            q + (size_t)t * LH_QUERY + kvh * 4 * LH_HEAD_DIM) + tid,
-            reinterpret_cast<float4*>(qs) + 64 * wave, 16, 0, 0);
-    }
-    // K: wave w covers positions 16w..16w+15; lane = 4 * (position - 16w) +
-    // quarter. The tile's word order (lh_ktile_word) makes load i of wave w
-    // the contiguous 1 KiB of words (8w + i) * 64 .. +63, written to LDS in
-    // the same order, so lane l later reads word (8w + i) * 64 + l.
-    const uint32_t p = 16 * wave + (lane >> 2), quarter = lane & 3;
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        __builtin_amdgcn_global_load_lds(kb + (wave * 8 + i) * 64 + lane,
-            T + (wave * 8 + i) * 64, 16, 0, 0);
-    }
-    __builtin_amdgcn_sched_barrier(0);   // V's loads stay behind K's
-    // (A native vector type: a float4 struct copy is a memcpy that, with the
-    // intrinsics around it, stays in scratch memory.)
-    typedef float v4f __attribute__((ext_vector_type(4)));
-    v4f vr[8];
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        vr[i] = reinterpret_cast<const v4f*>(vb)[tid + 256 * i];   // row (tid + 256 i) >> 5
-    }
-    // No early exit for blocks past token t's last position (multi-token
-    // steps): a branch here lets the compiler sink the V loads below it. Such
-    // a workgroup runs with valid = 0 and writes nothing.
-    const uint32_t n = params->length + t + 1;
-    const uint32_t nbc = capacity / LH_ATTN_BLOCK;
-    const uint32_t rest = n > b * LH_ATTN_BLOCK ? n - b * LH_ATTN_BLOCK : 0;
-    const uint32_t valid = rest < LH_ATTN_BLOCK ? rest : LH_ATTN_BLOCK;
-    // s_waitcnt vmcnt(8), then a bare barrier: __syncthreads()'s workgroup
-    // fence would also wait for the V loads.
-    __builtin_amdgcn_s_waitcnt(0x0f78);
-    __builtin_amdgcn_s_barrier();
-    // The K and q words of step i + 1 are read while step i's products run.
-    float c[4] = {0.f, 0.f, 0.f, 0.f};
-    float4 k = T[wave * 8 * 64 + lane];
-    float4 qq[4];
-#pragma unroll
-    for (int hh = 0; hh < 4; hh++) {
-        qq[hh] = qs[hh][8 * quarter];
-    }
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        float4 kn, qn[4];
-        if (i < 7) {
-            kn = T[(wave * 8 + i + 1) * 64 + lane];
-#pragma unroll
-            for (int hh = 0; hh < 4; hh++) {
-                qn[hh] = qs[hh][8 * quarter + i + 1];
-            }
-        }
-#pragma unroll
-        for (int hh = 0; hh < 4; hh++) {
-            c[hh] = __builtin_fmaf(qq[hh].x, k.x, c[hh]);
-            c[hh] = __builtin_fmaf(qq[hh].y, k.y, c[hh]);
-            c[hh] = __builtin_fmaf(qq[hh].z, k.z, c[hh]);
-            c[hh] = __builtin_fmaf(qq[hh].w, k.w, c[hh]);
-        }
-        if (i < 7) {
-            k = kn;
-#pragma unroll
-            for (int hh = 0; hh < 4; hh++) {
-                qq[hh] = qn[hh];
-            }
-        }
-        // Each step's four chains complete here (an empty asm that reads and
-        // writes them), so the compiler cannot defer three of them past the
-        // loop with every step's operands held in registers.
-        asm volatile("" : "+v"(c[0]), "+v"(c[1]), "+v"(c[2]), "+v"(c[3]));
-    }
-#pragma unroll
-    for (int hh = 0; hh < 4; hh++) {
-        const float v = quad_sum(c[hh]);  // (c0 + c1) + (c2 + c3)
-        if (quarter == 0 && p < valid) {
-            S[hh][p] = v * LH_SCORE_SCALE;
-        }
-    }
-    __syncthreads();   // every read of K is done; S holds the scores
-#pragma unroll
-    for (int i = 0; i < 8; i++) {
-        reinterpret_cast<v4f*>(T)[tid + 256 * i] = vr[i];
-    }
-    __syncthreads();
-    // Wave w = head kvh*4 + w from here on; lane = position. e_j reaches every
-    // lane by a scalar read of lane j.
-    const float s = lane < valid ? S[wave][lane] : -__builtin_inff();
-    const float m = wave_max64(s);
-    const float e = lane < valid ? expf_cw(s - m) : 0.0f;
-    const float total = wave_tree64(e);
-    const uint32_t d0 = 2 * lane;
-    float a0 = 0.0f, a1 = 0.0f;
-    const float* vt = reinterpret_cast<const float*>(T) + d0;
-    if (valid == LH_ATTN_BLOCK) {
-#pragma unroll
-        for (uint32_t j = 0; j < LH_ATTN_BLOCK; j++) {
-            const float ej = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
-            const float2 v = *reinterpret_cast<const float2*>(vt + j * LH_HEAD_DIM);
-            a0 = __builtin_fmaf(ej, v.x, a0);
-            a1 = __builtin_fmaf(ej, v.y, a1);
-        }
-    } else {
-        for (uint32_t j = 0; j < valid; j++) {
-            const float ej = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(e), j));
-            const float2 v = *reinterpret_cast<const float2*>(vt + j * LH_HEAD_DIM);
-            a0 = __builtin_fmaf(ej, v.x, a0);
-            a1 = __builtin_fmaf(ej, v.y, a1);
-        }
-    }
-    const size_t th = (size_t)t * LH_HEADS + kvh * 4 + wave;
-    if (valid) {
-        if (lane == 0) {
-            PM[th * nbc + b] = m;
-            PT[th * nbc + b] = total;
-        }
-        *reinterpret_cast<float2*>(PA + (th * nbc + b) * LH_HEAD_DIM + d0) = make_float2(a0, a1);
-    }
-    if (FUSED) {
-        attn_combine_last(PM, PT, PA, arrive, out, t, kvh, nblk, nbc, n);
-    }
+    attn_block<FUSED ? TAIL_COMBINE : TAIL_NONE, false>(q, kcache, vcache, params, capacity,
+        nblk, PM, PT, PA, arrive, nullptr, 0, out, b, kvh, t, sh);
 }
 
 // grid (32 heads x 4 dimension quarters, count), 256 threads: thread
@@ -548,9 +285,33 @@ static bool fused_attention_ok()
         __atomic_load_n(&xcd_dispatch[device], __ATOMIC_RELAXED) == 1;
 }
 
+// A decode token whose attention spans at most this many blocks (4608
+// positions) runs q|k|v and the attention blocks in one launch. Measured on
+// the 26-layer decode step: 34, 29 and 18 us faster at 1000, 3000 and 4300
+// positions, 30 to 50 us slower from 5500 on, where the blocks outnumber the
+// CU slots the projection leaves free and those waiting hold slots the later
+// ones need.
+#ifndef LH_CHAIN_MAX_BLOCKS
+#define LH_CHAIN_MAX_BLOCKS 72
+#endif
+
+extern "C" int lh_attention_chained(uint32_t length)
+{
+    return lh_attention_blocks(length, 1) <= LH_CHAIN_MAX_BLOCKS && fused_attention_ok();
+}
+
+extern "C" int lh_launch_attention_combine(const float* PM, const float* PT, const float* PA,
+    const lh_step_params* params, uint32_t capacity, uint32_t count, float* out, hipStream_t s)
+{
+    hipLaunchKernelGGL(k_attn_combine, dim3(LH_HEADS * 4, count), dim3(256), 0, s, PM, PT, PA,
+        params, capacity, out);
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
 // The kernels read the step length from params (device memory); `length`
 // here must equal params->length and only sizes the block grid. With arrive
-// set (count * 8 zeroed 64-bit words, left zeroed) and a block grid of at most
+// set (count * 8 zeroed arrival words, ARRIVE_STRIDE 64-bit words apart, left
+// zeroed) and a block grid of at most
 // LH_ATTN_FUSED_BLOCKS on a device whose dispatch the probe confirmed, one
 // launch does the blocks and the combine; otherwise two.
 extern "C" int lh_launch_attention(const float* q, const float* kcache_layer,

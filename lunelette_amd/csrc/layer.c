@@ -17,9 +17,13 @@ static int check(hipError_t status, const char *what)
     return 0;
 }
 
-/* 64-bit arrival words of the fused attention launch: one per (token, kv
- * head), and at least the XCD dispatch probe's 2048 32-bit words. */
-#define ARRIVE_WORDS(B) ((B) * LH_KV_HEADS > 1024 ? (B) * LH_KV_HEADS : 1024)
+/* 64-bit words of one-launch attention: an arrival word per (token, kv
+ * head), each on a 256-byte line of its own, then the 8 x 64 flags of a
+ * chained decode launch's q|k|v workgroups; at least the XCD dispatch
+ * probe's 2048 32-bit words. */
+#define FLAGS_WORD(B) ((B) * LH_KV_HEADS * LH_ARRIVE_STRIDE)
+#define ARRIVE_WORDS(B) (FLAGS_WORD(B) + LH_KV_HEADS * 64 > 1024 ? \
+    FLAGS_WORD(B) + LH_KV_HEADS * 64 : 1024)
 
 static int alloc_device(void **out, size_t bytes, uint64_t *total)
 {
@@ -75,6 +79,14 @@ lh_workspace *lh_workspace_create(size_t capacity, size_t block)
     }
     memset(ws->h_params, 0, sizeof(lh_step_params));
     return ws;
+}
+
+int lh_workspace_clear_arrivals(lh_workspace *ws)
+{
+    if (!ws || !ws->d_arrive) {
+        return -1;
+    }
+    return check(hipMemset(ws->d_arrive, 0, ARRIVE_WORDS(ws->block) * 8), "arrival words clear");
 }
 
 void lh_workspace_destroy(lh_workspace *ws)
@@ -268,11 +280,19 @@ static int layer_fused(const lh_layer_weights *w, float *x, float *keys, float *
 {
     const uint32_t n = (uint32_t)ws->count, C = (uint32_t)ws->capacity;
     const lh_step_params *params = ws->d_params;
-    if (launched(lh_launch_qkv_rope(lookup, w->qkv, w->scale[0], w->scale[1], w->scale[2],
-            w->input_norm, x, params, n, ws->d_q, keys, values, C, s), "qkv") ||
-        launched(lh_launch_attention(ws->d_q, keys, values, ws->d_params, (uint32_t)ws->length, n,
-            C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_arrive, ws->d_attn, s),
-            "attention") ||
+    /* One decode token: q|k|v and the attention blocks share a launch. */
+    const int chained = n == 1 && lh_attention_chained((uint32_t)ws->length);
+    if ((chained ?
+            launched(lh_launch_qkv_attention(lookup, w->qkv, w->scale[0], w->scale[1],
+                w->scale[2], w->input_norm, x, params, (uint32_t)ws->length, ws->d_q, keys,
+                values, C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_arrive,
+                ws->d_arrive + FLAGS_WORD(ws->block), ++ws->epoch, ws->d_attn, s),
+                "qkv/attention") :
+            launched(lh_launch_qkv_rope(lookup, w->qkv, w->scale[0], w->scale[1], w->scale[2],
+                w->input_norm, x, params, n, ws->d_q, keys, values, C, s), "qkv") ||
+            launched(lh_launch_attention(ws->d_q, keys, values, ws->d_params,
+                (uint32_t)ws->length, n, C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_arrive,
+                ws->d_attn, s), "attention")) ||
         launched(lh_launch_matvec(0, lookup, w->o, w->scale[3], ws->d_attn, x, x, LH_HIDDEN,
             LH_QUERY, n, s), "o") ||
         launched(lh_launch_gateup_silu(lookup, w->gate, w->up, w->scale[4], w->scale[5],

@@ -21,7 +21,9 @@ struct lh_workspace {
     float *d_qraw, *d_kraw, *d_vraw;
     float *d_PM, *d_PT;            /* [B][32][C/64] block maxima and sums */
     float *d_PA;                   /* [B][32][C/64][128] block P.V partials */
-    unsigned long long *d_arrive;  /* [max(B * 8, 1024)] arrival words of fused attention, zero between launches */
+    unsigned long long *d_arrive;  /* one-launch attention: B * 8 arrival words 256 B apart,
+                                      then 512 producer flags (ARRIVE_WORDS) */
+    unsigned long long epoch;      /* last epoch stored in the producer flags */
     float *d_yarn;                 /* [C][128]: cos[64], sin[64] per position (decode) */
     float *h_yarn;                 /* host copy of the same rows, filled on first use */
     uint8_t *h_yarn_ready;         /* [C]: row p of h_yarn holds lh_yarn(p) */
@@ -41,6 +43,9 @@ int lh_layer_forward_mfma(const lh_layer_weights *w, float *d_x, float *d_keys,
     float *d_values, lh_workspace *ws, int input_split, const float *next_norm, hipStream_t s);
 /* Allocates the MFMA path's extra workspace buffers (idempotent). */
 int lh_mfma_prepare(lh_workspace *ws);
+/* Returns the one-launch attention's arrival words to zero (after a failed
+ * step, whose launches may have left them mid-count). Synchronous. */
+int lh_workspace_clear_arrivals(lh_workspace *ws);
 /* Builds the device YaRN table of every position below the capacity from the
  * host YaRN (idempotent), for lh_workspace_set_decode. */
 int lh_workspace_prepare_decode(lh_workspace *ws);

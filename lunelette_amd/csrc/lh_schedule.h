@@ -38,6 +38,7 @@
 #define LH_CHUNK 1024      /* columns per canonical chunk */
 #define LH_LANE_COLS 16    /* columns per lane per chunk */
 #define LH_ATTN_BLOCK 64   /* positions per attention block */
+#define LH_ARRIVE_STRIDE 32 /* 64-bit words between one-launch attention's arrival words */
 #define LH_MAX_BLOCK 256   /* largest executed block (B) */
 
 #define LH_SCORE_SCALE 0.08838834764831845f

@@ -11,6 +11,7 @@
 // applies the canonical RMSNorm there before any dot. The q|k|v and gate/up
 // kernels split each output pair (RoPE halves, gate and up) over two waves
 // and join the two dots through LDS.
+#include "lh_attention_blocks.h"
 #include "lh_device.h"
 #include "lh_internal.h"
 
@@ -453,63 +454,78 @@ k_rows_generic(const void* __restrict__ W, float scale, const float* __restrict_
 // ---------------------------------------------------------------------------
 // RMSNorm -> q|k|v -> RoPE (+ query factor on Q) -> Q scratch and KV append
 // (src/metal_encode.m:129-153). The 48 heads (32 q, 8 k, 8 v) hold 64 RoPE
-// pairs each, rows head*128 + i and + 64. A workgroup owns the six pairs
-// P = 6b .. 6b+5 (head P/64, i = P%64): waves 0 and 1 dot the three lower rows
-// (i) of pairs 6b+3k .. +2, waves 2 and 3 the matching upper rows (i + 64), and
-// the scaled dots meet in LDS, where threads 0..5 rotate one pair each.
-// The row loads of all four waves are issued before any weight load (the
-// first barrier), so the RMSNorm prologue is not queued behind weight misses.
-// grid (512, count), block 256.
+// pairs each, rows head*128 + i and + 64. A workgroup owns six pairs: waves 0
+// and 1 dot the three lower rows (i) of pairs 3k .. 3k+2 of its six, waves 2
+// and 3 the matching upper rows (i + 64), and the scaled dots meet in LDS,
+// where threads 0..5 rotate one pair each. The row loads of all four waves
+// are issued before any weight load (the first barrier), so the RMSNorm
+// prologue is not queued behind weight misses.
 template <bool LUT>
-__global__ void __launch_bounds__(256)
-k_qkv_rope(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restrict__ gamma,
-    const float* __restrict__ xin, const lh_step_params* __restrict__ params,
-    float* __restrict__ qout, float* __restrict__ kcache, float* __restrict__ vcache,
-    uint32_t capacity)
+struct QkvShared {
+    float lut[LUT ? 256 : 1];
+    float4 xin[3 * 4 * 64];
+    float prod[2][6];
+    float r;
+};
+
+// Pair m of a workgroup's six: g * 6 + m in head order, or (BYKV) item
+// g * 6 + m of kv head kvh's 384 pairs (its four query heads, then its key
+// head, then its value head).
+template <bool BYKV>
+__device__ __forceinline__ uint32_t qkv_pair(uint32_t g, uint32_t kvh, uint32_t m)
+{
+    const uint32_t li = g * 6 + m;
+    if constexpr (!BYKV) {
+        return li;
+    }
+    return li < 256 ? kvh * 256 + li
+        : li < 320 ? (32 + kvh) * 64 + (li - 256) : (40 + kvh) * 64 + (li - 320);
+}
+
+template <bool LUT, bool BYKV>
+__device__ __forceinline__ void qkv_rope_body(const uint8_t* __restrict__ Wqkv, float3 scales,
+    const float* __restrict__ gamma, const float* __restrict__ xin,
+    const lh_step_params* __restrict__ params, float* __restrict__ qout,
+    float* __restrict__ kcache, float* __restrict__ vcache, uint32_t capacity, uint32_t g,
+    uint32_t kvh, uint32_t t, QkvShared<LUT>& sh)
 {
     constexpr int T = 256;
-    __shared__ float lut_s[LUT ? 256 : 1];
-    __shared__ float4 xin_s[3 * 4 * 64];
-    __shared__ float prod[2][6];
-    __shared__ float r_s;
     if constexpr (LUT) {
-        fill_lut(lut_s);  // published by the barriers below, before any dot
+        fill_lut(sh.lut);  // published by the barriers below, before any dot
     }
     const uint32_t tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
-    const uint32_t t = blockIdx.y;
     const bool upper = wave >= 2;
     const uint32_t k0 = 3 * (wave & 1);
-    const uint32_t base = blockIdx.x * 6;
     float2 xv[1536 / T], gv[1536 / T];
     norm_load<T>(xin + (size_t)t * LH_HIDDEN, gamma, xv, gv);
     __syncthreads();
     uint32_t rr[3];
 #pragma unroll
     for (int j = 0; j < 3; j++) {
-        const uint32_t pair = base + k0 + j;
+        const uint32_t pair = qkv_pair<BYKV>(g, kvh, k0 + j);
         rr[j] = (pair >> 6) * 128 + (pair & 63) + (upper ? 64 : 0);
     }
     WVec<K_FP8> wv[3][3];
     issue_rows<K_FP8, 3, 3>(Wqkv, rr, wv);
-    norm_commit<T>(xv, gv, xin_s, &r_s);
+    norm_commit<T>(xv, gv, sh.xin, &sh.r);
     float dots[3];
-    dot_rows<K_FP8, LUT, 3, 3>(wv, xin_s, lut_s, dots);
+    dot_rows<K_FP8, LUT, 3, 3>(wv, sh.xin, sh.lut, dots);
     if (lane == 0) {
 #pragma unroll
         for (int j = 0; j < 3; j++) {
-            const uint32_t head = (base + k0 + j) >> 6;
+            const uint32_t head = qkv_pair<BYKV>(g, kvh, k0 + j) >> 6;
             const float scale = head < 32 ? scales.x : (head < 40 ? scales.y : scales.z);
-            prod[upper][k0 + j] = dots[j] * scale;
+            sh.prod[upper][k0 + j] = dots[j] * scale;
         }
     }
     __syncthreads();
     if (tid < 6) {
         const lh_token_params* tp = &params->tokens[t];
         const uint32_t position = params->length + t;
-        const uint32_t pair = base + tid, head = pair >> 6, i = pair & 63;
-        const float lo = prod[0][tid];
-        const float hi = prod[1][tid];
+        const uint32_t pair = qkv_pair<BYKV>(g, kvh, tid), head = pair >> 6, i = pair & 63;
+        const float lo = sh.prod[0][tid];
+        const float hi = sh.prod[1][tid];
         if (head < 40) {
             // column i < 64 rotates with -x[i+64]; column i+64 with x[i].
             float out_lo = lo * tp->cosine[i] + (-hi) * tp->sine[i];
@@ -530,6 +546,63 @@ k_qkv_rope(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restr
             vr[i + 64] = hi;
         }
     }
+}
+
+// grid (512, count), block 256: workgroup x owns pairs 6x .. 6x+5.
+template <bool LUT>
+__global__ void __launch_bounds__(256)
+k_qkv_rope(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restrict__ gamma,
+    const float* __restrict__ xin, const lh_step_params* __restrict__ params,
+    float* __restrict__ qout, float* __restrict__ kcache, float* __restrict__ vcache,
+    uint32_t capacity)
+{
+    __shared__ QkvShared<LUT> sh;
+    qkv_rope_body<LUT, false>(Wqkv, scales, gamma, xin, params, qout, kcache, vcache, capacity,
+        blockIdx.x, 0, blockIdx.y, sh);
+}
+
+// One decode token's q|k|v projection and attention blocks in one launch
+// (src/metal_encode.m:129-153 then :154-160). Workgroups 0..511 are the q|k|v
+// projection, workgroup j * 8 + kvh owning pairs 6j .. 6j+5 of kv head kvh;
+// once its rows are stored (acknowledged by the L2) each stores its flag,
+// flags[kvh * 64 + j] = (epoch, XCD), with a plain store: an atomic per
+// workgroup on shared words costs microseconds, the flags nothing.
+// Workgroups 512 + b * 8 + kvh are attention block b of kv head kvh:
+// they load their K/V tiles while the projection streams its weights, wait
+// for their kv head's 64 producers, then load q and the new row. Ids that
+// agree mod 8 run on one XCD, so the producers' stores and the waiting blocks
+// meet in that XCD's L2. The dispatcher starts a launch's workgroups in id
+// order on each XCD, so every producer has started before any block waits.
+// COMBINE: up to 16 blocks, the last block of each kv head combines
+// (otherwise k_attn_combine follows). epoch: nonzero, new for every launch
+// on these flags. grid 512 + 8 * nblk, block 256.
+template <bool LUT, bool COMBINE>
+__global__ void __launch_bounds__(256)
+k_qkv_attn(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restrict__ gamma,
+    const float* __restrict__ xin, const lh_step_params* __restrict__ params,
+    float* __restrict__ qout, float* __restrict__ kcache, float* __restrict__ vcache,
+    uint32_t capacity, uint32_t nblk, float* __restrict__ PM, float* __restrict__ PT,
+    float* __restrict__ PA, unsigned long long* __restrict__ arrive,
+    unsigned long long* flags, unsigned long long epoch, float* __restrict__ out)
+{
+    __shared__ union {
+        QkvShared<LUT> qkv;
+        AttnShared attn;
+    } sh;
+    const uint32_t kvh = blockIdx.x & 7;
+    if (blockIdx.x < 8 * QKV_PRODUCERS) {
+        qkv_rope_body<LUT, true>(Wqkv, scales, gamma, xin, params, qout, kcache, vcache,
+            capacity, blockIdx.x >> 3, kvh, 0, sh.qkv);
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the rows are in L2
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            flags[kvh * QKV_PRODUCERS + (blockIdx.x >> 3)] = producer_flag(epoch, xcc_id());
+        }
+        return;
+    }
+    attn_block<COMBINE ? TAIL_COMBINE : TAIL_NONE, true>(qout, kcache, vcache, params, capacity,
+        nblk, PM, PT, PA, arrive, flags + kvh * QKV_PRODUCERS, epoch, out,
+        (blockIdx.x >> 3) - QKV_PRODUCERS, kvh, 0, sh.attn);
 }
 
 // RMSNorm -> gate and up rows -> SiLU(gate)*up (src/metal_encode.m:162-171).
@@ -761,6 +834,51 @@ extern "C" int lh_launch_qkv_rope(int lookup, const uint8_t* Wqkv, float sq, flo
     } else {
         hipLaunchKernelGGL(k_qkv_rope<false>, grid, dim3(256), 0, s, Wqkv, scales, gamma, x, params,
             q, kcache_layer, vcache_layer, capacity);
+    }
+    return hipGetLastError() == hipSuccess ? 0 : -1;
+}
+
+#ifndef LH_ATTN_FUSED_BLOCKS
+#define LH_ATTN_FUSED_BLOCKS LH_ATTN_FUSED_MAX   // largest block grid combined in one launch
+#endif
+
+// One decode token (count 1): the q|k|v projection and the attention blocks in
+// one launch, then k_attn_combine when the block grid exceeds
+// LH_ATTN_FUSED_BLOCKS. arrive: the blocks' 8 zeroed arrival words (left
+// zeroed); flags: the producers' 512 flags, epoch new for every launch on
+// them (nonzero). Callers check lh_attention_chained(length) first.
+extern "C" int lh_launch_qkv_attention(int lookup, const uint8_t* Wqkv, float sq, float sk,
+    float sv, const float* gamma, const float* x, const lh_step_params* params, uint32_t length,
+    float* q, float* kcache_layer, float* vcache_layer, uint32_t capacity, float* PM, float* PT,
+    float* PA, unsigned long long* arrive, unsigned long long* flags, unsigned long long epoch,
+    float* out, hipStream_t s)
+{
+    if (capacity % LH_ATTN_BLOCK || length + 1 > capacity || !arrive || !flags || !epoch) {
+        return -1;
+    }
+    const uint32_t nblk = lh_attention_blocks(length, 1);
+    const dim3 grid(8 * QKV_PRODUCERS + LH_KV_HEADS * nblk);
+    const float3 scales = make_float3(sq, sk, sv);
+    const bool combine = nblk <= LH_ATTN_FUSED_BLOCKS;
+#define LH_QKV_ATTN(L, C) hipLaunchKernelGGL((k_qkv_attn<L, C>), grid, dim3(256), 0, s, Wqkv, \
+        scales, gamma, x, params, q, kcache_layer, vcache_layer, capacity, nblk, PM, PT, PA, \
+        arrive, flags, epoch, out)
+    if (lookup) {
+        if (combine) {
+            LH_QKV_ATTN(true, true);
+        } else {
+            LH_QKV_ATTN(true, false);
+        }
+    } else {
+        if (combine) {
+            LH_QKV_ATTN(false, true);
+        } else {
+            LH_QKV_ATTN(false, false);
+        }
+    }
+#undef LH_QKV_ATTN
+    if (!combine && lh_launch_attention_combine(PM, PT, PA, params, capacity, 1, out, s)) {
+        return -1;
     }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }

@@ -794,6 +794,7 @@ static int execute(lunelette_metal *context, const int64_t *ids, size_t count, b
     if (failed || status != hipSuccess) {
         snprintf(error, capacity, "execution failed; reset required: %s",
             failed ? lh_last_error() : hipGetErrorString(status));
+        lh_workspace_clear_arrivals(rt->ws);
         return -1;
     }
     if (hipEventElapsedTime(&rt->last_ms, rt->started, rt->finished) != hipSuccess) {
@@ -807,6 +808,7 @@ static int execute(lunelette_metal *context, const int64_t *ids, size_t count, b
     const size_t bad = *rt->h_nonfinite ? lh_first_nonfinite(rt->h_logits, LH_VOCAB) : LH_VOCAB;
     if (bad < LH_VOCAB) {
         snprintf(error, capacity, "nonfinite logit %zu; reset required", bad);
+        lh_workspace_clear_arrivals(rt->ws);
         return -1;
     }
     rt->length += count;

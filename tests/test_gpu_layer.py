@@ -98,6 +98,14 @@ def test_decode_layer_short_prefix(gpu, layer_host):
         check_layer(gpu, layer_host, length, 1, 4352, [lh.PATH_FUSED])
 
 
+def test_decode_layer_one_launch_boundaries(gpu, layer_host):
+    """A decode token's q|k|v projection and attention blocks share one
+    launch; its blocks combine in that launch up to 16 blocks and through
+    k_attn_combine past it: both sides, both FP8 strategies, bitwise."""
+    for length in (1023, 1024, 2047):
+        check_layer(gpu, layer_host, length, 1, 4352, [lh.PATH_FUSED, lh.PATH_LOOKUP])
+
+
 def test_config3_prefill_chunk_precise_path(gpu, layer_host):
     check_layer(gpu, layer_host, 4096, 256, 4352, [lh.PATH_FUSED])
 
