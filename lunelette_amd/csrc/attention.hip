@@ -33,129 +33,49 @@
 
 namespace lh {
 
-constexpr uint32_t ROUND = 256;   // blocks per combine round (32 groups)
-
 // grid (8 * nblk * count): workgroup id = (t * nblk + b) * 8 + kvh, so every
 // block of a (token, kv head) group runs on one XCD (the dispatcher deals a
 // launch's workgroups to the 8 XCDs in turn, so ids that agree mod 8 share
-// one). FUSED: the last workgroup of a group to arrive combines the group's
-// four heads itself (k_attn_combine's schedule), reading the partials from
-// that XCD's L2.
-template <bool FUSED>
+// one). TAIL_COMBINE: the last workgroup of a group to arrive combines the
+// group's four heads itself (k_attn_combine's schedule), reading the
+// partials from that XCD's L2. TAIL_FLAG (one token): 128 combiner
+// workgroups follow the blocks, id 8 * nblk + (4 * (h % 4) + qd) * 8 + h / 4
+// for head h and dimension quarter qd, so each runs on its kv head's XCD and
+// combines from its L2 once the head's blocks have flagged their partials.
+template <AttnTail TAIL>
 __global__ void __launch_bounds__(256)
 k_attn_blocks(const float* __restrict__ q, const float* __restrict__ kcache,
     const float* __restrict__ vcache, const lh_step_params* __restrict__ params,
     uint32_t capacity, uint32_t nblk, float* __restrict__ PM, float* __restrict__ PT,
-    float* __restrict__ PA, unsigned long long* __restrict__ arrive, float* __restrict__ out)
+    float* __restrict__ PA, unsigned long long* __restrict__ arrive, unsigned long long* bflags,
+    unsigned long long epoch, float* __restrict__ out)
 {
-    __shared__ AttnShared sh;
-    const uint32_t kvh = blockIdx.x & 7, b = (blockIdx.x >> 3) % nblk,
-                   t = (blockIdx.x >> 3) / nblk;
-    attn_block<FUSED ? TAIL_COMBINE : TAIL_NONE, false>(q, kcache, vcache, params, capacity,
-        nblk, PM, PT, PA, arrive, nullptr, 0, out, b, kvh, t, sh);
+    __shared__ union {
+        AttnShared blocks;
+        CombineShared combine;
+    } sh;
+    const uint32_t id = blockIdx.x;
+    if (TAIL == TAIL_FLAG && id >= 8 * nblk) {
+        const uint32_t j = id - 8 * nblk, kvh = j & 7, r = j >> 3;
+        attn_combiner(PM, PT, PA, params, capacity, bflags + kvh * (capacity / LH_ATTN_BLOCK),
+            epoch, kvh * 4 + (r >> 2), r & 3, out, sh.combine);
+        return;
+    }
+    const uint32_t kvh = id & 7, b = (id >> 3) % nblk, t = (id >> 3) / nblk;
+    attn_block<TAIL, false>(q, kcache, vcache, params, capacity, nblk, PM, PT, PA, arrive, nullptr,
+        bflags, epoch, out, b, kvh, t, sh.blocks);
 }
 
-// grid (32 heads x 4 dimension quarters, count), 256 threads: thread
-// (c = tid & 7, s = tid >> 3) owns dims 32q + 4c .. +3 of group s of each
-// 256-block round; every quarter recomputes M and the block factors, so the
-// four workgroups of a head are independent. Bitwise the schedule above (the
-// dims never mix; groups start at multiples of 8 from block 0 and add left
-// to right across rounds).
+// grid (32 heads x 4 dimension quarters, count), 256 threads (attn_combine).
 __global__ void __launch_bounds__(256)
 k_attn_combine(const float* __restrict__ PM, const float* __restrict__ PT,
     const float* __restrict__ PA, const lh_step_params* __restrict__ params, uint32_t capacity,
     float* __restrict__ out)
 {
-    __shared__ float wmax[4];
-    __shared__ float fs[ROUND], ts[ROUND];
-    __shared__ float4 sg[ROUND / GROUP][8];
-    __shared__ float ug[ROUND / GROUP];
-    const uint32_t h = blockIdx.x >> 2, qd = blockIdx.x & 3, t = blockIdx.y;
-    const uint32_t nbc = capacity / LH_ATTN_BLOCK;
-    const size_t th = (size_t)t * LH_HEADS + h;
-    const float* pm = PM + th * nbc;
-    const float* pt = PT + th * nbc;
-    const uint32_t tid = threadIdx.x, c = tid & 7, s = tid >> 3;
-    const float4* pa = reinterpret_cast<const float4*>(PA + th * nbc * LH_HEAD_DIM) + 8 * qd + c;
-    // A round's partial loads are clamped to the capacity, not to the valid
-    // block count, so the first round's issue before the step record is
-    // read; rows past the valid count never enter arithmetic.
-    float4 a[GROUP];
-    float m_own, t_own;
-    auto load_round = [&](uint32_t r0) {
-#pragma unroll
-        for (uint32_t k = 0; k < GROUP; k++) {
-            const uint32_t bb = r0 + s * GROUP + k;
-            a[k] = pa[(size_t)(bb < nbc ? bb : nbc - 1) * (LH_HEAD_DIM / 4)];
-        }
-        const uint32_t bb = r0 + tid < nbc ? r0 + tid : nbc - 1;
-        m_own = pm[bb];
-        t_own = pt[bb];
-    };
-    load_round(0);
-    const uint32_t n = params->length + t + 1;
-    const uint32_t nb = (n + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
-    float M = tid < nb ? m_own : -__builtin_inff();
-    for (uint32_t j = tid + ROUND; j < nb; j += ROUND) {
-        M = fmaxf(M, pm[j]);
-    }
-    M = wave_max64(M);
-    if ((tid & 63) == 0) {
-        wmax[tid >> 6] = M;
-    }
-    __syncthreads();
-    M = fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3]));
-    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-    float T = 0.0f;
-    for (uint32_t r0 = 0; r0 < nb; r0 += ROUND) {
-        if (r0) {
-            load_round(r0);
-        }
-        {
-            const uint32_t bb = r0 + tid;
-            fs[tid] = bb < nb ? expf_cw(m_own - M) : 0.0f;
-            ts[tid] = bb < nb ? t_own : 0.0f;
-        }
-        __syncthreads();
-        float4 Sg = make_float4(0.f, 0.f, 0.f, 0.f);
-        float Ug = 0.0f;
-#pragma unroll
-        for (uint32_t k = 0; k < GROUP; k++) {
-            if (r0 + s * GROUP + k < nb) {
-                const float f = fs[s * GROUP + k];
-                Sg.x = __builtin_fmaf(f, a[k].x, Sg.x);
-                Sg.y = __builtin_fmaf(f, a[k].y, Sg.y);
-                Sg.z = __builtin_fmaf(f, a[k].z, Sg.z);
-                Sg.w = __builtin_fmaf(f, a[k].w, Sg.w);
-                Ug = __builtin_fmaf(f, ts[s * GROUP + k], Ug);
-            }
-        }
-        sg[s][c] = Sg;
-        if (c == 0) {
-            ug[s] = Ug;
-        }
-        __syncthreads();
-        if (tid < 8) {
-            for (uint32_t g = 0; g < ROUND / GROUP && r0 + g * GROUP < nb; g++) {
-                const float4 v = sg[g][c];
-                if (r0 == 0 && g == 0) {
-                    A = v;
-                    T = ug[0];
-                } else {
-                    A.x = A.x + v.x;
-                    A.y = A.y + v.y;
-                    A.z = A.z + v.z;
-                    A.w = A.w + v.w;
-                    T = T + ug[g];
-                }
-            }
-        }
-        __syncthreads();
-    }
-    if (tid < 8) {
-        reinterpret_cast<float4*>(out + (size_t)t * LH_QUERY + h * LH_HEAD_DIM)[8 * qd + c] =
-            make_float4(A.x / T, A.y / T, A.z / T, A.w / T);
-    }
+    __shared__ CombineShared sh;
+    const uint32_t t = blockIdx.y;
+    attn_combine(PM, PT, PA, params->length + t + 1, capacity, blockIdx.x >> 2, blockIdx.x & 3,
+        t, out, sh);
 }
 
 // Embedding gather with exact BF16 widening (src/metal_runtime.m:388-395 copies
@@ -300,36 +220,35 @@ extern "C" int lh_attention_chained(uint32_t length)
     return lh_attention_blocks(length, 1) <= LH_CHAIN_MAX_BLOCKS && fused_attention_ok();
 }
 
-extern "C" int lh_launch_attention_combine(const float* PM, const float* PT, const float* PA,
-    const lh_step_params* params, uint32_t capacity, uint32_t count, float* out, hipStream_t s)
-{
-    hipLaunchKernelGGL(k_attn_combine, dim3(LH_HEADS * 4, count), dim3(256), 0, s, PM, PT, PA,
-        params, capacity, out);
-    return hipGetLastError() == hipSuccess ? 0 : -1;
-}
-
 // The kernels read the step length from params (device memory); `length`
-// here must equal params->length and only sizes the block grid. With arrive
-// set (count * 8 zeroed arrival words, ARRIVE_STRIDE 64-bit words apart, left
-// zeroed) and a block grid of at most
-// LH_ATTN_FUSED_BLOCKS on a device whose dispatch the probe confirmed, one
-// launch does the blocks and the combine; otherwise two.
+// here must equal params->length and only sizes the block grid. On a device
+// whose dispatch the probe confirmed, with arrive set (count * 8 zeroed
+// arrival words, ARRIVE_STRIDE 64-bit words apart, left zeroed) a block grid
+// of at most LH_ATTN_FUSED_BLOCKS combines in its own launch; with bflags
+// set (8 * capacity/64 words; epoch nonzero and new for every launch on them)
+// one token's longer grid runs its blocks and combiners in one launch;
+// otherwise blocks and k_attn_combine run as two launches.
 extern "C" int lh_launch_attention(const float* q, const float* kcache_layer,
     const float* vcache_layer, const lh_step_params* params, uint32_t length, uint32_t count,
-    uint32_t capacity, float* PM, float* PT, float* PA, unsigned long long* arrive, float* out,
-    hipStream_t s)
+    uint32_t capacity, float* PM, float* PT, float* PA, unsigned long long* arrive,
+    unsigned long long* bflags, unsigned long long epoch, float* out, hipStream_t s)
 {
     if (!count || capacity % LH_ATTN_BLOCK || length + count > capacity) {
         return -1;
     }
     const uint32_t nblk = lh_attention_blocks(length, count);
     const dim3 grid(LH_KV_HEADS * nblk * count);
-    if (arrive && nblk <= LH_ATTN_FUSED_BLOCKS && fused_attention_ok()) {
-        hipLaunchKernelGGL(k_attn_blocks<true>, grid, dim3(256), 0, s, q, kcache_layer,
-            vcache_layer, params, capacity, nblk, PM, PT, PA, arrive, out);
+    const bool ok = fused_attention_ok();
+    if (ok && arrive && nblk <= LH_ATTN_FUSED_BLOCKS) {
+        hipLaunchKernelGGL(k_attn_blocks<TAIL_COMBINE>, grid, dim3(256), 0, s, q, kcache_layer,
+            vcache_layer, params, capacity, nblk, PM, PT, PA, arrive, nullptr, 0ull, out);
+    } else if (ok && bflags && epoch && count == 1) {
+        hipLaunchKernelGGL(k_attn_blocks<TAIL_FLAG>, dim3(LH_KV_HEADS * nblk + LH_HEADS * 4),
+            dim3(256), 0, s, q, kcache_layer, vcache_layer, params, capacity, nblk, PM, PT, PA,
+            nullptr, bflags, epoch, out);
     } else {
-        hipLaunchKernelGGL(k_attn_blocks<false>, grid, dim3(256), 0, s, q, kcache_layer,
-            vcache_layer, params, capacity, nblk, PM, PT, PA, nullptr, nullptr);
+        hipLaunchKernelGGL(k_attn_blocks<TAIL_NONE>, grid, dim3(256), 0, s, q, kcache_layer,
+            vcache_layer, params, capacity, nblk, PM, PT, PA, nullptr, nullptr, 0ull, nullptr);
         hipLaunchKernelGGL(k_attn_combine, dim3(LH_HEADS * 4, count), dim3(256), 0, s, PM, PT, PA,
             params, capacity, out);
     }
@@ -403,7 +322,7 @@ extern "C" int lh_attention_noalloc(const float* d_q, const float* d_keys, const
         (uint32_t)count);
     if (hipGetLastError() != hipSuccess ||
         lh_launch_attention(d_q, d_keys, d_values, params, (uint32_t)length, (uint32_t)count,
-            (uint32_t)capacity, PM, PT, PA, nullptr, d_out, s)) {
+            (uint32_t)capacity, PM, PT, PA, nullptr, nullptr, 0ull, d_out, s)) {
         lh_set_error("attention_noalloc: launch failed");
         return -1;
     }

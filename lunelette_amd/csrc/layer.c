@@ -67,7 +67,9 @@ lh_workspace *lh_workspace_create(size_t capacity, size_t block)
         alloc_device((void **)&ws->d_PA, B * LH_HEADS * nbc * LH_HEAD_DIM * sizeof(float),
             &ws->bytes) ||
         alloc_device((void **)&ws->d_arrive, ARRIVE_WORDS(B) * 8, &ws->bytes) ||
-        check(hipMemset(ws->d_arrive, 0, ARRIVE_WORDS(B) * 8), "workspace clear")) {
+        check(hipMemset(ws->d_arrive, 0, ARRIVE_WORDS(B) * 8), "workspace clear") ||
+        alloc_device((void **)&ws->d_bflags, LH_KV_HEADS * nbc * 8, &ws->bytes) ||
+        check(hipMemset(ws->d_bflags, 0, LH_KV_HEADS * nbc * 8), "workspace clear")) {
         lh_workspace_destroy(ws);
         return NULL;
     }
@@ -83,10 +85,13 @@ lh_workspace *lh_workspace_create(size_t capacity, size_t block)
 
 int lh_workspace_clear_arrivals(lh_workspace *ws)
 {
-    if (!ws || !ws->d_arrive) {
+    if (!ws || !ws->d_arrive || !ws->d_bflags) {
         return -1;
     }
-    return check(hipMemset(ws->d_arrive, 0, ARRIVE_WORDS(ws->block) * 8), "arrival words clear");
+    ws->epoch = 0;
+    return check(hipMemset(ws->d_arrive, 0, ARRIVE_WORDS(ws->block) * 8), "arrival words clear") ||
+        check(hipMemset(ws->d_bflags, 0, LH_KV_HEADS * (ws->capacity / LH_ATTN_BLOCK) * 8),
+            "block flags clear");
 }
 
 void lh_workspace_destroy(lh_workspace *ws)
@@ -96,6 +101,7 @@ void lh_workspace_destroy(lh_workspace *ws)
     }
     void *device[] = {ws->d_params, ws->d_q, ws->d_attn, ws->d_gated, ws->d_up, ws->d_xn,
         ws->d_qraw, ws->d_kraw, ws->d_vraw, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_arrive,
+        ws->d_bflags,
         ws->d_split, ws->d_gemm, ws->d_yarn};
     for (size_t i = 0; i < sizeof device / sizeof device[0]; i++) {
         lh_dev_free(device[i]);
@@ -257,7 +263,7 @@ static int layer_unfused(const lh_layer_weights *w, float *x, float *keys, float
         launched(lh_launch_rope_append(ws->d_qraw, ws->d_kraw, ws->d_vraw, params, n, ws->d_q,
             keys, values, C, s), "rope/append") ||
         launched(lh_launch_attention(ws->d_q, keys, values, ws->d_params, (uint32_t)ws->length, n,
-            C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_arrive, ws->d_attn, s),
+            C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_arrive, ws->d_bflags, ++ws->epoch, ws->d_attn, s),
             "attention") ||
         launched(lh_launch_matvec(kind, 0, wo, w->scale[3], ws->d_attn, x, x, LH_HIDDEN,
             LH_QUERY, n, s), "o") ||
@@ -286,13 +292,13 @@ static int layer_fused(const lh_layer_weights *w, float *x, float *keys, float *
             launched(lh_launch_qkv_attention(lookup, w->qkv, w->scale[0], w->scale[1],
                 w->scale[2], w->input_norm, x, params, (uint32_t)ws->length, ws->d_q, keys,
                 values, C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_arrive,
-                ws->d_arrive + FLAGS_WORD(ws->block), ++ws->epoch, ws->d_attn, s),
+                ws->d_arrive + FLAGS_WORD(ws->block), ws->d_bflags, ++ws->epoch, ws->d_attn, s),
                 "qkv/attention") :
             launched(lh_launch_qkv_rope(lookup, w->qkv, w->scale[0], w->scale[1], w->scale[2],
                 w->input_norm, x, params, n, ws->d_q, keys, values, C, s), "qkv") ||
             launched(lh_launch_attention(ws->d_q, keys, values, ws->d_params,
                 (uint32_t)ws->length, n, C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_arrive,
-                ws->d_attn, s), "attention")) ||
+                ws->d_bflags, ++ws->epoch, ws->d_attn, s), "attention")) ||
         launched(lh_launch_matvec(0, lookup, w->o, w->scale[3], ws->d_attn, x, x, LH_HIDDEN,
             LH_QUERY, n, s), "o") ||
         launched(lh_launch_gateup_silu(lookup, w->gate, w->up, w->scale[4], w->scale[5],
@@ -319,7 +325,7 @@ int lh_layer_operator(int op, const lh_layer_weights *w, float *d_x, float *d_ke
             w->input_norm, d_x, ws->d_params, n, ws->d_q, d_keys, d_values, C, s), "qkv");
     case LH_OP_ATTENTION:
         return launched(lh_launch_attention(ws->d_q, d_keys, d_values, ws->d_params, (uint32_t)ws->length, n,
-            C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_arrive, ws->d_attn, s),
+            C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_arrive, ws->d_bflags, ++ws->epoch, ws->d_attn, s),
             "attention");
     case LH_OP_O_RESIDUAL:
         return launched(lh_launch_matvec(0, 0, w->o, w->scale[3], ws->d_attn, d_x, d_x, LH_HIDDEN,
@@ -374,7 +380,8 @@ int lh_attention(const float *d_q, const float *d_keys, const float *d_values, l
     }
     return launched(lh_launch_attention(d_q, d_keys, d_values, ws->d_params,
         (uint32_t)ws->length, (uint32_t)ws->count, (uint32_t)ws->capacity, ws->d_PM, ws->d_PT,
-        ws->d_PA, ws->d_arrive, d_out, (hipStream_t)stream), "attention");
+        ws->d_PA, ws->d_arrive, ws->d_bflags, ++ws->epoch, d_out, (hipStream_t)stream),
+        "attention");
 }
 
 int lh_attention_mfma(const float *d_q, const float *d_keys, const float *d_values,

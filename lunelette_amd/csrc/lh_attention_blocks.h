@@ -65,6 +65,149 @@ __device__ __forceinline__ uint32_t arrivals(unsigned long long word)
     return total;
 }
 
+constexpr uint32_t ROUND = 256;   // blocks per combine round (32 groups)
+
+struct CombineShared {
+    float wmax[4];
+    float fs[ROUND], ts[ROUND];
+    float4 sg[ROUND / GROUP][8];
+    float ug[ROUND / GROUP];
+};
+
+// The combine of head h, dimension quarter qd, token t over the n positions
+// (0..n-1): thread (c = tid & 7, s = tid >> 3) owns dims 32qd + 4c .. +3 of
+// group s of each 256-block round; every quarter recomputes M and the block
+// factors, so the four workgroups of a head are independent. Bitwise the
+// schedule above (the dims never mix; groups start at multiples of 8 from
+// block 0 and add left to right across rounds).
+__device__ __forceinline__ void attn_combine(const float* __restrict__ PM,
+    const float* __restrict__ PT, const float* __restrict__ PA, uint32_t n, uint32_t capacity,
+    uint32_t h, uint32_t qd, uint32_t t, float* __restrict__ out, CombineShared& sh)
+{
+    const uint32_t nbc = capacity / LH_ATTN_BLOCK;
+    const size_t th = (size_t)t * LH_HEADS + h;
+    const float* pm = PM + th * nbc;
+    const float* pt = PT + th * nbc;
+    const uint32_t tid = threadIdx.x, c = tid & 7, s = tid >> 3;
+    const float4* pa = reinterpret_cast<const float4*>(PA + th * nbc * LH_HEAD_DIM) + 8 * qd + c;
+    // A round's partial loads are clamped to the capacity, not to the valid
+    // block count, so the first round's issue before the step record is
+    // read; rows past the valid count never enter arithmetic.
+    float4 a[GROUP];
+    float m_own, t_own;
+    auto load_round = [&](uint32_t r0) {
+#pragma unroll
+        for (uint32_t k = 0; k < GROUP; k++) {
+            const uint32_t bb = r0 + s * GROUP + k;
+            a[k] = pa[(size_t)(bb < nbc ? bb : nbc - 1) * (LH_HEAD_DIM / 4)];
+        }
+        const uint32_t bb = r0 + tid < nbc ? r0 + tid : nbc - 1;
+        m_own = pm[bb];
+        t_own = pt[bb];
+    };
+    load_round(0);
+    const uint32_t nb = (n + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
+    float M = tid < nb ? m_own : -__builtin_inff();
+    for (uint32_t j = tid + ROUND; j < nb; j += ROUND) {
+        M = fmaxf(M, pm[j]);
+    }
+    M = wave_max64(M);
+    if ((tid & 63) == 0) {
+        sh.wmax[tid >> 6] = M;
+    }
+    __syncthreads();
+    M = fmaxf(fmaxf(sh.wmax[0], sh.wmax[1]), fmaxf(sh.wmax[2], sh.wmax[3]));
+    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+    float T = 0.0f;
+    for (uint32_t r0 = 0; r0 < nb; r0 += ROUND) {
+        if (r0) {
+            load_round(r0);
+        }
+        {
+            const uint32_t bb = r0 + tid;
+            sh.fs[tid] = bb < nb ? expf_cw(m_own - M) : 0.0f;
+            sh.ts[tid] = bb < nb ? t_own : 0.0f;
+        }
+        __syncthreads();
+        float4 Sg = make_float4(0.f, 0.f, 0.f, 0.f);
+        float Ug = 0.0f;
+#pragma unroll
+        for (uint32_t k = 0; k < GROUP; k++) {
+            if (r0 + s * GROUP + k < nb) {
+                const float f = sh.fs[s * GROUP + k];
+                Sg.x = __builtin_fmaf(f, a[k].x, Sg.x);
+                Sg.y = __builtin_fmaf(f, a[k].y, Sg.y);
+                Sg.z = __builtin_fmaf(f, a[k].z, Sg.z);
+                Sg.w = __builtin_fmaf(f, a[k].w, Sg.w);
+                Ug = __builtin_fmaf(f, sh.ts[s * GROUP + k], Ug);
+            }
+        }
+        sh.sg[s][c] = Sg;
+        if (c == 0) {
+            sh.ug[s] = Ug;
+        }
+        __syncthreads();
+        if (tid < 8) {
+            for (uint32_t g = 0; g < ROUND / GROUP && r0 + g * GROUP < nb; g++) {
+                const float4 v = sh.sg[g][c];
+                if (r0 == 0 && g == 0) {
+                    A = v;
+                    T = sh.ug[0];
+                } else {
+                    A.x = A.x + v.x;
+                    A.y = A.y + v.y;
+                    A.z = A.z + v.z;
+                    A.w = A.w + v.w;
+                    T = T + sh.ug[g];
+                }
+            }
+        }
+        __syncthreads();
+    }
+    if (tid < 8) {
+        reinterpret_cast<float4*>(out + (size_t)t * LH_QUERY + h * LH_HEAD_DIM)[8 * qd + c] =
+            make_float4(A.x / T, A.y / T, A.z / T, A.w / T);
+    }
+}
+
+// Combiner workgroup of a one-token launch whose blocks (kv head h / 4, on
+// this workgroup's XCD) each store bflags[b] = epoch once their partials are
+// acknowledged: waits (bounded; polls by volatile loads, which miss the L1)
+// until the first nb flags carry the epoch, then combines from the XCD's L2
+// (no workgroup loaded the partials before in this launch, so this CU's L1
+// holds none of their lines). If it gives up it writes NaN.
+__device__ __forceinline__ void attn_combiner(const float* __restrict__ PM,
+    const float* __restrict__ PT, const float* __restrict__ PA,
+    const lh_step_params* __restrict__ params, uint32_t capacity,
+    const unsigned long long* bflags, unsigned long long epoch, uint32_t h, uint32_t qd,
+    float* __restrict__ out, CombineShared& sh)
+{
+    const uint32_t n = params->length + 1;
+    const uint32_t nb = (n + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
+    const volatile unsigned long long* f = bflags;
+    bool ready = false;
+    for (uint32_t spin = 0; spin < SPIN_LIMIT; spin++) {
+        int mine = 1;
+        for (uint32_t b = threadIdx.x; b < nb; b += 256) {
+            mine &= f[b] == epoch;
+        }
+        if (__syncthreads_and(mine)) {
+            ready = true;
+            break;
+        }
+        __builtin_amdgcn_s_sleep(2);
+    }
+    if (!ready) {
+        if (threadIdx.x < 8) {
+            const float nan = __builtin_nanf("");
+            reinterpret_cast<float4*>(out + h * LH_HEAD_DIM)[8 * qd + threadIdx.x] =
+                make_float4(nan, nan, nan, nan);
+        }
+        return;
+    }
+    attn_combine(PM, PT, PA, n, capacity, h, qd, 0, out, sh);
+}
+
 // LDS of one block workgroup: one 32 KiB tile region holds K for the scores,
 // then V for the P.V chains.
 struct AttnShared {
@@ -76,8 +219,9 @@ struct AttnShared {
 
 // What follows a block's partials. NONE: nothing (k_attn_combine follows).
 // COMBINE: the last workgroup of the (token, kv head) group to arrive
-// combines.
-enum AttnTail { TAIL_NONE = 0, TAIL_COMBINE = 1 };
+// combines. FLAG (one token): once its partial stores are acknowledged the
+// block stores bflags[b] = epoch for the combiners of its kv head.
+enum AttnTail { TAIL_NONE = 0, TAIL_COMBINE = 1, TAIL_FLAG = 2 };
 
 // The hand-off of a one-launch group. Each workgroup waits until its partial
 // stores are acknowledged (the vector L1 writes through, so they are in its
@@ -206,8 +350,8 @@ __device__ __forceinline__ void attn_block(const float* __restrict__ q,
     const lh_step_params* __restrict__ params, uint32_t capacity, uint32_t nblk,
     float* __restrict__ PM, float* __restrict__ PT, float* __restrict__ PA,
     unsigned long long* __restrict__ arrive, const unsigned long long* flags,
-    unsigned long long epoch, float* __restrict__ out, uint32_t b, uint32_t kvh, uint32_t t,
-    AttnShared& sh)
+    unsigned long long* bflags, unsigned long long epoch, float* __restrict__ out, uint32_t b,
+    uint32_t kvh, uint32_t t, AttnShared& sh)
 {
     float4* T = sh.T;
     const uint64_t tile = lh_kv_index(capacity, 0, kvh, (uint64_t)b * LH_ATTN_BLOCK);
@@ -399,8 +543,15 @@ __device__ __forceinline__ void attn_block(const float* __restrict__ q,
         *reinterpret_cast<float2*>(PA + (th * nbc + b) * LH_HEAD_DIM + d0) =
             fed ? make_float2(a0, a1) : make_float2(nan, nan);
     }
-    if constexpr (TAIL != TAIL_NONE) {
+    if constexpr (TAIL == TAIL_COMBINE) {
         attn_block_tail<TAIL>(PM, PT, PA, arrive, out, t, kvh, nblk, nbc, n, sh.verdict);
+    }
+    if constexpr (TAIL == TAIL_FLAG) {
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        __syncthreads();
+        if (tid == 0) {
+            bflags[kvh * nbc + b] = epoch;
+        }
     }
 }
 

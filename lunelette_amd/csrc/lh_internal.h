@@ -30,23 +30,21 @@ int lh_launch_rmsnorm(const float *gamma, const float *x, float *out, uint32_t w
  * params->length) sizes the block grid only. */
 int lh_launch_attention(const float *q, const float *kcache_layer, const float *vcache_layer,
     const lh_step_params *params, uint32_t length, uint32_t count, uint32_t capacity, float *PM,
-    float *PT, float *PA, unsigned long long *arrive, float *out, hipStream_t s);
-/* The combine of lh_launch_attention's two-launch form, on its own. */
-int lh_launch_attention_combine(const float *PM, const float *PT, const float *PA,
-    const lh_step_params *params, uint32_t capacity, uint32_t count, float *out, hipStream_t s);
+    float *PT, float *PA, unsigned long long *arrive, unsigned long long *bflags,
+    unsigned long long epoch, float *out, hipStream_t s);
 /* Whether a decode token at this length runs q|k|v and its attention blocks
  * in one launch on the current device (its dispatch probed). */
 int lh_attention_chained(uint32_t length);
-/* One decode token: RMSNorm -> q|k|v -> RoPE -> KV append and the attention
- * blocks in one launch (plus k_attn_combine past 16 blocks); arrive: the
- * blocks' arrival words (zeroed, left zeroed); flags: 512 words of producer
- * flags, epoch nonzero and new for every launch on them. Needs
+/* One decode token: RMSNorm -> q|k|v -> RoPE -> KV append, the attention
+ * blocks and their combine in one launch; arrive: the blocks' arrival words
+ * (zeroed, left zeroed); flags: 512 producer flags; bflags: 8 * capacity/64
+ * block flags; epoch nonzero and new for every launch on them. Needs
  * lh_attention_chained(length). */
 int lh_launch_qkv_attention(int lookup, const uint8_t *Wqkv, float sq, float sk, float sv,
     const float *gamma, const float *x, const lh_step_params *params, uint32_t length, float *q,
     float *kcache_layer, float *vcache_layer, uint32_t capacity, float *PM, float *PT, float *PA,
-    unsigned long long *arrive, unsigned long long *flags, unsigned long long epoch, float *out,
-    hipStream_t s);
+    unsigned long long *arrive, unsigned long long *flags, unsigned long long *bflags,
+    unsigned long long epoch, float *out, hipStream_t s);
 /* Records once per device whether a launch's workgroups whose ids agree mod 8
  * run on one XCD (five probe launches into d_words, at least 2048 words, left
  * zeroed); *ok receives the verdict. A fused attention launch needs it. */

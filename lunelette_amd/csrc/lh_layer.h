@@ -23,7 +23,8 @@ struct lh_workspace {
     float *d_PA;                   /* [B][32][C/64][128] block P.V partials */
     unsigned long long *d_arrive;  /* one-launch attention: B * 8 arrival words 256 B apart,
                                       then 512 producer flags (ARRIVE_WORDS) */
-    unsigned long long epoch;      /* last epoch stored in the producer flags */
+    unsigned long long *d_bflags;  /* [8][C/64] block flags of one-launch long attention */
+    unsigned long long epoch;      /* last epoch stored in the producer and block flags */
     float *d_yarn;                 /* [C][128]: cos[64], sin[64] per position (decode) */
     float *h_yarn;                 /* host copy of the same rows, filled on first use */
     uint8_t *h_yarn_ready;         /* [C]: row p of h_yarn holds lh_yarn(p) */

@@ -573,9 +573,11 @@ k_qkv_rope(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restr
 // agree mod 8 run on one XCD, so the producers' stores and the waiting blocks
 // meet in that XCD's L2. The dispatcher starts a launch's workgroups in id
 // order on each XCD, so every producer has started before any block waits.
-// COMBINE: up to 16 blocks, the last block of each kv head combines
-// (otherwise k_attn_combine follows). epoch: nonzero, new for every launch
-// on these flags. grid 512 + 8 * nblk, block 256.
+// COMBINE: up to 16 blocks, the last block of each kv head combines;
+// otherwise each block flags its partials in bflags and 128 combiner
+// workgroups follow the blocks (id 512 + 8 * nblk + (4 * (h % 4) + qd) * 8 +
+// h / 4, on kv head h / 4's XCD). epoch: nonzero, new for every launch on
+// these flags. grid 512 + 8 * nblk (+ 128), block 256.
 template <bool LUT, bool COMBINE>
 __global__ void __launch_bounds__(256)
 k_qkv_attn(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restrict__ gamma,
@@ -583,13 +585,21 @@ k_qkv_attn(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restr
     float* __restrict__ qout, float* __restrict__ kcache, float* __restrict__ vcache,
     uint32_t capacity, uint32_t nblk, float* __restrict__ PM, float* __restrict__ PT,
     float* __restrict__ PA, unsigned long long* __restrict__ arrive,
-    unsigned long long* flags, unsigned long long epoch, float* __restrict__ out)
+    unsigned long long* flags, unsigned long long* bflags, unsigned long long epoch,
+    float* __restrict__ out)
 {
     __shared__ union {
         QkvShared<LUT> qkv;
         AttnShared attn;
+        CombineShared combine;
     } sh;
     const uint32_t kvh = blockIdx.x & 7;
+    if (!COMBINE && blockIdx.x >= 8 * (QKV_PRODUCERS + nblk)) {
+        const uint32_t r = (blockIdx.x - 8 * (QKV_PRODUCERS + nblk)) >> 3;
+        attn_combiner(PM, PT, PA, params, capacity, bflags + kvh * (capacity / LH_ATTN_BLOCK),
+            epoch, kvh * 4 + (r >> 2), r & 3, out, sh.combine);
+        return;
+    }
     if (blockIdx.x < 8 * QKV_PRODUCERS) {
         qkv_rope_body<LUT, true>(Wqkv, scales, gamma, xin, params, qout, kcache, vcache,
             capacity, blockIdx.x >> 3, kvh, 0, sh.qkv);
@@ -600,8 +610,8 @@ k_qkv_attn(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restr
         }
         return;
     }
-    attn_block<COMBINE ? TAIL_COMBINE : TAIL_NONE, true>(qout, kcache, vcache, params, capacity,
-        nblk, PM, PT, PA, arrive, flags + kvh * QKV_PRODUCERS, epoch, out,
+    attn_block<COMBINE ? TAIL_COMBINE : TAIL_FLAG, true>(qout, kcache, vcache, params, capacity,
+        nblk, PM, PT, PA, arrive, flags + kvh * QKV_PRODUCERS, bflags, epoch, out,
         (blockIdx.x >> 3) - QKV_PRODUCERS, kvh, 0, sh.attn);
 }
 
@@ -842,27 +852,28 @@ extern "C" int lh_launch_qkv_rope(int lookup, const uint8_t* Wqkv, float sq, flo
 #define LH_ATTN_FUSED_BLOCKS LH_ATTN_FUSED_MAX   // largest block grid combined in one launch
 #endif
 
-// One decode token (count 1): the q|k|v projection and the attention blocks in
-// one launch, then k_attn_combine when the block grid exceeds
-// LH_ATTN_FUSED_BLOCKS. arrive: the blocks' 8 zeroed arrival words (left
-// zeroed); flags: the producers' 512 flags, epoch new for every launch on
-// them (nonzero). Callers check lh_attention_chained(length) first.
+// One decode token (count 1): the q|k|v projection, the attention blocks and
+// their combine in one launch. arrive: the blocks' 8 zeroed arrival words
+// (left zeroed); flags: the producers' 512 flags; bflags: 8 * capacity/64
+// block flags; epoch new for every launch on them (nonzero). Callers check
+// lh_attention_chained(length) first.
 extern "C" int lh_launch_qkv_attention(int lookup, const uint8_t* Wqkv, float sq, float sk,
     float sv, const float* gamma, const float* x, const lh_step_params* params, uint32_t length,
     float* q, float* kcache_layer, float* vcache_layer, uint32_t capacity, float* PM, float* PT,
-    float* PA, unsigned long long* arrive, unsigned long long* flags, unsigned long long epoch,
-    float* out, hipStream_t s)
+    float* PA, unsigned long long* arrive, unsigned long long* flags, unsigned long long* bflags,
+    unsigned long long epoch, float* out, hipStream_t s)
 {
-    if (capacity % LH_ATTN_BLOCK || length + 1 > capacity || !arrive || !flags || !epoch) {
+    if (capacity % LH_ATTN_BLOCK || length + 1 > capacity || !arrive || !flags || !bflags ||
+        !epoch) {
         return -1;
     }
     const uint32_t nblk = lh_attention_blocks(length, 1);
-    const dim3 grid(8 * QKV_PRODUCERS + LH_KV_HEADS * nblk);
-    const float3 scales = make_float3(sq, sk, sv);
     const bool combine = nblk <= LH_ATTN_FUSED_BLOCKS;
+    const dim3 grid(8 * QKV_PRODUCERS + LH_KV_HEADS * nblk + (combine ? 0 : LH_HEADS * 4));
+    const float3 scales = make_float3(sq, sk, sv);
 #define LH_QKV_ATTN(L, C) hipLaunchKernelGGL((k_qkv_attn<L, C>), grid, dim3(256), 0, s, Wqkv, \
         scales, gamma, x, params, q, kcache_layer, vcache_layer, capacity, nblk, PM, PT, PA, \
-        arrive, flags, epoch, out)
+        arrive, flags, bflags, epoch, out)
     if (lookup) {
         if (combine) {
             LH_QKV_ATTN(true, true);
@@ -877,9 +888,6 @@ extern "C" int lh_launch_qkv_attention(int lookup, const uint8_t* Wqkv, float sq
         }
     }
 #undef LH_QKV_ATTN
-    if (!combine && lh_launch_attention_combine(PM, PT, PA, params, capacity, 1, out, s)) {
-        return -1;
-    }
     return hipGetLastError() == hipSuccess ? 0 : -1;
 }
 
