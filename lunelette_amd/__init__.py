@@ -107,6 +107,7 @@ def test_lib():
         _proto(l, "lunelette_metal_test_fail_after_layer", i, c_void, ctypes.c_uint32)
         _proto(l, "lunelette_metal_test_set_epoch", i, c_void, ctypes.c_uint64)
         _proto(l, "lunelette_metal_test_set_logit", i, c_void, c_size, f)
+        _proto(l, "lunelette_metal_test_chained", i, ctypes.c_uint32)
         _proto(l, "lunelette_metal_test_fail_allocation", None, ctypes.c_uint)
         _proto(l, "lunelette_metal_test_allocations", ctypes.c_uint)
         _proto(l, "lunelette_metal_test_live_allocations", ctypes.c_long)

@@ -63,7 +63,7 @@ k_attn_blocks(const float* __restrict__ q, const float* __restrict__ kcache,
     }
     const uint32_t kvh = id & 7, b = (id >> 3) % nblk, t = (id >> 3) / nblk;
     attn_block<TAIL, false>(q, kcache, vcache, params, capacity, nblk, PM, PT, PA, arrive, nullptr,
-        bflags, epoch, out, b, kvh, t, sh.blocks);
+        bflags, epoch, 0, 0, out, b, kvh, t, sh.blocks);
 }
 
 // grid (32 heads x 4 dimension quarters, count), 256 threads (attn_combine).

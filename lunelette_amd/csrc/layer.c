@@ -292,7 +292,8 @@ static int layer_fused(const lh_layer_weights *w, float *x, float *keys, float *
             launched(lh_launch_qkv_attention(lookup, w->qkv, w->scale[0], w->scale[1],
                 w->scale[2], w->input_norm, x, params, (uint32_t)ws->length, ws->d_q, keys,
                 values, C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_arrive,
-                ws->d_arrive + FLAGS_WORD(ws->block), ws->d_bflags, ++ws->epoch, ws->d_attn, s),
+                ws->d_arrive + FLAGS_WORD(ws->block), ws->d_bflags, ++ws->epoch,
+                ws->handoff_fault, ws->d_attn, s),
                 "qkv/attention") :
             launched(lh_launch_qkv_rope(lookup, w->qkv, w->scale[0], w->scale[1], w->scale[2],
                 w->input_norm, x, params, n, ws->d_q, keys, values, C, s), "qkv") ||

@@ -340,18 +340,19 @@ __device__ __forceinline__ void attn_block_tail(const float* __restrict__ PM,
 // CHAINED (one decode token, t = 0): q and the current position's K and V rows
 // are written in the same launch by the q|k|v workgroups of kv head kvh,
 // each of which then stores its flag (this launch's epoch and its XCD) in
-// flags[0..63]; the block issues its K/V tile loads, then waits (bounded)
-// until all QKV_PRODUCERS flags carry the epoch and its own XCD, before
-// loading q and patching the current row. A block that gives up writes NaN
-// partials.
+// flags[0..63]; the block issues its K/V tile loads, then waits (at most
+// `spins` polls) until all QKV_PRODUCERS flags carry the epoch `want` and its
+// own XCD, before loading q and patching the current row. A block that gives
+// up writes NaN partials (want differs from the producers' epoch only when
+// the test build forces that path).
 template <AttnTail TAIL, bool CHAINED>
 __device__ __forceinline__ void attn_block(const float* __restrict__ q,
     const float* __restrict__ kcache, const float* __restrict__ vcache,
     const lh_step_params* __restrict__ params, uint32_t capacity, uint32_t nblk,
     float* __restrict__ PM, float* __restrict__ PT, float* __restrict__ PA,
     unsigned long long* __restrict__ arrive, const unsigned long long* flags,
-    unsigned long long* bflags, unsigned long long epoch, float* __restrict__ out, uint32_t b,
-    uint32_t kvh, uint32_t t, AttnShared& sh)
+    unsigned long long* bflags, unsigned long long epoch, unsigned long long want, uint32_t spins,
+    float* __restrict__ out, uint32_t b, uint32_t kvh, uint32_t t, AttnShared& sh)
 {
     float4* T = sh.T;
     const uint64_t tile = lh_kv_index(capacity, 0, kvh, (uint64_t)b * LH_ATTN_BLOCK);
@@ -408,11 +409,11 @@ __device__ __forceinline__ void attn_block(const float* __restrict__ q,
         // XCD's L2, where the producers' stores land.
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
         if (wave == 0) {
-            const unsigned long long want = producer_flag(epoch, xcc_id());
+            const unsigned long long flag = producer_flag(want, xcc_id());
             const volatile unsigned long long* f = flags + lane;
             bool ready = false;
-            for (uint32_t spin = 0; spin < SPIN_LIMIT && !ready; spin++) {
-                ready = __builtin_amdgcn_ballot_w64(*f != want) == 0;
+            for (uint32_t spin = 0; spin < spins && !ready; spin++) {
+                ready = __builtin_amdgcn_ballot_w64(*f != flag) == 0;
                 if (!ready) {
                     __builtin_amdgcn_s_sleep(2);
                 }

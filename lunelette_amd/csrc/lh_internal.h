@@ -44,7 +44,7 @@ int lh_launch_qkv_attention(int lookup, const uint8_t *Wqkv, float sq, float sk,
     const float *gamma, const float *x, const lh_step_params *params, uint32_t length, float *q,
     float *kcache_layer, float *vcache_layer, uint32_t capacity, float *PM, float *PT, float *PA,
     unsigned long long *arrive, unsigned long long *flags, unsigned long long *bflags,
-    unsigned long long epoch, float *out, hipStream_t s);
+    unsigned long long epoch, int fault, float *out, hipStream_t s);
 /* Records once per device whether a launch's workgroups whose ids agree mod 8
  * run on one XCD (five probe launches into d_words, at least 2048 words, left
  * zeroed); *ok receives the verdict. A fused attention launch needs it. */
@@ -108,7 +108,8 @@ enum {
     LH_FAULT_NONFINITE = 2,        /* next execution publishes an Inf logit */
     LH_FAULT_CHECKPOINT_ALLOC = 3, /* next checkpoint allocation fails */
     LH_FAULT_AFTER_LAYER = 4,      /* next execution fails after layer arg's kernels ran */
-    LH_FAULT_EPOCH = 5             /* checkpoint epoch counter set to arg */
+    LH_FAULT_EPOCH = 5,            /* checkpoint epoch counter set to arg */
+    LH_FAULT_HANDOFF = 6           /* next execution's one-launch attention blocks give up */
 };
 struct lunelette_metal;
 int lh_runtime_fault(struct lunelette_metal *context, int kind, uint64_t arg);

@@ -18,13 +18,19 @@ extern "C" {
 
 struct lunelette_metal;
 /* what = 1: the next execution fails before any device work; 2: the next
- * execution publishes an Inf logit; 3: the next checkpoint allocation fails. */
+ * execution publishes an Inf logit; 3: the next checkpoint allocation fails;
+ * 6: in the next execution every attention block that shares a launch with
+ * the q|k|v projection waits for producer flags that never come, gives up
+ * after 64 polls and writes NaN (each kernel still runs to its end). */
 int lunelette_metal_test_inject(struct lunelette_metal *context, int what);
 /* The next execution fails after layer `layer`'s kernels ran, so layers
  * 0..layer have written their KV rows for it. */
 int lunelette_metal_test_fail_after_layer(struct lunelette_metal *context, uint32_t layer);
 /* Sets the context's checkpoint epoch counter (UINT64_MAX: exhausted). */
 int lunelette_metal_test_set_epoch(struct lunelette_metal *context, uint64_t epoch);
+/* Whether a decode token at this length runs q|k|v and its attention blocks
+ * in one launch on the current device. */
+int lunelette_metal_test_chained(uint32_t length);
 /* Overwrites one published host logit. */
 int lunelette_metal_test_set_logit(struct lunelette_metal *context, size_t index, float value);
 /* Arms the allocation counter: the nth device or pinned-host allocation from

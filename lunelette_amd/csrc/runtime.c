@@ -59,7 +59,7 @@ typedef struct lh_runtime {
     uint64_t identity, checkpoint_epoch;
     lunelette_metal_checkpoint *active_checkpoint;
     struct {                  /* host-forced faults (lh_runtime_fault) */
-        bool before_device, nonfinite, checkpoint_alloc;
+        bool before_device, nonfinite, checkpoint_alloc, handoff;
         uint32_t after_layer;     /* fail after layer after_layer - 1; 0 off */
     } fault;
 } lh_runtime;
@@ -785,12 +785,15 @@ static int execute(lunelette_metal *context, const int64_t *ids, size_t count, b
     /* The head kernel sets the flag on an Inf/NaN logit; the host then scans
      * only to name the first one. */
     *rt->h_nonfinite = 0;
+    rt->ws->handoff_fault = rt->fault.handoff;
+    rt->fault.handoff = false;
     int failed = hipEventRecord(rt->started, s) != hipSuccess ||
         (device_record &&
             lh_workspace_set_decode(rt->ws, rt->d_embedding, ids[0], rt->length, rt->d_x, s)) ||
         launch_step(rt, count, path, !device_record, s) ||
         hipEventRecord(rt->finished, s) != hipSuccess;
     hipError_t status = hipStreamSynchronize(s);
+    rt->ws->handoff_fault = 0;
     if (failed || status != hipSuccess) {
         snprintf(error, capacity, "execution failed; reset required: %s",
             failed ? lh_last_error() : hipGetErrorString(status));
@@ -998,6 +1001,9 @@ int lh_runtime_fault(lunelette_metal *context, int kind, uint64_t arg)
         return 0;
     case LH_FAULT_EPOCH:
         rt->checkpoint_epoch = arg;
+        return 0;
+    case LH_FAULT_HANDOFF:
+        rt->fault.handoff = true;
         return 0;
     default:
         return -1;

@@ -6,7 +6,8 @@
 
 int lunelette_metal_test_inject(struct lunelette_metal *context, int what)
 {
-    if (what < LH_FAULT_BEFORE_DEVICE || what > LH_FAULT_CHECKPOINT_ALLOC) {
+    if ((what < LH_FAULT_BEFORE_DEVICE || what > LH_FAULT_CHECKPOINT_ALLOC) &&
+        what != LH_FAULT_HANDOFF) {
         return -1;
     }
     return lh_runtime_fault(context, what, 0);
@@ -55,4 +56,9 @@ unsigned lunelette_metal_test_host_allocations(void)
 long lunelette_metal_test_live_host_allocations(void)
 {
     return lh_host_allocations_live();
+}
+
+int lunelette_metal_test_chained(uint32_t length)
+{
+    return lh_attention_chained(length);
 }

@@ -23,6 +23,7 @@ The failure cases run on the test build of the library
 lunelette_amd/csrc/lh_test_seams.h); every fault is forced from the host.
 """
 import math
+import time
 
 import numpy as np
 import pytest
@@ -315,6 +316,36 @@ def test_failure_after_layer_then_reset_replays_bitwise(gpu, mode):
         assert np.array_equal(bits(rt.append([8, 9, 10])), bits(want[2]))
         with pytest.raises(RuntimeError_):
             rt.fail_after_layer(LAYERS)  # no such layer
+
+
+def test_one_launch_attention_gives_up_then_reset_replays_bitwise(gpu):
+    """A decode step's attention blocks share a launch with the q|k|v
+    projection and wait, bounded, for its flags. The test build makes every
+    such block of one step wait for flags that never come: each gives up
+    after 64 polls and writes NaN partials, so the step reports a nonfinite
+    logit and invalidates the sequence, and every kernel still ends. After
+    reset (the arrival words and flags cleared) the same calls give the
+    logits of a fresh context bit for bit."""
+    prompt = syn.tokens(SEED, 21, 40)
+    with Runtime(seed=SEED, layers=LAYERS, context=256, block=256,
+                 prefill=lh.PREFILL_CUSTOM) as fresh:
+        want = [fresh.prefill(prompt), fresh.decode(7), fresh.decode(8)]
+    with Runtime(seed=SEED, layers=LAYERS, context=256, block=256, prefill=lh.PREFILL_CUSTOM,
+                 seams=True) as rt:
+        if not lh.test_lib().lunelette_metal_test_chained(len(prompt)):
+            pytest.skip("this device runs the attention blocks in launches of their own")
+        assert np.array_equal(bits(rt.prefill(prompt)), bits(want[0]))
+        rt.inject(6)
+        started = time.perf_counter()
+        with pytest.raises(RuntimeError_, match="nonfinite"):
+            rt.decode(7)
+        assert time.perf_counter() - started < 10.0
+        with pytest.raises(RuntimeError_):
+            rt.decode(7)  # invalid until reset
+        rt.reset()
+        assert np.array_equal(bits(rt.prefill(prompt)), bits(want[0]))
+        assert np.array_equal(bits(rt.decode(7)), bits(want[1]))
+        assert np.array_equal(bits(rt.decode(8)), bits(want[2]))
 
 
 @pytest.mark.parametrize("context,block", [(256, 256), (4352, 128)])
