@@ -53,6 +53,8 @@ sys.path.insert(0, ROOT)
 HBM_PEAK_GBPS = 8000.0
 # Timed repetitions of the 512-token prefill (median reported).
 PREFILL_TRIALS = 5
+# Every DEVICE_SAMPLE-th timed decode step reports its device time.
+DEVICE_SAMPLE = 8
 METRIC = "decode tok/s + 256-chunk prefill tok/s @4352 ctx; FP8 matvec % HBM peak"
 
 # FP8 weight elements per layer and projection.
@@ -369,6 +371,34 @@ def prefill_layer(lh, syn, seed, repeats=8):
             "gemm_mfma_util_lower_bound": round(mfma_gemm / (us * 1e-6) / 2.5e15, 4)}
 
 
+def decode_loop(rt, token, steps, sample):
+    """The timed greedy decode from `token`: each step is lunelette_metal_decode
+    (every layer, the head, the logits in host memory, the finite check) and
+    lunelette_select_greedy over the borrowed logits, called straight through
+    the C ABI as a C caller would (the Runtime methods add interpreter work
+    per step that is not the library's). The device time of every
+    `sample`-th step is kept in rt.sampled_device_ms. Returns the tokens."""
+    lib = rt._lib
+    decode, select, device = (lib.lunelette_metal_decode, lib.lunelette_select_greedy,
+                              lib.lunelette_metal_last_device_ms)
+    handle, err, logits = rt.handle, rt._err, rt._logits
+    logits_ref = ctypes.byref(logits)
+    tok = ctypes.c_int64(token)
+    tok_ref = ctypes.byref(tok)
+    ms = ctypes.c_float()
+    ms_ref = ctypes.byref(ms)
+    rt.sampled_device_ms = []
+    out = []
+    for i in range(steps):
+        if decode(handle, tok.value, logits_ref, err, 512) or select(logits, tok_ref, err, 512):
+            raise RuntimeError(err.value.decode())
+        if i % sample == 0:
+            device(handle, ms_ref)
+            rt.sampled_device_ms.append(ms.value)
+        out.append(tok.value)
+    return out
+
+
 def agreement(got, want):
     """Number of leading ids of `got` equal to `want`."""
     n = min(len(got), len(want))
@@ -436,17 +466,13 @@ def decode_near_capacity(lh, Runtime, seed, steps, prefill_mode):
                 rt.append(ids, copy=False)
         token = rt.greedy()
         lh.check(lh.lib().lh_device_synchronize())
-        device_ms = 0.0
         t = time.perf_counter()
-        for _ in range(steps):
-            rt.decode(token, copy=False)
-            device_ms += rt.last_device_ms()
-            token = rt.greedy()
+        decode_loop(rt, token, steps, DEVICE_SAMPLE)
         lh.check(lh.lib().lh_device_synchronize())
         wall = time.perf_counter() - t
         return {"decode_tok_s": round(steps / wall, 2),
                 "ms_per_step": round(wall * 1e3 / steps, 4),
-                "device_ms_per_step": round(device_ms / steps, 4),
+                "device_ms_per_step": round(statistics.mean(rt.sampled_device_ms), 4),
                 "positions": [length, 4351], "prompt": length}
     finally:
         rt.close()
@@ -500,13 +526,10 @@ def long_context(lh, syn, Runtime, seed, prefill_mode):
             token = rt.greedy()
             tokens.append(token)
             t = time.perf_counter()
-            for _ in range(128):
-                rt.decode(token, copy=False)
-                decode_device += rt.last_device_ms()
-                token = rt.greedy()
-                tokens.append(token)
-                decoded += 1
+            tokens += decode_loop(rt, token, 128, DEVICE_SAMPLE)
             decode_s += time.perf_counter() - t
+            decode_device += statistics.mean(rt.sampled_device_ms) * 128
+            decoded += 128
         rt.destroy_checkpoint(checkpoint)
         fx = fixture_tokens("long_c17920_26layer.json")
         match = None
@@ -693,15 +716,11 @@ def main():
         prefill_s * 1e3, chunk1_ms, chunk2_ms, PREFILL_TRIALS))
 
     lh.check(lh.lib().lh_device_synchronize())
-    device_ms = 0.0
     t = time.perf_counter()
-    for _ in range(args.steps):
-        rt.decode(token, copy=False)
-        device_ms += rt.last_device_ms()
-        token = rt.greedy()
-        tokens.append(token)
+    tokens += decode_loop(rt, token, args.steps, DEVICE_SAMPLE)
     lh.check(lh.lib().lh_device_synchronize())
     decode_s = time.perf_counter() - t
+    device_ms = statistics.mean(rt.sampled_device_ms) * args.steps
     rt.close()
     decode_tok_s = args.steps / decode_s
     log("decode %d steps: %.3f ms/step (device %.3f ms/step)" % (
