@@ -121,7 +121,7 @@ def parse():
 
 
 def time_operators(lh, syn, seed, repeats):
-    """Per-operator device time at decode position 4351 (config 2 shape)."""
+    """Per-operator device time at decode position 4351 (one layer, 4352 cached positions)."""
     lib = lh.lib()
     copies = 26
     capacity, length = 4352, 4351
@@ -614,7 +614,7 @@ def cpu_baseline(syn, seed, budget_s=10.0):
 
 
 def cpu_configs(syn, seed, o, oracle_lib, layers, model, share, budget_s=1.0):
-    """The oracle's reference-literal schedule on the other BASELINE configs,
+    """The oracle's reference-literal schedule on the other workloads,
     each bounded to about budget_s of repeats: the FP8 linear 9216x3072 (1
     thread and the host share), one decode layer at position 4351, one
     256-token prefill layer after a 4096-token prefix, and one decode step of

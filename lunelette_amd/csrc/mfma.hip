@@ -1135,8 +1135,8 @@ extern "C" int lh_fp8_gemm(lh_workspace* ws, const uint8_t* d_w, float scale, co
 // token for gate|up, per token and 576-column K granule for down). The q|k|v
 // input stays in three exact BF16 planes: its error reaches the attention
 // scores, which the softmax amplifies (at scores of a few hundred, two FP16
-// planes put the config-3 layer at 1.2e-3 of the row maximum, over the 1e-3
-// tolerance).
+// planes put the layer of 256 tokens after a 4096-token prefix at 1.2e-3 of
+// the row maximum, over the 1e-3 tolerance).
 extern "C" int lh_layer_forward_mfma(const lh_layer_weights* w, float* d_x, float* d_keys,
     float* d_values, lh_workspace* ws, int input_split, const float* next_norm, hipStream_t s)
 {

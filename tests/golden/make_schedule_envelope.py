@@ -1,7 +1,8 @@
 """How far two FP32 schedules of the same model lie apart: the oracle's
 reference-literal schedule (ORC_REF: the arithmetic of
 src/metal_kernels.metal, per-lane Kahan sums, two-pass softmax) against its
-device-mirror schedule (ORC_MIRROR), run in lockstep on the config-4 workload.
+device-mirror schedule (ORC_MIRROR), run in lockstep on the 26-layer decode
+workload at context 4352.
 
 Workload: the seeded 26-layer synthetic model, context 4352, the 512-token
 prompt (synthetic.tokens(seed, 1, 512)) prefilled in two 256-token chunks,

@@ -2,8 +2,8 @@
 
 Bit-exact against the oracle's device-mirror schedule; within fp32 tolerance
 of the reference-literal schedule. Shapes and scales follow the reference's
-own tests (tests/test_metal_compact.m:46-145) and BASELINE config 1
-(9216x3072 FP8, scale 0.0125, x ~ N(0,1)).
+own tests (tests/test_metal_compact.m:46-145) and the single FP8 linear
+9216x3072 (scale 0.0125, x ~ N(0,1)).
 """
 import ctypes
 import json
@@ -77,7 +77,7 @@ def run_fp8(gpu, w, scale, x, rows, cols, tokens=1, lookup=0, guard=4):
     return out[:tokens * rows * 4].view(np.float32)
 
 
-def test_fp8_matvec_config1_bitwise_mirror(gpu):
+def test_fp8_matvec_9216x3072_bitwise_mirror(gpu):
     rows, cols, scale = 9216, 3072, 0.0125
     w = syn.fp8(11, 500, rows, cols)
     x = syn.normal_f32(11, 501, cols)

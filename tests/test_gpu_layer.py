@@ -1,9 +1,9 @@
-"""GPU parity of one decoder layer (BASELINE configs 2 and 3) through the
-kernel-level C-ABI lh_layer_forward.
+"""GPU parity of one decoder layer through the kernel-level C-ABI
+lh_layer_forward.
 
-Config 2: decode of one token at position 4351 over a 4351-entry N(0,1) FP32
+Decode: one token at position 4351 over a 4351-entry N(0,1) FP32
 KV cache, seeded FP8 weights with per-tensor scales in [0.01, 0.02].
-Config 3 (precise path): a 256-token chunk appended after a 4096-token prefix
+Prefill (precise path): a 256-token chunk appended after a 4096-token prefix
 with causal masking inside the chunk.
 The fused, lookup, unfused and resident-FP32 paths must give identical bits,
 equal to the oracle's device-mirror schedule; the reference-literal schedule
@@ -88,7 +88,7 @@ def check_layer(gpu, host, length, count, capacity, paths):
     assert np.median(np.abs(got - want) / np.maximum(np.abs(want), 1e-30)) < 1e-6
 
 
-def test_config2_decode_layer_all_paths(gpu, layer_host):
+def test_decode_layer_pos4351_all_paths(gpu, layer_host):
     check_layer(gpu, layer_host, 4351, 1, 4352,
                 [lh.PATH_FUSED, lh.PATH_LOOKUP, lh.PATH_UNFUSED, lh.PATH_RESIDENT])
 
@@ -106,7 +106,7 @@ def test_decode_layer_one_launch_boundaries(gpu, layer_host):
         check_layer(gpu, layer_host, length, 1, 4352, [lh.PATH_FUSED, lh.PATH_LOOKUP])
 
 
-def test_config3_prefill_chunk_precise_path(gpu, layer_host):
+def test_prefill_chunk_256_after_4096_precise_path(gpu, layer_host):
     check_layer(gpu, layer_host, 4096, 256, 4352, [lh.PATH_FUSED])
 
 

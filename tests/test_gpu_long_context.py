@@ -25,7 +25,7 @@ tests/golden/make_long_golden.py (device-mirror schedule):
   error measured on MI355X is 2.7e-3 of the range and the median about
   1.2e-4, with no id flipped (builds with another prefill summation order
   flipped two of the 1032, both at gaps below twice the error). The bound is
-  looser than the 1e-3 of the 2-layer and config-4 workloads because after a
+  looser than the 1e-3 of the 2-layer and 4352-context workloads because after a
   16K-token matrix-core prefill the 26-layer stack amplifies the prefill's
   rounding through near-tie softmax rows; those errors move no selected id.
 """

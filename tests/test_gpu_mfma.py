@@ -4,7 +4,7 @@ The reference's own MPS path is pinned only by tolerance (tests/test_metal.m:
 200-259: |err| <= 2e-4 + 1e-4|ref| vs double); this path is held tighter:
 - lh_fp8_gemm vs double: |err| <= 2e-6 * sum_c |w x| (exact BF16 operands,
   FP32 accumulation), output guard untouched;
-- one decoder layer at config 3 (256 tokens after a 4096 prefix) vs the
+- one decoder layer of 256 tokens after a 4096-token prefix vs the
   oracle: activations within 1e-3 of the row max-abs (median relative
   <= 1e-5), appended K/V rows within 1e-5 of the row max-abs;
 - runtime prefill of a 2-layer model in MPS mode: logits within 1e-3 of the
@@ -75,7 +75,7 @@ def test_rejects_unsupported_gemm_shapes(gpu):
         gpu.lh_workspace_destroy(ws)
 
 
-def test_mfma_layer_config3(gpu):
+def test_mfma_layer_256_after_4096(gpu):
     from test_gpu_layer import oracle_layer, run_layer
     host = syn.layer(SEED, 0)
     length, count, capacity = 4096, 256, 4352
@@ -185,8 +185,8 @@ def test_mfma_layer_down_input_range(gpu, shift):
     """gate and up scales times 2^shift put SiLU(gate)*up up to about 1e13
     (far past FP16's 65504) or below about 1e-4 (mostly FP16 subnormals):
     the down projection's two FP16 planes carry a power-of-two scale per token
-    and K split, so the layer stays within the config-3 tolerance of the
-    oracle."""
+    and K split, so the layer stays within the matrix-core layer tolerance
+    of the oracle."""
     from test_gpu_layer import oracle_layer, run_layer
     host = dict(syn.layer(SEED, 2))
     for name in ("scale_gate", "scale_up"):
@@ -211,8 +211,8 @@ def test_mfma_layer_down_granule_gap(gpu):
     SiLU(gate) * up near 2^-100 there, against about 2^17 in the granules
     before them. A stream-K segment that crosses such a boundary must not
     carry its accumulator over by the ratio of the granules' scales (it would
-    overflow FP32); the layer stays finite and within the config-3 tolerance
-    of the oracle."""
+    overflow FP32); the layer stays finite and within the matrix-core layer
+    tolerance of the oracle."""
     from test_gpu_layer import oracle_layer, run_layer
     host = dict(syn.layer(SEED, 3))
     length, count, capacity = 64, 192, 256

@@ -51,7 +51,7 @@ def test_all_ones_dot_is_exactly_k(schedule, cols):
 
 
 @pytest.mark.parametrize("schedule", SCHEDULES)
-def test_fp8_matvec_vs_double_config1_shape(schedule, product):
+def test_fp8_matvec_vs_double_9216x3072(schedule, product):
     import lunelette_amd.synthetic as syn
     rows, cols, scale = 9216, 3072, 0.0125
     w = syn.fp8(11, 500, rows, cols)

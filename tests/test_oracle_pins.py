@@ -185,7 +185,8 @@ def test_silu_schedules_close(oracle):
 
 def test_schedule_envelope_fixture_consistent():
     """tests/golden/schedule_envelope_c4352_26layer.json (the oracle's two
-    exact FP32 schedules in lockstep on the config-4 workload) belongs to the
+    exact FP32 schedules in lockstep on the 26-layer decode workload at context
+    4352) belongs to the
     stream fixture's workload: same seed and first ids, one entry per call,
     and the reordering alone moves a few calls past 1e-3 of the logit range
     while the median call stays near 1e-5."""

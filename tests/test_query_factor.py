@@ -10,8 +10,8 @@ admits positions up to 17919, so every path that forms Q must apply it there:
   and V rows bit for bit equal to the oracle's mirror schedule, the
   reference-literal schedule within the layer tolerance;
 - the matrix-core epilogue (PATH_MFMA): a 128-token chunk at 16320 (straddling
-  16384) and a 256-token chunk at 17664 (up to 17919), within the config-3
-  tolerance;
+  16384) and a 256-token chunk at 17664 (up to 17919), within the tolerance
+  of the matrix-core layer after a 4096-token prefix;
 - the runtime: a 2-layer model decoding from 16300 to 16448, then an append
   of 200 tokens at 16300 and 4 decodes (tests/golden/make_qfactor_golden.py):
   precise logits bit for bit equal to the oracle fixture per call, the
