@@ -41,14 +41,15 @@ namespace lh {
 // partials from that XCD's L2. TAIL_FLAG (one token): 128 combiner
 // workgroups follow the blocks, id 8 * nblk + (4 * (h % 4) + qd) * 8 + h / 4
 // for head h and dimension quarter qd, so each runs on its kv head's XCD and
-// combines from its L2 once the head's blocks have flagged their partials.
+// combines from its L2 once the head's blocks have flagged their partials
+// (flags of epoch `cwant`, at most `cspins` polls; see attn_combiner).
 template <AttnTail TAIL>
 __global__ void __launch_bounds__(256)
 k_attn_blocks(const float* __restrict__ q, const float* __restrict__ kcache,
     const float* __restrict__ vcache, const lh_step_params* __restrict__ params,
     uint32_t capacity, uint32_t nblk, float* __restrict__ PM, float* __restrict__ PT,
     float* __restrict__ PA, unsigned long long* __restrict__ arrive, unsigned long long* bflags,
-    unsigned long long epoch, float* __restrict__ out)
+    unsigned long long epoch, unsigned long long cwant, uint32_t cspins, float* __restrict__ out)
 {
     __shared__ union {
         AttnShared blocks;
@@ -58,7 +59,7 @@ k_attn_blocks(const float* __restrict__ q, const float* __restrict__ kcache,
     if (TAIL == TAIL_FLAG && id >= 8 * nblk) {
         const uint32_t j = id - 8 * nblk, kvh = j & 7, r = j >> 3;
         attn_combiner(PM, PT, PA, params, capacity, bflags + kvh * (capacity / LH_ATTN_BLOCK),
-            epoch, kvh * 4 + (r >> 2), r & 3, out, sh.combine);
+            cwant, cspins, kvh * 4 + (r >> 2), r & 3, out, sh.combine);
         return;
     }
     const uint32_t kvh = id & 7, b = (id >> 3) % nblk, t = (id >> 3) / nblk;
@@ -227,11 +228,13 @@ extern "C" int lh_attention_chained(uint32_t length)
 // of at most LH_ATTN_FUSED_BLOCKS combines in its own launch; with bflags
 // set (8 * capacity/64 words; epoch nonzero and new for every launch on them)
 // one token's longer grid runs its blocks and combiners in one launch;
-// otherwise blocks and k_attn_combine run as two launches.
+// otherwise blocks and k_attn_combine run as two launches. fault (test build
+// only): LH_HANDOFF_COMBINERS makes the combiners wait for an epoch no block
+// stores, LH_GIVE_UP_POLLS polls at most, so they give up and write NaN.
 extern "C" int lh_launch_attention(const float* q, const float* kcache_layer,
     const float* vcache_layer, const lh_step_params* params, uint32_t length, uint32_t count,
     uint32_t capacity, float* PM, float* PT, float* PA, unsigned long long* arrive,
-    unsigned long long* bflags, unsigned long long epoch, float* out, hipStream_t s)
+    unsigned long long* bflags, unsigned long long epoch, int fault, float* out, hipStream_t s)
 {
     if (!count || capacity % LH_ATTN_BLOCK || length + count > capacity) {
         return -1;
@@ -241,14 +244,18 @@ extern "C" int lh_launch_attention(const float* q, const float* kcache_layer,
     const bool ok = fused_attention_ok();
     if (ok && arrive && nblk <= LH_ATTN_FUSED_BLOCKS) {
         hipLaunchKernelGGL(k_attn_blocks<TAIL_COMBINE>, grid, dim3(256), 0, s, q, kcache_layer,
-            vcache_layer, params, capacity, nblk, PM, PT, PA, arrive, nullptr, 0ull, out);
+            vcache_layer, params, capacity, nblk, PM, PT, PA, arrive, nullptr, 0ull, 0ull, 0u,
+            out);
     } else if (ok && bflags && epoch && count == 1) {
+        const bool forced = fault == LH_HANDOFF_COMBINERS;
         hipLaunchKernelGGL(k_attn_blocks<TAIL_FLAG>, dim3(LH_KV_HEADS * nblk + LH_HEADS * 4),
             dim3(256), 0, s, q, kcache_layer, vcache_layer, params, capacity, nblk, PM, PT, PA,
-            nullptr, bflags, epoch, out);
+            nullptr, bflags, epoch, forced ? epoch + 1 : epoch,
+            forced ? LH_GIVE_UP_POLLS : SPIN_LIMIT, out);
     } else {
         hipLaunchKernelGGL(k_attn_blocks<TAIL_NONE>, grid, dim3(256), 0, s, q, kcache_layer,
-            vcache_layer, params, capacity, nblk, PM, PT, PA, nullptr, nullptr, 0ull, nullptr);
+            vcache_layer, params, capacity, nblk, PM, PT, PA, nullptr, nullptr, 0ull, 0ull, 0u,
+            nullptr);
         hipLaunchKernelGGL(k_attn_combine, dim3(LH_HEADS * 4, count), dim3(256), 0, s, PM, PT, PA,
             params, capacity, out);
     }
@@ -322,7 +329,7 @@ extern "C" int lh_attention_noalloc(const float* d_q, const float* d_keys, const
         (uint32_t)count);
     if (hipGetLastError() != hipSuccess ||
         lh_launch_attention(d_q, d_keys, d_values, params, (uint32_t)length, (uint32_t)count,
-            (uint32_t)capacity, PM, PT, PA, nullptr, nullptr, 0ull, d_out, s)) {
+            (uint32_t)capacity, PM, PT, PA, nullptr, nullptr, 0ull, 0, d_out, s)) {
         lh_set_error("attention_noalloc: launch failed");
         return -1;
     }

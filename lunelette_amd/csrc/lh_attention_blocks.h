@@ -172,24 +172,25 @@ __device__ __forceinline__ void attn_combine(const float* __restrict__ PM,
 
 // Combiner workgroup of a one-token launch whose blocks (kv head h / 4, on
 // this workgroup's XCD) each store bflags[b] = epoch once their partials are
-// acknowledged: waits (bounded; polls by volatile loads, which miss the L1)
-// until the first nb flags carry the epoch, then combines from the XCD's L2
+// acknowledged: waits, at most `spins` polls (volatile loads, which miss the
+// L1), until the first nb flags carry `want`, then combines from the XCD's L2
 // (no workgroup loaded the partials before in this launch, so this CU's L1
-// holds none of their lines). If it gives up it writes NaN.
+// holds none of their lines). If it gives up it writes NaN. want equals the
+// launch's epoch except where the test build forces the give-up.
 __device__ __forceinline__ void attn_combiner(const float* __restrict__ PM,
     const float* __restrict__ PT, const float* __restrict__ PA,
     const lh_step_params* __restrict__ params, uint32_t capacity,
-    const unsigned long long* bflags, unsigned long long epoch, uint32_t h, uint32_t qd,
-    float* __restrict__ out, CombineShared& sh)
+    const unsigned long long* bflags, unsigned long long want, uint32_t spins, uint32_t h,
+    uint32_t qd, float* __restrict__ out, CombineShared& sh)
 {
     const uint32_t n = params->length + 1;
     const uint32_t nb = (n + LH_ATTN_BLOCK - 1) / LH_ATTN_BLOCK;
     const volatile unsigned long long* f = bflags;
     bool ready = false;
-    for (uint32_t spin = 0; spin < SPIN_LIMIT; spin++) {
+    for (uint32_t spin = 0; spin < spins; spin++) {
         int mine = 1;
         for (uint32_t b = threadIdx.x; b < nb; b += 256) {
-            mine &= f[b] == epoch;
+            mine &= f[b] == want;
         }
         if (__syncthreads_and(mine)) {
             ready = true;

@@ -31,7 +31,7 @@ int lh_launch_rmsnorm(const float *gamma, const float *x, float *out, uint32_t w
 int lh_launch_attention(const float *q, const float *kcache_layer, const float *vcache_layer,
     const lh_step_params *params, uint32_t length, uint32_t count, uint32_t capacity, float *PM,
     float *PT, float *PA, unsigned long long *arrive, unsigned long long *bflags,
-    unsigned long long epoch, float *out, hipStream_t s);
+    unsigned long long epoch, int fault, float *out, hipStream_t s);
 /* Whether a decode token at this length runs q|k|v and its attention blocks
  * in one launch on the current device (its dispatch probed). */
 int lh_attention_chained(uint32_t length);
@@ -109,8 +109,14 @@ enum {
     LH_FAULT_CHECKPOINT_ALLOC = 3, /* next checkpoint allocation fails */
     LH_FAULT_AFTER_LAYER = 4,      /* next execution fails after layer arg's kernels ran */
     LH_FAULT_EPOCH = 5,            /* checkpoint epoch counter set to arg */
-    LH_FAULT_HANDOFF = 6           /* next execution's one-launch attention blocks give up */
+    LH_FAULT_HANDOFF = 6,          /* next execution's one-launch attention blocks give up */
+    LH_FAULT_COMBINERS = 7         /* next execution's attention flag combiners give up */
 };
+/* The workspace's handoff_fault (test build): which bounded wait of the next
+ * execution's attention launches waits for an epoch nobody stores, and so
+ * gives up after LH_GIVE_UP_POLLS polls and writes NaN. */
+enum { LH_HANDOFF_BLOCKS = 1, LH_HANDOFF_COMBINERS = 2 };
+#define LH_GIVE_UP_POLLS 64
 struct lunelette_metal;
 int lh_runtime_fault(struct lunelette_metal *context, int kind, uint64_t arg);
 int lh_runtime_set_logit(struct lunelette_metal *context, size_t index, float value);

@@ -25,7 +25,7 @@ struct lh_workspace {
                                       then 512 producer flags (ARRIVE_WORDS) */
     unsigned long long *d_bflags;  /* [8][C/64] block flags of one-launch long attention */
     unsigned long long epoch;      /* last epoch stored in the producer and block flags */
-    int handoff_fault;             /* test build: the next chained launches' blocks give up */
+    int handoff_fault;             /* test build: LH_HANDOFF_* wait of the next launches gives up */
     float *d_yarn;                 /* [C][128]: cos[64], sin[64] per position (decode) */
     float *h_yarn;                 /* host copy of the same rows, filled on first use */
     uint8_t *h_yarn_ready;         /* [C]: row p of h_yarn holds lh_yarn(p) */

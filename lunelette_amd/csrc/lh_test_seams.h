@@ -21,7 +21,10 @@ struct lunelette_metal;
  * execution publishes an Inf logit; 3: the next checkpoint allocation fails;
  * 6: in the next execution every attention block that shares a launch with
  * the q|k|v projection waits for producer flags that never come, gives up
- * after 64 polls and writes NaN (each kernel still runs to its end). */
+ * after 64 polls and writes NaN (each kernel still runs to its end); 7: in
+ * the next execution the attention's flag combiners (one token past 16 blocks,
+ * in the q|k|v launch or in the attention's own) wait for block flags that
+ * never come, give up after 64 polls and write NaN. */
 int lunelette_metal_test_inject(struct lunelette_metal *context, int what);
 /* The next execution fails after layer `layer`'s kernels ran, so layers
  * 0..layer have written their KV rows for it. */

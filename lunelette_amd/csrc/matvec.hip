@@ -577,9 +577,10 @@ k_qkv_rope(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restr
 // otherwise each block flags its partials in bflags and 128 combiner
 // workgroups follow the blocks (id 512 + 8 * nblk + (4 * (h % 4) + qd) * 8 +
 // h / 4, on kv head h / 4's XCD). epoch: nonzero, new for every launch on
-// these flags; the blocks wait for producer flags of epoch `want` (equal to
-// epoch but where the test build forces a block to give up) for at most
-// `spins` polls. grid 512 + 8 * nblk (+ 128), block 256.
+// these flags; the blocks wait for producer flags of epoch `want` for at most
+// `spins` polls, the combiners for block flags of epoch `cwant` for at most
+// `cspins` (each equal to epoch and SPIN_LIMIT but where the test build forces
+// that wait to give up). grid 512 + 8 * nblk (+ 128), block 256.
 template <bool LUT, bool COMBINE>
 __global__ void __launch_bounds__(256)
 k_qkv_attn(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restrict__ gamma,
@@ -588,7 +589,8 @@ k_qkv_attn(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restr
     uint32_t capacity, uint32_t nblk, float* __restrict__ PM, float* __restrict__ PT,
     float* __restrict__ PA, unsigned long long* __restrict__ arrive,
     unsigned long long* flags, unsigned long long* bflags, unsigned long long epoch,
-    unsigned long long want, uint32_t spins, float* __restrict__ out)
+    unsigned long long want, uint32_t spins, unsigned long long cwant, uint32_t cspins,
+    float* __restrict__ out)
 {
     __shared__ union {
         QkvShared<LUT> qkv;
@@ -599,7 +601,7 @@ k_qkv_attn(const uint8_t* __restrict__ Wqkv, float3 scales, const float* __restr
     if (!COMBINE && blockIdx.x >= 8 * (QKV_PRODUCERS + nblk)) {
         const uint32_t r = (blockIdx.x - 8 * (QKV_PRODUCERS + nblk)) >> 3;
         attn_combiner(PM, PT, PA, params, capacity, bflags + kvh * (capacity / LH_ATTN_BLOCK),
-            epoch, kvh * 4 + (r >> 2), r & 3, out, sh.combine);
+            cwant, cspins, kvh * 4 + (r >> 2), r & 3, out, sh.combine);
         return;
     }
     if (blockIdx.x < 8 * QKV_PRODUCERS) {
@@ -858,9 +860,10 @@ extern "C" int lh_launch_qkv_rope(int lookup, const uint8_t* Wqkv, float sq, flo
 // their combine in one launch. arrive: the blocks' 8 zeroed arrival words
 // (left zeroed); flags: the producers' 512 flags; bflags: 8 * capacity/64
 // block flags; epoch new for every launch on them (nonzero). fault (test
-// build only): the blocks wait for an epoch no producer stores, 64 polls at
-// most, so every one gives up and the step's output is NaN. Callers check
-// lh_attention_chained(length) first.
+// build only): LH_HANDOFF_BLOCKS makes the blocks, LH_HANDOFF_COMBINERS the
+// combiners (past 16 blocks), wait for an epoch nobody stores,
+// LH_GIVE_UP_POLLS polls at most, so they give up and the step's output is
+// NaN. Callers check lh_attention_chained(length) first.
 extern "C" int lh_launch_qkv_attention(int lookup, const uint8_t* Wqkv, float sq, float sk,
     float sv, const float* gamma, const float* x, const lh_step_params* params, uint32_t length,
     float* q, float* kcache_layer, float* vcache_layer, uint32_t capacity, float* PM, float* PT,
@@ -871,15 +874,18 @@ extern "C" int lh_launch_qkv_attention(int lookup, const uint8_t* Wqkv, float sq
         !epoch) {
         return -1;
     }
-    const unsigned long long want = fault ? epoch + 1 : epoch;
-    const uint32_t spins = fault ? 64 : SPIN_LIMIT;
+    const bool blocks = fault == LH_HANDOFF_BLOCKS, combiners = fault == LH_HANDOFF_COMBINERS;
+    const unsigned long long want = blocks ? epoch + 1 : epoch;
+    const uint32_t spins = blocks ? LH_GIVE_UP_POLLS : SPIN_LIMIT;
+    const unsigned long long cwant = combiners ? epoch + 1 : epoch;
+    const uint32_t cspins = combiners ? LH_GIVE_UP_POLLS : SPIN_LIMIT;
     const uint32_t nblk = lh_attention_blocks(length, 1);
     const bool combine = nblk <= LH_ATTN_FUSED_BLOCKS;
     const dim3 grid(8 * QKV_PRODUCERS + LH_KV_HEADS * nblk + (combine ? 0 : LH_HEADS * 4));
     const float3 scales = make_float3(sq, sk, sv);
 #define LH_QKV_ATTN(L, C) hipLaunchKernelGGL((k_qkv_attn<L, C>), grid, dim3(256), 0, s, Wqkv, \
         scales, gamma, x, params, q, kcache_layer, vcache_layer, capacity, nblk, PM, PT, PA, \
-        arrive, flags, bflags, epoch, want, spins, out)
+        arrive, flags, bflags, epoch, want, spins, cwant, cspins, out)
     if (lookup) {
         if (combine) {
             LH_QKV_ATTN(true, true);

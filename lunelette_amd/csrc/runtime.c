@@ -59,7 +59,8 @@ typedef struct lh_runtime {
     uint64_t identity, checkpoint_epoch;
     lunelette_metal_checkpoint *active_checkpoint;
     struct {                  /* host-forced faults (lh_runtime_fault) */
-        bool before_device, nonfinite, checkpoint_alloc, handoff;
+        bool before_device, nonfinite, checkpoint_alloc;
+        int handoff;              /* LH_HANDOFF_* wait that gives up; 0 off */
         uint32_t after_layer;     /* fail after layer after_layer - 1; 0 off */
     } fault;
 } lh_runtime;
@@ -786,7 +787,7 @@ static int execute(lunelette_metal *context, const int64_t *ids, size_t count, b
      * only to name the first one. */
     *rt->h_nonfinite = 0;
     rt->ws->handoff_fault = rt->fault.handoff;
-    rt->fault.handoff = false;
+    rt->fault.handoff = 0;
     int failed = hipEventRecord(rt->started, s) != hipSuccess ||
         (device_record &&
             lh_workspace_set_decode(rt->ws, rt->d_embedding, ids[0], rt->length, rt->d_x, s)) ||
@@ -1003,7 +1004,10 @@ int lh_runtime_fault(lunelette_metal *context, int kind, uint64_t arg)
         rt->checkpoint_epoch = arg;
         return 0;
     case LH_FAULT_HANDOFF:
-        rt->fault.handoff = true;
+        rt->fault.handoff = LH_HANDOFF_BLOCKS;
+        return 0;
+    case LH_FAULT_COMBINERS:
+        rt->fault.handoff = LH_HANDOFF_COMBINERS;
         return 0;
     default:
         return -1;

@@ -7,7 +7,7 @@
 int lunelette_metal_test_inject(struct lunelette_metal *context, int what)
 {
     if ((what < LH_FAULT_BEFORE_DEVICE || what > LH_FAULT_CHECKPOINT_ALLOC) &&
-        what != LH_FAULT_HANDOFF) {
+        what != LH_FAULT_HANDOFF && what != LH_FAULT_COMBINERS) {
         return -1;
     }
     return lh_runtime_fault(context, what, 0);

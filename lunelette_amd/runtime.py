@@ -138,8 +138,8 @@ class Runtime:
 
     def inject(self, what):
         """Test build only: 1 fail before device work, 2 Inf logit, 3 checkpoint
-        allocation failure, 6 the one-launch attention blocks give up (next
-        call)."""
+        allocation failure, 6 the one-launch attention blocks give up, 7 the
+        attention's flag combiners give up (next call)."""
         if self._lib.lunelette_metal_test_inject(self.handle, what):
             raise RuntimeError_("inject rejected")
 

@@ -348,6 +348,51 @@ def test_one_launch_attention_gives_up_then_reset_replays_bitwise(gpu):
         assert np.array_equal(bits(rt.decode(8)), bits(want[2]))
 
 
+@pytest.mark.parametrize("what,prompt_length,context", [
+    (6, 1100, 4352),    # 18 blocks in the q|k|v launch: its blocks give up
+    (7, 1100, 4352),    # 18 blocks in the q|k|v launch: its combiners give up
+    (7, 4700, 17920),   # 74 blocks in the attention's own launch: its combiners give up
+])
+def test_flag_combiners_give_up_then_reset_replays_bitwise(gpu, what, prompt_length, context):
+    """Past 16 blocks a decode token's attention is combined in the same
+    launch by 128 combiner workgroups that wait, bounded, for every block's
+    flag. The test build forces one bounded wait of one step to give up: the
+    blocks' wait for the q|k|v producers (their NaN partials then reach the
+    combiners) or the combiners' own wait for the block flags. The step
+    reports a nonfinite logit and invalidates the sequence, every kernel still
+    ends, and after reset the same calls give the logits of a fresh context
+    bit for bit."""
+    seams = lh.test_lib()
+    if not seams.lunelette_metal_test_chained(64):
+        pytest.skip("this device runs the attention blocks and combine in launches of their own")
+    assert bool(seams.lunelette_metal_test_chained(prompt_length)) == (prompt_length < 72 * 64)
+    prompt = syn.tokens(SEED, 23, prompt_length)
+
+    def ingest(r):   # the prompt in 256-token calls
+        for begin in range(0, prompt_length, 256):
+            ids = prompt[begin:begin + 256]
+            logits = r.prefill(ids) if begin == 0 else r.append(ids)
+        return logits
+
+    with Runtime(seed=SEED, layers=LAYERS, context=context, block=256,
+                 prefill=lh.PREFILL_MPS) as fresh:
+        want = [ingest(fresh), fresh.decode(7), fresh.decode(8)]
+    with Runtime(seed=SEED, layers=LAYERS, context=context, block=256, prefill=lh.PREFILL_MPS,
+                 seams=True) as rt:
+        assert np.array_equal(bits(ingest(rt)), bits(want[0]))
+        rt.inject(what)
+        started = time.perf_counter()
+        with pytest.raises(RuntimeError_, match="nonfinite"):
+            rt.decode(7)
+        assert time.perf_counter() - started < 10.0
+        with pytest.raises(RuntimeError_):
+            rt.decode(7)  # invalid until reset
+        rt.reset()
+        assert np.array_equal(bits(ingest(rt)), bits(want[0]))
+        assert np.array_equal(bits(rt.decode(7)), bits(want[1]))
+        assert np.array_equal(bits(rt.decode(8)), bits(want[2]))
+
+
 @pytest.mark.parametrize("context,block", [(256, 256), (4352, 128)])
 def test_allocation_failure_at_every_index(gpu, context, block):
     """The N-th device or pinned-host allocation of create fails, for every N
