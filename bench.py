@@ -23,7 +23,8 @@ Also measured, with HIP events on the stream the kernels run on:
 - each fused decode operator at position 4351 launched over 26 distinct layer
   weight/KV copies (3.0 GB + 0.9 GB, far beyond the 256 MB Infinity Cache),
   giving the FP8 matvec HBM bandwidth; `roofline` reports the dominant kernel
-  (norm + gate/up + SiLU);
+  (norm + gate/up + SiLU), back to back and, as `in_layer_sequence`, its
+  marginal time inside the layer's operator sequence (o before it, down after);
 - decode attention at 550, 4352 and 16000 cached positions;
 - one FP8 linear 9216x3072 and one prefill layer (256 tokens after 4096);
 - the long-context prefix-reuse workload at capacity 17920 (16384-token
@@ -191,6 +192,32 @@ def time_operators(lh, syn, seed, repeats):
         ms = ctypes.c_float()
         lh.check(lib.lh_event_elapsed_ms(start, stop, ctypes.byref(ms)))
         result[name] = ms.value * 1e3 / n  # microseconds per launch
+    # Gate/up inside a layer's operator sequence (q|k|v, attention, o, gate/up,
+    # down; each pass on the next weight and KV copy), where o runs before it
+    # and down after it as in a decode step: its marginal device time is the
+    # sequence's less that of the same sequence without it.
+    def sequence(names):
+        chosen = [op for name, op in ops if name in names]
+        def one(i):
+            keys = kv.ptr + (2 * (i % copies)) * kv_elems * 4
+            for op in chosen:
+                lh.check(lib.lh_layer_operator(op, ctypes.byref(layers[i % copies]), x.ptr,
+                                               keys, keys + kv_elems * 4, ws, stream), "sequence")
+        for i in range(copies):
+            one(i)
+        n = copies * repeats
+        lh.check(lib.lh_event_record(start, stream))
+        for i in range(n):
+            one(i)
+        lh.check(lib.lh_event_record(stop, stream))
+        ms = ctypes.c_float()
+        lh.check(lib.lh_event_elapsed_ms(start, stop, ctypes.byref(ms)))
+        return ms.value * 1e3 / n
+    everything = [name for name, _ in ops]
+    full = sequence(everything)
+    without = sequence([name for name in everything if name != "gateup_silu"])
+    in_sequence = {"layer_us": round(full, 3), "layer_without_gateup_us": round(without, 3),
+                   "gateup_silu_us": round(full - without, 3)}
     # Pure-read floors: the same weight bytes (q|k|v, o, gate and up together,
     # down) streamed by lh_read_floor from the same rotating copies, the best
     # grid and loads-in-flight that divide the size.
@@ -228,7 +255,7 @@ def time_operators(lh, syn, seed, repeats):
     lib.lh_event_destroy(stop)
     lib.lh_workspace_destroy(ws)
     lib.lh_stream_destroy(stream)
-    return result, floors
+    return result, floors, in_sequence
 
 
 def time_attention(lh, syn, seed, lengths=(550, 4352, 16000), copies=16, repeats=4):
@@ -781,7 +808,7 @@ def main():
     out["config"]["prefill_activations"] = dict({k: v[1] for k, v in PREFILL_PLANES.items()},
                                                 **PREFILL_ATTENTION)
     if not args.no_operators:
-        ops, floors = time_operators(lh, syn, args.seed, args.op_repeats)
+        ops, floors, in_sequence = time_operators(lh, syn, args.seed, args.op_repeats)
         fp8_us = sum(ops[k] for k in FP8_BYTES)
         fp8_gbps = sum(FP8_BYTES.values()) / (fp8_us * 1e-6) / 1e9
         dom = "gateup_silu"
@@ -795,7 +822,10 @@ def main():
                            "row dots + SiLU*up)", "achieved": round(achieved, 1),
                            "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                            "frac": round(achieved / HBM_PEAK_GBPS, 4), "traffic": pmc_traffic(),
-                           "bytes_per_launch": dom_bytes, "avg_us": round(ops[dom], 3)}
+                           "bytes_per_launch": dom_bytes, "avg_us": round(ops[dom], 3),
+                           "in_layer_sequence": dict(in_sequence, frac=round(
+                               dom_bytes / (in_sequence["gateup_silu_us"] * 1e-6) / 1e9
+                               / HBM_PEAK_GBPS, 4))}
         log("operators (us): %s" % out["operators_us_at_pos4351"])
         log("read floors: %s" % floors)
         out["decode_attention"] = time_attention(lh, syn, args.seed)
