@@ -263,8 +263,8 @@ static int layer_unfused(const lh_layer_weights *w, float *x, float *keys, float
         launched(lh_launch_rope_append(ws->d_qraw, ws->d_kraw, ws->d_vraw, params, n, ws->d_q,
             keys, values, C, s), "rope/append") ||
         launched(lh_launch_attention(ws->d_q, keys, values, ws->d_params, (uint32_t)ws->length, n,
-            C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_arrive, ws->d_bflags, ++ws->epoch, ws->handoff_fault, ws->d_attn, s),
-            "attention") ||
+            C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_arrive, ws->d_bflags, ++ws->epoch,
+            ws->handoff_fault, ws->d_attn, s), "attention") ||
         launched(lh_launch_matvec(kind, 0, wo, w->scale[3], ws->d_attn, x, x, LH_HIDDEN,
             LH_QUERY, n, s), "o") ||
         launched(lh_launch_rmsnorm(w->post_norm, x, ws->d_xn, LH_HIDDEN, n, s), "post norm") ||
@@ -325,9 +325,9 @@ int lh_layer_operator(int op, const lh_layer_weights *w, float *d_x, float *d_ke
         return launched(lh_launch_qkv_rope(0, w->qkv, w->scale[0], w->scale[1], w->scale[2],
             w->input_norm, d_x, ws->d_params, n, ws->d_q, d_keys, d_values, C, s), "qkv");
     case LH_OP_ATTENTION:
-        return launched(lh_launch_attention(ws->d_q, d_keys, d_values, ws->d_params, (uint32_t)ws->length, n,
-            C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_arrive, ws->d_bflags, ++ws->epoch, ws->handoff_fault, ws->d_attn, s),
-            "attention");
+        return launched(lh_launch_attention(ws->d_q, d_keys, d_values, ws->d_params,
+            (uint32_t)ws->length, n, C, ws->d_PM, ws->d_PT, ws->d_PA, ws->d_arrive, ws->d_bflags,
+            ++ws->epoch, ws->handoff_fault, ws->d_attn, s), "attention");
     case LH_OP_O_RESIDUAL:
         return launched(lh_launch_matvec(0, 0, w->o, w->scale[3], ws->d_attn, d_x, d_x, LH_HIDDEN,
             LH_QUERY, n, s), "o");
@@ -381,8 +381,8 @@ int lh_attention(const float *d_q, const float *d_keys, const float *d_values, l
     }
     return launched(lh_launch_attention(d_q, d_keys, d_values, ws->d_params,
         (uint32_t)ws->length, (uint32_t)ws->count, (uint32_t)ws->capacity, ws->d_PM, ws->d_PT,
-        ws->d_PA, ws->d_arrive, ws->d_bflags, ++ws->epoch, ws->handoff_fault, d_out, (hipStream_t)stream),
-        "attention");
+        ws->d_PA, ws->d_arrive, ws->d_bflags, ++ws->epoch, ws->handoff_fault, d_out,
+        (hipStream_t)stream), "attention");
 }
 
 int lh_attention_mfma(const float *d_q, const float *d_keys, const float *d_values,
